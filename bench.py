@@ -1,0 +1,186 @@
+#!/usr/bin/env python3
+"""Benchmark: paged decode attention + append on one MI355X.
+
+One step = one layer's work for the whole batch of the chosen configuration
+(default c2, the Llama-3-8B-shaped B=32 ragged batch): page copies and chunk
+appends where the config has them, then the fused 1-token append + split-K
+paged decode attention.  Inputs are resident in HBM before timing starts.
+Steps cycle through --layers independent pools (4 by default, 4 GB for c2) so
+that no step finds the previous step's pages in the 256 MB last-level cache,
+as in a real multi-layer decode.
+
+Prints ONE JSON line.  `value` is achieved GB/s = algorithmic bytes per step
+(K+V of every attended token, append read+write, q/out, block-table entries,
+page copies) / wall time per step; `roofline` divides the same bytes by the
+HIP-event duration of the step's kernels, measured live on their stream;
+`cpu_baseline` times the oracle's reference-order CPU scan (append + online
+softmax per query head, OpenMP over sequence x kv head) on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "lns-ml_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged decode-attn+append µs/step and achieved HBM GB/s (% of peak), 8B-shape b=32"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    p.add_argument("--layers", type=int, default=4, help="pools cycled across steps (defeats the LLC)")
+    p.add_argument("--split", type=int, default=-1, help="split-K tokens (-1 = the config's choice)")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample budget (0 = skip)")
+    p.add_argument("--cpu-threads", type=int, default=0, help="0 = all cores the process may use")
+    return p.parse_args()
+
+
+def cpu_baseline(w, runner, seconds: float, threads: int):
+    """Oracle reference-order scan on a host copy of the step's pages, timed on
+    a bounded sample: whole steps until `seconds` of CPU work have run."""
+    import numpy as np
+
+    import oracle as O
+    from lnskv.configs import used_pages
+
+    pk = runner.layers[0]
+    pages = used_pages(w.tables)
+    idx = __import__("torch").from_numpy(pages.astype(np.int64)).to(pk.device)
+    conv = (lambda t: t.cpu().numpy().view(np.uint16)) if w.dtype == 1 else (lambda t: t.cpu().numpy())
+    ks = vs = None
+    if pk.ks is not None:
+        sidx = (idx[:, None] * 16 + __import__("torch").arange(16, device=pk.device)[None, :]).reshape(-1)
+        ks, vs = pk.ks.index_select(0, sidx).cpu().numpy(), pk.vs.index_select(0, sidx).cpu().numpy()
+    hp = O.HostPages(conv(pk.k.index_select(0, idx)), conv(pk.v.index_select(0, idx)), ks, vs, dtype=w.dtype)
+    remap = np.full(w.num_pages, O.NO_PAGE, np.uint32)
+    remap[pages] = np.arange(len(pages), dtype=np.uint32)
+    rows = runner.dec_rows
+    t = w.tables[rows]
+    tables = np.where(t != O.NO_PAGE, remap[np.minimum(t, w.num_pages - 1)], O.NO_PAGE).astype(np.uint32)
+    kv_len = w.kv_len[rows]
+    q = runner.q.cpu().numpy()
+    k_new, v_new = runner.k_new.cpu().numpy(), runner.v_new.cpu().numpy()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        O.append_decode_refscan(hp, q, k_new, v_new, tables, kv_len, None, w.scale, n_threads=threads)
+        n += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(dt * 1e6, 1), "unit": "µs/step", "cores": threads, "kind": "port",
+            "sample": f"{n} whole {w.name} steps (append + reference-order f32 scan of all "
+                      f"{len(rows)} decoding sequences), {threads} OpenMP threads, "
+                      f"{dt * n:.1f} s; nproc={os.cpu_count()}",
+            "gb_per_s": round(w.algorithmic_bytes()["total"] / dt / 1e9, 2)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}); the paged KV path shards by sequence "
+              f"or kv head with no exchange, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from lnskv.configs import make
+    from lnskv.step import StepRunner
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    w = make(args.config)
+    if args.split >= 0:
+        w.split = args.split
+    runner = StepRunner(w, dev, n_layers=args.layers, seed=1)
+    torch.cuda.synchronize()
+    nb = w.algorithmic_bytes()
+    stream = torch.cuda.current_stream(dev)
+
+    for i in range(args.warmup):
+        runner.run(i % args.layers)
+    torch.cuda.synchronize()
+
+    # timed region: exactly K steps, synchronized on both sides
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        runner.run(i % args.layers)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    ev = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))  # ms, on the kernels' stream
+    ev_mean = sum(ev) / len(ev) / 1e3
+    ev_med = ev[len(ev) // 2] / 1e3
+
+    gbs_wall = nb["total"] / wall / 1e9
+    gbs_ev = nb["total"] / ev_mean / 1e9
+    cpu = None
+    if args.cpu_seconds > 0:
+        threads = args.cpu_threads or len(os.sched_getaffinity(0))
+        threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
+        cpu = cpu_baseline(w, runner, args.cpu_seconds, threads)
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs_wall, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3, 5),
+        "us_per_step": round(wall * 1e6, 2),
+        "us_per_step_event_median": round(ev_med * 1e6, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1)*scale pages, seeded SplitMix64 lengths and page order)",
+        "config": {
+            "workload": {"c1": "c1 single sequence Hq32/Hkv4/d64 f32 ctx 512",
+                         "c2": "c2 Llama-3-8B layer Hq32/Hkv8/d128 f16 pages, B=32, ctx U[512,4096], "
+                               "1-token append + decode",
+                         "c3": "c3 Hq32/Hkv8/d128 f16, B=4 x 32768, split-K 512",
+                         "c4": "c4 16 x 256-token chunk appends + 48 decodes at U[1024,8192]",
+                         "c5": "c5 B=128 churn: 32 freed/reallocated, 8 CoW forks, 136 decodes"}[w.name],
+            "kv_dtype": {0: "f32", 1: "f16", 2: "q8a"}[w.dtype],
+            "n_seq": int(w.n_seq),
+            "tokens_attended": int(w.kv_len[w.decode].sum()),
+            "split_tokens": int(w.split),
+            "layers_cycled": args.layers,
+            "algorithmic_bytes_per_step": int(nb["total"]),
+            "bytes_breakdown": {k: int(v) for k, v in nb.items() if k != "total"},
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs_ev, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs_ev / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "append_decode step (decode_kernel + combine_kernel), HIP events per step",
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

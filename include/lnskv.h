@@ -1,0 +1,258 @@
+/*
+ * lnskv.h — C ABI of the MI355X (gfx950) paged KV-cache library.
+ *
+ * Replaces lns-ml's paged KV path:
+ *   - the paged attention call on MetalContext (encode_/dispatch_/
+ *     attention_paged_q8a[_enc], lns-metal/src/lib.rs:997-1094, 2085-2129)
+ *     and its kernel flash_attention_paged_q8a
+ *     (lns-metal/src/shaders/lns_decode.metal:498-646);
+ *   - the engine's page bookkeeping: PagePool (lns-inference/src/engine.rs:20-44),
+ *     ensure_kv_page / evict_kv_pages / upload_block_table / kv_p_start
+ *     (engine.rs:2958-3013) and clear_kv_cache (engine.rs:2911-2934).
+ *
+ * Conventions
+ *   - Every entry point returns 0 (LNSKV_OK) or a negative lnskv_status; the
+ *     message of the last failure on the calling thread is lnskv_last_error().
+ *     (The reference returns Result<(), String>; a binding maps status+message
+ *     to that.)
+ *   - Pointers named *_dev are device memory; everything else is host memory.
+ *   - Device work is enqueued on the caller's HIP stream (hipStream_t passed as
+ *     lnskv_stream_t; NULL = the null stream) and returns without waiting,
+ *     except the lnskv_dispatch_* variants, which wait (the reference's
+ *     dispatch_* commit-and-wait semantics, lib.rs:1091-1092).
+ *   - Page layout, per layer: separate K and V pools
+ *       pages[num_pages][16][n_kv_heads][head_dim]   (slot-major, engine.rs:731-734)
+ *     Q8A adds f32 scales[num_pages*16][n_kv_heads] for K and for V.
+ *     slot = block_table[pos/16]*16 + pos%16   (lns_decode.metal:541-545)
+ *   - Block tables are u32 rows, LNSKV_NO_PAGE (u32::MAX) = unallocated
+ *     (engine.rs:65).  Batched calls take [n_seq][bt_stride] row-major tables.
+ *   - Query head h reads kv head h / (n_heads / n_kv_heads)  (lns_decode.metal:536-537).
+ *   - Supported shapes: head_dim in {64, 128, 256}; n_heads a multiple of
+ *     n_kv_heads with n_heads/n_kv_heads in {1, 2, 4, 8}.
+ */
+#ifndef LNSKV_H
+#define LNSKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LNSKV_PAGE_SIZE 16           /* engine.rs:16 PAGE_SIZE, metal:516 PAGED_PAGE_SZ */
+#define LNSKV_NO_PAGE 0xFFFFFFFFu    /* engine.rs:65 u32::MAX */
+
+typedef void* lnskv_stream_t;        /* a hipStream_t */
+
+typedef enum {
+  LNSKV_DTYPE_F32 = 0,               /* plain copy on append */
+  LNSKV_DTYPE_F16 = 1,               /* (half)x, round to nearest even (metal:284-287) */
+  LNSKV_DTYPE_Q8A = 2                /* int8 + f32 absmax scale per (slot, head) (metal:547-593) */
+} lnskv_dtype;
+
+typedef enum {
+  LNSKV_OK = 0,
+  LNSKV_ERR_INVALID = -1,            /* bad argument or shape */
+  LNSKV_ERR_NOMEM = -2,              /* host or device allocation failed */
+  LNSKV_ERR_POOL_EXHAUSTED = -3,     /* engine.rs:2969-2971 "KV page pool exhausted ..." */
+  LNSKV_ERR_HIP = -4,                /* a HIP runtime call failed */
+  LNSKV_ERR_UNSUPPORTED = -5,        /* shape/dtype combination not built */
+  LNSKV_ERR_WORKSPACE = -6           /* caller workspace smaller than required */
+} lnskv_status;
+
+/* One layer's paged K/V pools (device memory, owned by the caller or by an
+ * lnskv_ctx).  Replaces the (k_cache, v_cache, k_scales, v_scales) buffer
+ * quadruple of encode_attention_paged_q8a (lib.rs:997-1010). */
+typedef struct lnskv_pages {
+  void* k_pages;                     /* device, [num_pages][16][n_kv_heads][head_dim] */
+  void* v_pages;                     /* device, same shape */
+  float* k_scales;                   /* device, Q8A only: [num_pages*16][n_kv_heads] */
+  float* v_scales;                   /* device, Q8A only */
+  uint32_t num_pages;
+  uint32_t n_kv_heads;
+  uint32_t head_dim;
+  int32_t dtype;                     /* lnskv_dtype */
+} lnskv_pages;
+
+const char* lnskv_last_error(void);
+const char* lnskv_version(void);
+/* bytes of one K (or V) page: 16 * n_kv_heads * head_dim * elem */
+size_t lnskv_page_bytes(const lnskv_pages* c);
+
+/* ---------------------------------------------------------------------------
+ * Device pools.  lnskv_pages_alloc fills c->k_pages/v_pages (and scales for
+ * Q8A) with zeroed device memory for the geometry already in *c; the caller
+ * frees them with lnskv_pages_free.  Replaces the per-layer Metal buffer
+ * allocation in InferenceEngine::new (engine.rs:717-773).
+ * ------------------------------------------------------------------------- */
+int lnskv_pages_alloc(lnskv_pages* c);
+int lnskv_pages_free(lnskv_pages* c);
+
+/* Zero every page and scale of the layer: clear_kv_cache's data part
+ * (engine.rs:2912-2922).  Async on stream. */
+int lnskv_clear(const lnskv_pages* c, lnskv_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Append: token t's K and V (k_new_dev/v_new_dev [n_tok][n_kv_heads][head_dim],
+ * f32) are converted to the page dtype and written to the slot of position
+ * tok_pos_dev[t] in sequence tok_seq_dev[t] (row tok_seq_dev[t] of
+ * block_tables_dev).  Tokens may straddle pages and any number of sequences.
+ * A token whose page entry is LNSKV_NO_PAGE or >= num_pages is not written.
+ * Replaces the write half of flash_attention_paged_q8a (metal:541-593),
+ * performed once per (token, kv head) instead of once per query head.
+ * ------------------------------------------------------------------------- */
+int lnskv_append(const lnskv_pages* c, const float* k_new_dev, const float* v_new_dev,
+                 const int32_t* tok_seq_dev, const int32_t* tok_pos_dev, int32_t n_tok,
+                 const uint32_t* block_tables_dev, int32_t bt_stride, lnskv_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Single-query paged decode attention over a batch of sequences.
+ *   q_dev [n_seq][n_heads][head_dim] f32 -> out_dev [n_seq][n_heads][head_dim] f32
+ *   sequence s attends tokens [p_start_dev[s], kv_len_dev[s]) (p_start_dev may
+ *   be NULL = 0; kv_len counts the newest token, so it is the reference's pos+1,
+ *   and p_start is kv_p_start, engine.rs:3008-3013).
+ *   out = softmax(scale * q.K^T) . V, by online softmax (metal:595-645).
+ *   max_kv_len: host upper bound of kv_len over the batch (sizes the grid).
+ *   split_tokens: tokens per split-K partition (multiple of 16), 0 = choose.
+ *   workspace_dev/ws_bytes: device scratch of at least
+ *   lnskv_decode_workspace_size(...) bytes, or NULL/0 to use a buffer the
+ *   library keeps per device (grown with hipMalloc on demand).
+ * Pages in the window whose table entry is LNSKV_NO_PAGE or >= num_pages are
+ * skipped (contribute nothing).  An empty window gives a zero output row.
+ * ------------------------------------------------------------------------- */
+int lnskv_decode_workspace_size(const lnskv_pages* c, int32_t n_seq, int32_t n_heads,
+                                int32_t max_kv_len, int32_t split_tokens, size_t* bytes);
+int lnskv_decode(const lnskv_pages* c, const float* q_dev, float* out_dev,
+                 const uint32_t* block_tables_dev, int32_t bt_stride,
+                 const int32_t* kv_len_dev, const int32_t* p_start_dev,
+                 int32_t n_seq, int32_t n_heads, int32_t max_kv_len, float scale,
+                 int32_t split_tokens, void* workspace_dev, size_t ws_bytes,
+                 lnskv_stream_t stream);
+
+/* Append + decode in one pass, the reference's per-layer step (engine.rs:
+ * 3401-3422 -> metal:518-646): the newest token of every sequence, at
+ * position kv_len_dev[s]-1, takes k_new_dev/v_new_dev[s] ([n_seq][n_kv][d]
+ * f32), is written to its page, and is attended to with the stored (converted)
+ * values.  Its page must already be allocated in the table (ensure_kv_page). */
+int lnskv_append_decode(const lnskv_pages* c, const float* q_dev, const float* k_new_dev,
+                        const float* v_new_dev, float* out_dev,
+                        const uint32_t* block_tables_dev, int32_t bt_stride,
+                        const int32_t* kv_len_dev, const int32_t* p_start_dev,
+                        int32_t n_seq, int32_t n_heads, int32_t max_kv_len, float scale,
+                        int32_t split_tokens, void* workspace_dev, size_t ws_bytes,
+                        lnskv_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * The reference call itself, one sequence: append the token at `pos` (k_in,
+ * v_in [n_kv_heads*head_dim] f32) into its page and attend over [p_start, pos]
+ * with scale 1/sqrt(head_dim) (metal:539).  Arguments follow
+ * MetalContext::encode_attention_paged_q8a (lib.rs:997-1013): q, k_in, v_in,
+ * the cache buffers (here the descriptor c, whose dtype may be Q8A as in the
+ * reference, or F16/F32), block_table, out, pos, head_dim, n_heads,
+ * n_kv_heads, p_start.  head_dim and n_kv_heads must match c.
+ * lnskv_dispatch_attention_paged additionally waits for completion
+ * (dispatch_attention_paged_q8a, lib.rs:1046-1094).
+ * ------------------------------------------------------------------------- */
+int lnskv_attention_paged(const float* q_dev, const float* k_in_dev, const float* v_in_dev,
+                          const lnskv_pages* c, const uint32_t* block_table_dev, float* out_dev,
+                          uint32_t pos, uint32_t head_dim, uint32_t n_heads, uint32_t n_kv_heads,
+                          uint32_t p_start, lnskv_stream_t stream);
+int lnskv_dispatch_attention_paged(const float* q_dev, const float* k_in_dev,
+                                   const float* v_in_dev, const lnskv_pages* c,
+                                   const uint32_t* block_table_dev, float* out_dev, uint32_t pos,
+                                   uint32_t head_dim, uint32_t n_heads, uint32_t n_kv_heads,
+                                   uint32_t p_start, lnskv_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Page copy (eviction churn, copy-on-write fork): page dst_dev[i] of K, V and
+ * (Q8A) both scale arrays becomes a copy of page src_dev[i].  The reference has
+ * no copy op; its free is PagePool::free_page (engine.rs:37-39).  Pairs whose
+ * ids are >= num_pages are skipped.  dst pages must be distinct from every src.
+ * ------------------------------------------------------------------------- */
+int lnskv_page_copy(const lnskv_pages* c, const uint32_t* src_dev, const uint32_t* dst_dev,
+                    int32_t n, lnskv_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Block-table gather: tokens [start, start+n_tok) of one sequence (its table
+ * row block_table_dev) copied into contiguous k_out_dev/v_out_dev
+ * [n_tok][n_kv_heads][head_dim] in the page dtype, plus (Q8A, may be NULL)
+ * ks_out_dev/vs_out_dev [n_tok][n_kv_heads].  The reference reads pages through
+ * the table inside its scan (metal:606-612); this is that address math as an
+ * export.  Tokens on missing pages come out as zeros.
+ * ------------------------------------------------------------------------- */
+int lnskv_gather(const lnskv_pages* c, const uint32_t* block_table_dev, int32_t start,
+                 int32_t n_tok, void* k_out_dev, void* v_out_dev, float* ks_out_dev,
+                 float* vs_out_dev, lnskv_stream_t stream);
+
+/* Wait for all work queued on stream (the commit + wait_until_completed of
+ * dispatch_*, lib.rs:1091-1092). */
+int lnskv_sync(lnskv_stream_t stream);
+
+/* ===========================================================================
+ * Host-side page bookkeeping (no device memory; usable without a GPU).
+ * ========================================================================= */
+
+/* PagePool, engine.rs:20-44: FIFO free list of physical page ids.
+ * create(cap) holds 0..cap in order; alloc = pop_front (LNSKV_ERR_POOL_EXHAUSTED
+ * when empty); free = push_back; reset refills 0..cap.  Adds a reference count
+ * per page for copy-on-write sharing (retain): free returns a page to the list
+ * only when its count drops to zero.  Without retain this is exactly the
+ * reference's behaviour. */
+typedef struct lnskv_page_pool lnskv_page_pool;
+int lnskv_page_pool_create(uint32_t capacity, lnskv_page_pool** out);
+void lnskv_page_pool_destroy(lnskv_page_pool* p);
+int lnskv_page_pool_alloc(lnskv_page_pool* p, uint32_t* page_out);
+int lnskv_page_pool_free(lnskv_page_pool* p, uint32_t page);
+int lnskv_page_pool_retain(lnskv_page_pool* p, uint32_t page);
+void lnskv_page_pool_reset(lnskv_page_pool* p);
+uint32_t lnskv_page_pool_num_free(const lnskv_page_pool* p);
+uint32_t lnskv_page_pool_capacity(const lnskv_page_pool* p);
+uint32_t lnskv_page_pool_refcount(const lnskv_page_pool* p, uint32_t page);
+
+/* Batched block tables: n_seq rows of max_pages u32 entries (LNSKV_NO_PAGE
+ * initialised) and a per-row logical length, the batched form of the engine's
+ * kv_block_tables (engine.rs:65) for one layer.  Row-major with stride
+ * max_pages, so lnskv_block_tables_host() can be uploaded as is. */
+typedef struct lnskv_block_tables lnskv_block_tables;
+int lnskv_block_tables_create(int32_t n_seq, int32_t max_pages, lnskv_block_tables** out);
+void lnskv_block_tables_destroy(lnskv_block_tables* t);
+const uint32_t* lnskv_block_tables_host(const lnskv_block_tables* t);
+int32_t lnskv_block_tables_stride(const lnskv_block_tables* t);
+int32_t lnskv_block_tables_len(const lnskv_block_tables* t, int32_t seq);
+/* clear_kv_cache's table part (engine.rs:2923-2930): every row emptied and
+ * filled with LNSKV_NO_PAGE (pages are not returned; reset the pool too). */
+void lnskv_block_tables_reset(lnskv_block_tables* t);
+
+/* ensure_kv_page (engine.rs:2960-2974): make sure logical page pos/16 of row
+ * seq has a physical page, allocating from pool.  On exhaustion returns
+ * LNSKV_ERR_POOL_EXHAUSTED with "KV page pool exhausted at layer {layer}
+ * (pos={pos})"; a position past the row's capacity returns LNSKV_ERR_INVALID
+ * (the reference's fixed 2 KB table would overflow, engine.rs:2999-3003). */
+int lnskv_ensure_kv_page(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t layer,
+                         int32_t seq, int32_t pos);
+/* evict_kv_pages (engine.rs:2976-2990): with window > 0, free every logical
+ * page of row seq that lies wholly before kv_p_start(pos, window). */
+int lnskv_evict_kv_pages(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t seq,
+                         int32_t pos, int32_t window);
+/* kv_p_start (engine.rs:3007-3013): pos - window + 1 clamped at 0, or 0. */
+int32_t lnskv_kv_p_start(int32_t pos, int32_t window);
+/* Free every page of row seq (sequence finished or evicted) and empty it. */
+int lnskv_free_sequence(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t seq);
+/* Copy-on-write fork: row child becomes a view of the first n_tok tokens of
+ * row parent.  Full pages are shared (refcount + 1); a partially filled tail
+ * page gets a fresh page, and the (src, dst) pair the device must copy is
+ * written to *copy_src / *copy_dst with *n_copy = 1 (else 0).  Row child must
+ * be empty. */
+int lnskv_fork_sequence(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t parent,
+                        int32_t child, int32_t n_tok, uint32_t* copy_src, uint32_t* copy_dst,
+                        int32_t* n_copy);
+/* upload_block_table (engine.rs:2992-3005): copy rows [0, n_seq) to the device
+ * table (same stride), async on stream. */
+int lnskv_block_tables_upload(const lnskv_block_tables* t, uint32_t* dst_dev,
+                              lnskv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LNSKV_H */

@@ -1,0 +1,308 @@
+// Host-side page bookkeeping of liblnskv: the PagePool free list, batched block
+// tables and the engine's page helpers, plus the error channel shared by every
+// entry point.  Nothing here touches the GPU except lnskv_block_tables_upload.
+//
+// Mirrors lns-inference/src/engine.rs:
+//   PagePool                      :20-44
+//   kv_block_tables (u32::MAX)    :65
+//   ensure_kv_page                :2960-2974
+//   evict_kv_pages                :2976-2990
+//   upload_block_table            :2992-3005
+//   kv_p_start                    :3007-3013
+//   clear_kv_cache (tables part)  :2923-2930
+#include <hip/hip_runtime_api.h>
+
+#include <cstdio>
+#include <cstring>
+#include <deque>
+#include <new>
+#include <vector>
+
+#include "lnskv_internal.h"
+
+namespace lnskv {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int check_geometry(const lnskv_pages* c) {
+  if (!c) return fail(LNSKV_ERR_INVALID, "page descriptor is NULL");
+  if (c->dtype != LNSKV_DTYPE_F32 && c->dtype != LNSKV_DTYPE_F16 && c->dtype != LNSKV_DTYPE_Q8A)
+    return fail(LNSKV_ERR_INVALID, "unknown dtype %d", c->dtype);
+  if (c->head_dim != 64 && c->head_dim != 128 && c->head_dim != 256)
+    return fail(LNSKV_ERR_UNSUPPORTED, "head_dim %u not supported (64, 128, 256)", c->head_dim);
+  if (c->n_kv_heads == 0 || c->n_kv_heads > 256)
+    return fail(LNSKV_ERR_INVALID, "n_kv_heads %u out of range [1, 256]", c->n_kv_heads);
+  if (c->num_pages == 0 || c->num_pages >= (1u << 27))
+    return fail(LNSKV_ERR_INVALID, "num_pages %u out of range [1, 2^27)", c->num_pages);
+  return LNSKV_OK;
+}
+
+int check_pages(const lnskv_pages* c) {
+  if (int rc = check_geometry(c)) return rc;
+  if (!c->k_pages || !c->v_pages) return fail(LNSKV_ERR_INVALID, "K/V page pools are NULL");
+  if (c->dtype == LNSKV_DTYPE_Q8A && (!c->k_scales || !c->v_scales))
+    return fail(LNSKV_ERR_INVALID, "Q8A pools need k_scales and v_scales");
+  return LNSKV_OK;
+}
+
+}  // namespace lnskv
+
+using lnskv::fail;
+
+// ---------------------------------------------------------------------------
+// PagePool (engine.rs:20-44).  The free list is a FIFO deque exactly as the
+// reference's VecDeque<u32>: new/reset hold 0..capacity in order, alloc pops
+// the front, free pushes the back.  The reference frees unconditionally; here
+// a page carries a reference count so that copy-on-write forks can share it,
+// and free returns it to the list when the count reaches zero.  With no
+// retain calls the observable order is identical to the reference.
+struct lnskv_page_pool {
+  uint32_t capacity;
+  std::deque<uint32_t> free_list;
+  std::vector<uint32_t> refs;
+};
+
+extern "C" {
+
+const char* lnskv_last_error(void) { return lnskv::g_last_error.c_str(); }
+const char* lnskv_version(void) { return "lnskv 0.1.0 (gfx950)"; }
+
+size_t lnskv_page_bytes(const lnskv_pages* c) {
+  if (!c) return 0;
+  return (size_t)LNSKV_PAGE_SIZE * c->n_kv_heads * c->head_dim * lnskv::dtype_bytes(c->dtype);
+}
+
+int lnskv_page_pool_create(uint32_t capacity, lnskv_page_pool** out) {
+  if (!out) return fail(LNSKV_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  auto* p = new (std::nothrow) lnskv_page_pool();
+  if (!p) return fail(LNSKV_ERR_NOMEM, "page pool allocation failed");
+  p->capacity = capacity;
+  try {
+    p->refs.assign(capacity, 0);
+  } catch (...) {
+    delete p;
+    return fail(LNSKV_ERR_NOMEM, "page pool of %u pages: allocation failed", capacity);
+  }
+  lnskv_page_pool_reset(p);
+  *out = p;
+  return LNSKV_OK;
+}
+
+void lnskv_page_pool_destroy(lnskv_page_pool* p) { delete p; }
+
+void lnskv_page_pool_reset(lnskv_page_pool* p) {
+  if (!p) return;
+  p->free_list.clear();
+  for (uint32_t i = 0; i < p->capacity; ++i) p->free_list.push_back(i);
+  std::fill(p->refs.begin(), p->refs.end(), 0u);
+}
+
+int lnskv_page_pool_alloc(lnskv_page_pool* p, uint32_t* page_out) {
+  if (!p || !page_out) return fail(LNSKV_ERR_INVALID, "pool or page_out is NULL");
+  if (p->free_list.empty()) return fail(LNSKV_ERR_POOL_EXHAUSTED, "KV page pool exhausted");
+  const uint32_t id = p->free_list.front();
+  p->free_list.pop_front();
+  p->refs[id] = 1;
+  *page_out = id;
+  return LNSKV_OK;
+}
+
+int lnskv_page_pool_free(lnskv_page_pool* p, uint32_t page) {
+  if (!p) return fail(LNSKV_ERR_INVALID, "pool is NULL");
+  if (page >= p->capacity) return fail(LNSKV_ERR_INVALID, "page %u outside pool of %u", page, p->capacity);
+  if (p->refs[page] == 0) return fail(LNSKV_ERR_INVALID, "page %u is not allocated", page);
+  if (--p->refs[page] == 0) p->free_list.push_back(page);
+  return LNSKV_OK;
+}
+
+int lnskv_page_pool_retain(lnskv_page_pool* p, uint32_t page) {
+  if (!p) return fail(LNSKV_ERR_INVALID, "pool is NULL");
+  if (page >= p->capacity) return fail(LNSKV_ERR_INVALID, "page %u outside pool of %u", page, p->capacity);
+  if (p->refs[page] == 0) return fail(LNSKV_ERR_INVALID, "page %u is not allocated", page);
+  ++p->refs[page];
+  return LNSKV_OK;
+}
+
+uint32_t lnskv_page_pool_num_free(const lnskv_page_pool* p) {
+  return p ? (uint32_t)p->free_list.size() : 0;
+}
+uint32_t lnskv_page_pool_capacity(const lnskv_page_pool* p) { return p ? p->capacity : 0; }
+uint32_t lnskv_page_pool_refcount(const lnskv_page_pool* p, uint32_t page) {
+  return (p && page < p->capacity) ? p->refs[page] : 0;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Batched block tables: the reference keeps one growable Vec<u32> per layer for
+// its single sequence (engine.rs:65) and copies it into a fixed 2 KB buffer
+// (engine.rs:735-736).  Here a layer holds n_seq fixed-capacity rows, so a
+// position past the row is an error instead of an overflow of the device copy.
+struct lnskv_block_tables {
+  int32_t n_seq;
+  int32_t max_pages;
+  std::vector<uint32_t> table;  // [n_seq][max_pages]
+  std::vector<int32_t> len;     // logical pages in use per row
+};
+
+namespace {
+bool row_ok(const lnskv_block_tables* t, int32_t seq) {
+  return t && seq >= 0 && seq < t->n_seq;
+}
+}  // namespace
+
+extern "C" {
+
+int lnskv_block_tables_create(int32_t n_seq, int32_t max_pages, lnskv_block_tables** out) {
+  if (!out) return fail(LNSKV_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  if (n_seq <= 0 || max_pages <= 0)
+    return fail(LNSKV_ERR_INVALID, "n_seq %d and max_pages %d must be positive", n_seq, max_pages);
+  auto* t = new (std::nothrow) lnskv_block_tables();
+  if (!t) return fail(LNSKV_ERR_NOMEM, "block table allocation failed");
+  t->n_seq = n_seq;
+  t->max_pages = max_pages;
+  try {
+    t->table.assign((size_t)n_seq * (size_t)max_pages, LNSKV_NO_PAGE);
+    t->len.assign((size_t)n_seq, 0);
+  } catch (...) {
+    delete t;
+    return fail(LNSKV_ERR_NOMEM, "block tables %d x %d: allocation failed", n_seq, max_pages);
+  }
+  *out = t;
+  return LNSKV_OK;
+}
+
+void lnskv_block_tables_destroy(lnskv_block_tables* t) { delete t; }
+
+const uint32_t* lnskv_block_tables_host(const lnskv_block_tables* t) {
+  return t ? t->table.data() : nullptr;
+}
+int32_t lnskv_block_tables_stride(const lnskv_block_tables* t) { return t ? t->max_pages : 0; }
+int32_t lnskv_block_tables_len(const lnskv_block_tables* t, int32_t seq) {
+  return row_ok(t, seq) ? t->len[(size_t)seq] : 0;
+}
+
+void lnskv_block_tables_reset(lnskv_block_tables* t) {
+  if (!t) return;
+  std::fill(t->table.begin(), t->table.end(), LNSKV_NO_PAGE);
+  std::fill(t->len.begin(), t->len.end(), 0);
+}
+
+int lnskv_ensure_kv_page(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t layer,
+                         int32_t seq, int32_t pos) {
+  if (!row_ok(t, seq) || !pool) return fail(LNSKV_ERR_INVALID, "bad table/pool or seq %d", seq);
+  if (pos < 0) return fail(LNSKV_ERR_INVALID, "negative position %d", pos);
+  const int32_t lp = pos / LNSKV_PAGE_SIZE;
+  uint32_t* row = t->table.data() + (size_t)seq * (size_t)t->max_pages;
+  int32_t& len = t->len[(size_t)seq];
+  if (lp < len && row[lp] != LNSKV_NO_PAGE) return LNSKV_OK;
+  if (lp >= t->max_pages)
+    return fail(LNSKV_ERR_INVALID, "position %d needs logical page %d; the table row holds %d",
+                pos, lp, t->max_pages);
+  while (len <= lp) row[len++] = LNSKV_NO_PAGE;
+  uint32_t phys;
+  if (lnskv_page_pool_alloc(pool, &phys) != LNSKV_OK)
+    return fail(LNSKV_ERR_POOL_EXHAUSTED, "KV page pool exhausted at layer %d (pos=%d)", layer, pos);
+  row[lp] = phys;
+  return LNSKV_OK;
+}
+
+int32_t lnskv_kv_p_start(int32_t pos, int32_t window) {
+  if (window > 0) return pos > window - 1 ? pos - (window - 1) : 0;
+  return 0;
+}
+
+int lnskv_evict_kv_pages(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t seq, int32_t pos,
+                         int32_t window) {
+  if (!row_ok(t, seq) || !pool) return fail(LNSKV_ERR_INVALID, "bad table/pool or seq %d", seq);
+  if (window <= 0) return LNSKV_OK;
+  const int32_t evict_before = lnskv_kv_p_start(pos, window) / LNSKV_PAGE_SIZE;
+  uint32_t* row = t->table.data() + (size_t)seq * (size_t)t->max_pages;
+  const int32_t n = std::min(evict_before, t->len[(size_t)seq]);
+  for (int32_t lp = 0; lp < n; ++lp) {
+    if (row[lp] != LNSKV_NO_PAGE) {
+      if (int rc = lnskv_page_pool_free(pool, row[lp])) return rc;
+      row[lp] = LNSKV_NO_PAGE;
+    }
+  }
+  return LNSKV_OK;
+}
+
+int lnskv_free_sequence(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t seq) {
+  if (!row_ok(t, seq) || !pool) return fail(LNSKV_ERR_INVALID, "bad table/pool or seq %d", seq);
+  uint32_t* row = t->table.data() + (size_t)seq * (size_t)t->max_pages;
+  for (int32_t lp = 0; lp < t->len[(size_t)seq]; ++lp) {
+    if (row[lp] != LNSKV_NO_PAGE) {
+      if (int rc = lnskv_page_pool_free(pool, row[lp])) return rc;
+      row[lp] = LNSKV_NO_PAGE;
+    }
+  }
+  t->len[(size_t)seq] = 0;
+  return LNSKV_OK;
+}
+
+int lnskv_fork_sequence(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t parent,
+                        int32_t child, int32_t n_tok, uint32_t* copy_src, uint32_t* copy_dst,
+                        int32_t* n_copy) {
+  if (!row_ok(t, parent) || !row_ok(t, child) || !pool || parent == child || !n_copy)
+    return fail(LNSKV_ERR_INVALID, "bad fork arguments (parent %d, child %d)", parent, child);
+  *n_copy = 0;
+  if (t->len[(size_t)child] != 0) return fail(LNSKV_ERR_INVALID, "fork target row %d is not empty", child);
+  const int32_t n_pages = (n_tok + LNSKV_PAGE_SIZE - 1) / LNSKV_PAGE_SIZE;
+  if (n_tok < 0 || n_pages > t->len[(size_t)parent])
+    return fail(LNSKV_ERR_INVALID, "fork of %d tokens exceeds parent row %d", n_tok, parent);
+  const uint32_t* prow = t->table.data() + (size_t)parent * (size_t)t->max_pages;
+  uint32_t* crow = t->table.data() + (size_t)child * (size_t)t->max_pages;
+  const bool partial_tail = (n_tok % LNSKV_PAGE_SIZE) != 0;
+  const int32_t n_shared = partial_tail ? n_pages - 1 : n_pages;
+  uint32_t fresh = LNSKV_NO_PAGE;
+  if (partial_tail) {
+    if (prow[n_pages - 1] == LNSKV_NO_PAGE)
+      return fail(LNSKV_ERR_INVALID, "parent row %d has no page at its tail", parent);
+    if (lnskv_page_pool_alloc(pool, &fresh) != LNSKV_OK)
+      return fail(LNSKV_ERR_POOL_EXHAUSTED, "KV page pool exhausted forking row %d", parent);
+    if (!copy_src || !copy_dst) {
+      lnskv_page_pool_free(pool, fresh);
+      return fail(LNSKV_ERR_INVALID, "copy_src/copy_dst are NULL");
+    }
+  }
+  for (int32_t lp = 0; lp < n_shared; ++lp) {
+    if (prow[lp] != LNSKV_NO_PAGE) lnskv_page_pool_retain(pool, prow[lp]);
+    crow[lp] = prow[lp];
+  }
+  if (partial_tail) {
+    crow[n_pages - 1] = fresh;
+    *copy_src = prow[n_pages - 1];
+    *copy_dst = fresh;
+    *n_copy = 1;
+  }
+  t->len[(size_t)child] = n_pages;
+  return LNSKV_OK;
+}
+
+int lnskv_block_tables_upload(const lnskv_block_tables* t, uint32_t* dst_dev, lnskv_stream_t stream) {
+  if (!t || !dst_dev) return fail(LNSKV_ERR_INVALID, "table or destination is NULL");
+  const size_t bytes = t->table.size() * sizeof(uint32_t);
+  hipError_t e = hipMemcpyAsync(dst_dev, t->table.data(), bytes, hipMemcpyHostToDevice,
+                                (hipStream_t)stream);
+  if (e != hipSuccess) return fail(LNSKV_ERR_HIP, "block table upload: %s", hipGetErrorString(e));
+  return LNSKV_OK;
+}
+
+}  // extern "C"

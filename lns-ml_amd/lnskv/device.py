@@ -1,0 +1,187 @@
+"""Device-side entry points of liblnskv over torch tensors.
+
+torch is used only for device memory and the current HIP stream; every
+operation runs the library's HIP kernels through the C ABI.  Shapes, dtypes,
+devices and contiguity are checked here before any launch, because the C ABI
+receives raw pointers and the kernels index from the stated geometry.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q8A, PAGE_SIZE, Pages, check, lib)
+
+TORCH_DTYPE = {DTYPE_F32: torch.float32, DTYPE_F16: torch.float16, DTYPE_Q8A: torch.int8}
+
+
+def _ptr(t: torch.Tensor | None) -> C.c_void_p:
+    return C.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _stream(device: torch.device) -> C.c_void_p:
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _need(t: torch.Tensor, name: str, dtype, numel: int, device) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.device != device:
+        raise ValueError(f"{name} must be on {device}, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.numel() != numel:
+        raise ValueError(f"{name} must have {numel} elements, got {t.numel()}")
+
+
+class PagedKV:
+    """One layer's paged K/V pools in the reference layout
+    [num_pages][16][n_kv_heads][head_dim] (+ Q8A scales [num_pages*16][n_kv]),
+    held as torch tensors, with the library's operations on them."""
+
+    def __init__(self, num_pages: int, n_kv_heads: int, head_dim: int, dtype: int,
+                 device: str | torch.device = "cuda"):
+        self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.num_pages, self.n_kv, self.head_dim, self.dtype = num_pages, n_kv_heads, head_dim, dtype
+        shape = (num_pages, PAGE_SIZE, n_kv_heads, head_dim)
+        td = TORCH_DTYPE[dtype]
+        self.k = torch.zeros(shape, dtype=td, device=self.device)
+        self.v = torch.zeros(shape, dtype=td, device=self.device)
+        if dtype == DTYPE_Q8A:
+            self.ks = torch.zeros((num_pages * PAGE_SIZE, n_kv_heads), dtype=torch.float32, device=self.device)
+            self.vs = torch.zeros_like(self.ks)
+        else:
+            self.ks = self.vs = None
+        self.desc = Pages(self.k.data_ptr(), self.v.data_ptr(),
+                          self.ks.data_ptr() if self.ks is not None else None,
+                          self.vs.data_ptr() if self.vs is not None else None,
+                          num_pages, n_kv_heads, head_dim, dtype)
+
+    # -- helpers -------------------------------------------------------------
+    @property
+    def row_elems(self) -> int:
+        return self.n_kv * self.head_dim
+
+    def _tables(self, tables: torch.Tensor, n_seq: int) -> int:
+        if tables.dim() != 2 or tables.shape[0] != n_seq:
+            raise ValueError(f"block tables must be [n_seq={n_seq}][stride], got {tuple(tables.shape)}")
+        _need(tables, "block_tables", torch.int32 if tables.dtype == torch.int32 else torch.uint32,
+              tables.numel(), self.device)
+        return int(tables.shape[1])
+
+    # -- operations ----------------------------------------------------------
+    def clear(self) -> None:
+        check(lib().lnskv_clear(C.byref(self.desc), _stream(self.device)))
+
+    def append(self, k_new, v_new, tok_seq, tok_pos, tables) -> None:
+        n_tok = int(tok_seq.numel())
+        _need(k_new, "k_new", torch.float32, n_tok * self.row_elems, self.device)
+        _need(v_new, "v_new", torch.float32, n_tok * self.row_elems, self.device)
+        _need(tok_seq, "tok_seq", torch.int32, n_tok, self.device)
+        _need(tok_pos, "tok_pos", torch.int32, n_tok, self.device)
+        if tables.dim() != 2:
+            raise ValueError("block tables must be 2-D")
+        _need(tables, "block_tables", tables.dtype, tables.numel(), self.device)
+        n_rows = int(tables.shape[0])
+        if n_tok and (int(tok_seq.min()) < 0 or int(tok_seq.max()) >= n_rows):
+            raise ValueError("tok_seq names a row outside the block tables")
+        check(lib().lnskv_append(C.byref(self.desc), _ptr(k_new), _ptr(v_new), _ptr(tok_seq),
+                                 _ptr(tok_pos), n_tok, _ptr(tables), int(tables.shape[1]),
+                                 _stream(self.device)))
+
+    def workspace_size(self, n_seq: int, n_heads: int, max_kv_len: int, split: int = 0) -> int:
+        out = C.c_size_t()
+        check(lib().lnskv_decode_workspace_size(C.byref(self.desc), n_seq, n_heads, max_kv_len, split,
+                                                C.byref(out)))
+        return out.value
+
+    def _decode_common(self, q, tables, kv_len, p_start, n_heads):
+        n_seq = int(kv_len.numel())
+        _need(q, "q", torch.float32, n_seq * n_heads * self.head_dim, self.device)
+        _need(kv_len, "kv_len", torch.int32, n_seq, self.device)
+        if p_start is not None:
+            _need(p_start, "p_start", torch.int32, n_seq, self.device)
+        stride = self._tables(tables, n_seq)
+        return n_seq, stride
+
+    def decode(self, q, tables, kv_len, *, n_heads: int, max_kv_len: int, scale: float,
+               p_start=None, split: int = 0, workspace=None, out=None) -> torch.Tensor:
+        n_seq, stride = self._decode_common(q, tables, kv_len, p_start, n_heads)
+        if out is None:
+            out = torch.empty((n_seq, n_heads, self.head_dim), dtype=torch.float32, device=self.device)
+        _need(out, "out", torch.float32, n_seq * n_heads * self.head_dim, self.device)
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(lib().lnskv_decode(C.byref(self.desc), _ptr(q), _ptr(out), _ptr(tables), stride,
+                                 _ptr(kv_len), _ptr(p_start), n_seq, n_heads, max_kv_len, scale, split,
+                                 _ptr(workspace), ws_bytes, _stream(self.device)))
+        return out
+
+    def append_decode(self, q, k_new, v_new, tables, kv_len, *, n_heads: int, max_kv_len: int,
+                      scale: float, p_start=None, split: int = 0, workspace=None,
+                      out=None) -> torch.Tensor:
+        n_seq, stride = self._decode_common(q, tables, kv_len, p_start, n_heads)
+        _need(k_new, "k_new", torch.float32, n_seq * self.row_elems, self.device)
+        _need(v_new, "v_new", torch.float32, n_seq * self.row_elems, self.device)
+        if out is None:
+            out = torch.empty((n_seq, n_heads, self.head_dim), dtype=torch.float32, device=self.device)
+        _need(out, "out", torch.float32, n_seq * n_heads * self.head_dim, self.device)
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(lib().lnskv_append_decode(C.byref(self.desc), _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(out),
+                                        _ptr(tables), stride, _ptr(kv_len), _ptr(p_start), n_seq, n_heads,
+                                        max_kv_len, scale, split, _ptr(workspace), ws_bytes,
+                                        _stream(self.device)))
+        return out
+
+    def attention_paged(self, q, k_in, v_in, block_table, pos: int, n_heads: int, p_start: int = 0,
+                        out=None, dispatch: bool = False) -> torch.Tensor:
+        """The reference's single-sequence call (encode_attention_paged_q8a,
+        lns-metal/src/lib.rs:997-1043): append token `pos`, attend [p_start, pos]."""
+        _need(q, "q", torch.float32, n_heads * self.head_dim, self.device)
+        _need(k_in, "k_in", torch.float32, self.row_elems, self.device)
+        _need(v_in, "v_in", torch.float32, self.row_elems, self.device)
+        if block_table.numel() < pos // PAGE_SIZE + 1:
+            raise ValueError("block table shorter than pos/16 + 1")
+        _need(block_table, "block_table", block_table.dtype, block_table.numel(), self.device)
+        if out is None:
+            out = torch.empty((n_heads, self.head_dim), dtype=torch.float32, device=self.device)
+        _need(out, "out", torch.float32, n_heads * self.head_dim, self.device)
+        fn = lib().lnskv_dispatch_attention_paged if dispatch else lib().lnskv_attention_paged
+        check(fn(_ptr(q), _ptr(k_in), _ptr(v_in), C.byref(self.desc), _ptr(block_table), _ptr(out), pos,
+                 self.head_dim, n_heads, self.n_kv, p_start, _stream(self.device)))
+        return out
+
+    def page_copy(self, src, dst) -> None:
+        n = int(src.numel())
+        _need(src, "src", src.dtype, n, self.device)
+        _need(dst, "dst", dst.dtype, n, self.device)
+        check(lib().lnskv_page_copy(C.byref(self.desc), _ptr(src), _ptr(dst), n, _stream(self.device)))
+
+    def gather(self, block_table_row, start: int, n_tok: int):
+        """Tokens [start, start+n_tok) of one sequence as contiguous
+        [n_tok][n_kv][d] tensors in page dtype (+ Q8A scales [n_tok][n_kv])."""
+        if block_table_row.numel() * PAGE_SIZE < start + n_tok:
+            raise ValueError("block table row shorter than the gathered range")
+        _need(block_table_row, "block_table_row", block_table_row.dtype, block_table_row.numel(), self.device)
+        td = TORCH_DTYPE[self.dtype]
+        ko = torch.empty((n_tok, self.n_kv, self.head_dim), dtype=td, device=self.device)
+        vo = torch.empty_like(ko)
+        kso = vso = None
+        if self.dtype == DTYPE_Q8A:
+            kso = torch.empty((n_tok, self.n_kv), dtype=torch.float32, device=self.device)
+            vso = torch.empty_like(kso)
+        check(lib().lnskv_gather(C.byref(self.desc), _ptr(block_table_row), start, n_tok, _ptr(ko), _ptr(vo),
+                                 _ptr(kso), _ptr(vso), _stream(self.device)))
+        return ko, vo, kso, vso
+
+
+def sync(device=None) -> None:
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    check(lib().lnskv_sync(_stream(dev)))
+
+
+__all__ = ["PagedKV", "sync", "DTYPE_F32", "DTYPE_F16", "DTYPE_Q8A", "TORCH_DTYPE"]

@@ -1,0 +1,91 @@
+"""One step of one layer on the device, in the reference's call order.
+
+lns-inference/src/engine.rs:3218-3237 allocates pages, evicts and uploads the
+block tables on the host, then (engine.rs:3401-3422) appends the new token and
+attends in one kernel.  A Workload carries the host side already done (pages
+allocated by ensure_kv_page, CoW forks planned); StepRunner uploads its tables
+once and then runs, per step:
+  1. page_copy of the planned copy-on-write tail pages (if any),
+  2. lnskv_append of multi-token chunks (if any),
+  3. lnskv_append_decode for the decoding sequences (append 1 token + attend).
+`n_layers` pools of identical geometry let a benchmark cycle through layers so
+consecutive steps do not find the previous step's pages in the 256 MB
+last-level cache.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from ._lib import DTYPE_Q8A
+from .configs import Workload
+from .device import PagedKV
+
+
+def _i32(a: np.ndarray, dev) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(a.astype(np.int32, copy=False)).to(dev)
+
+
+class StepRunner:
+    def __init__(self, w: Workload, device="cuda", n_layers: int = 1, seed: int = 0,
+                 fill: bool = True):
+        self.w = w
+        self.dev = torch.device(device)
+        if self.dev.type == "cuda" and self.dev.index is None:
+            self.dev = torch.device("cuda", torch.cuda.current_device())
+        self.layers = [PagedKV(w.num_pages, w.n_kv, w.head_dim, w.dtype, self.dev) for _ in range(n_layers)]
+        if fill:
+            for i, pk in enumerate(self.layers):
+                self.fill(pk, seed + 1000 * i)
+        g = torch.Generator(device=self.dev)
+        g.manual_seed(seed + 7)
+        d, nkv, hq = w.head_dim, w.n_kv, w.n_heads
+        self.tables = _i32(w.tables, self.dev)
+        # decoding sequences get their own compact table / length rows
+        self.dec_rows = w.decode_rows()
+        self.n_dec = len(self.dec_rows)
+        self.dec_tables = _i32(w.tables[self.dec_rows], self.dev)
+        self.dec_kv_len = _i32(w.kv_len[self.dec_rows], self.dev)
+        self.max_kv_len = int(w.kv_len[self.dec_rows].max()) if self.n_dec else 0
+        self.q = torch.randn((self.n_dec, hq, d), generator=g, device=self.dev)
+        self.k_new = torch.randn((self.n_dec, nkv, d), generator=g, device=self.dev) * w.value_scale
+        self.v_new = torch.randn((self.n_dec, nkv, d), generator=g, device=self.dev) * w.value_scale
+        self.out = torch.empty((self.n_dec, hq, d), device=self.dev)
+        cs, cp = w.chunk_tokens()
+        self.n_chunk_tok = len(cs)
+        self.chunk_seq = _i32(cs, self.dev)
+        self.chunk_pos = _i32(cp, self.dev)
+        self.chunk_k = torch.randn((len(cs), nkv, d), generator=g, device=self.dev) * w.value_scale
+        self.chunk_v = torch.randn((len(cs), nkv, d), generator=g, device=self.dev) * w.value_scale
+        self.copy_src = _i32(np.array([c[0] for c in w.copies], np.uint32), self.dev)
+        self.copy_dst = _i32(np.array([c[1] for c in w.copies], np.uint32), self.dev)
+        ws = self.layers[0].workspace_size(max(self.n_dec, 1), hq, self.max_kv_len, w.split)
+        self.workspace = torch.empty(max(ws, 4), dtype=torch.uint8, device=self.dev)
+
+    def fill(self, pk: PagedKV, seed: int) -> None:
+        g = torch.Generator(device=self.dev)
+        g.manual_seed(seed)
+        if pk.dtype == DTYPE_Q8A:
+            for t in (pk.k, pk.v):
+                t.copy_(torch.randint(-127, 128, t.shape, generator=g, device=self.dev, dtype=torch.int8))
+            for t in (pk.ks, pk.vs):
+                t.copy_(torch.rand(t.shape, generator=g, device=self.dev) * 0.02 + 0.001)
+            return
+        for t in (pk.k, pk.v):
+            t.copy_((torch.randn(t.shape, generator=g, device=self.dev) * self.w.value_scale).to(t.dtype))
+
+    def run(self, layer: int = 0) -> torch.Tensor:
+        pk = self.layers[layer]
+        w = self.w
+        if len(w.copies):
+            pk.page_copy(self.copy_src, self.copy_dst)
+        if self.n_chunk_tok:
+            pk.append(self.chunk_k, self.chunk_v, self.chunk_seq, self.chunk_pos, self.tables)
+        if self.n_dec:
+            pk.append_decode(self.q, self.k_new, self.v_new, self.dec_tables, self.dec_kv_len,
+                             n_heads=w.n_heads, max_kv_len=self.max_kv_len, scale=w.scale, split=w.split,
+                             workspace=self.workspace, out=self.out)
+        return self.out

@@ -1,0 +1,84 @@
+"""The C ABI without a GPU: the library loads, exports every symbol the header
+declares, and rejects bad arguments before touching the device."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from lnskv import _lib
+from lnskv._lib import Pages
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lnskv.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lnskv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_api():
+    syms = declared_symbols()
+    assert "lnskv_append_decode" in syms and "lnskv_page_pool_alloc" in syms
+    assert len(syms) >= 30
+
+
+def test_library_exports_every_declared_symbol():
+    lib = C.CDLL(_lib.LIB_PATH)
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_binding_covers_every_declared_symbol():
+    assert sorted(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_version_and_page_bytes():
+    lib = _lib.lib()
+    assert b"gfx950" in lib.lnskv_version()
+    p = Pages(None, None, None, None, 16384, 8, 128, _lib.DTYPE_F16)
+    assert lib.lnskv_page_bytes(C.byref(p)) == 16 * 8 * 128 * 2
+
+
+def _status(fn, *args):
+    return fn(*args), _lib.last_error()
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    lib = _lib.lib()
+    bad_dim = Pages(1, 1, None, None, 64, 4, 96, _lib.DTYPE_F16)
+    rc, msg = _status(lib.lnskv_decode, C.byref(bad_dim), 1, 1, 1, 4, 1, None, 1, 32, 16, 0.1, 0, None, 0, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "head_dim" in msg
+    good = Pages(1, 1, None, None, 64, 4, 64, _lib.DTYPE_F16)
+    rc, msg = _status(lib.lnskv_decode, C.byref(good), 1, 1, 1, 4, 1, None, 1, 30, 16, 0.1, 0, None, 0, None)
+    assert rc == _lib.ERR_INVALID and "multiple" in msg
+    rc, msg = _status(lib.lnskv_decode, C.byref(good), 1, 1, 1, 4, 1, None, 1, 32, 16, 0.1, 24, None, 0, None)
+    assert rc == _lib.ERR_INVALID and "split" in msg
+    rc, msg = _status(lib.lnskv_decode, C.byref(good), 1, 1, 1, 4, 1, None, 1, 32, 16, -1.0, 0, None, 0, None)
+    assert rc == _lib.ERR_INVALID and "scale" in msg
+    rc, _ = _status(lib.lnskv_decode, C.byref(good), None, 1, 1, 4, 1, None, 1, 32, 16, 0.1, 0, None, 0, None)
+    assert rc == _lib.ERR_INVALID
+    q8_no_scales = Pages(1, 1, None, None, 64, 4, 64, _lib.DTYPE_Q8A)
+    rc, msg = _status(lib.lnskv_append, C.byref(q8_no_scales), 1, 1, 1, 1, 1, 1, 4, None)
+    assert rc == _lib.ERR_INVALID and "scales" in msg
+    rc, msg = _status(lib.lnskv_attention_paged, 1, 1, 1, C.byref(good), 1, 1, 10, 128, 32, 4, 0, None)
+    assert rc == _lib.ERR_INVALID and "differ" in msg
+    rc, _ = _status(lib.lnskv_gather, C.byref(good), 1, 0, 4, 1, 1, 1, 1, None)
+    assert rc == _lib.ERR_INVALID  # scale outputs only for Q8A
+
+
+def test_workspace_size_formula():
+    lib = _lib.lib()
+    p = Pages(None, None, None, None, 16384, 8, 128, _lib.DTYPE_F16)
+    out = C.c_size_t()
+    assert lib.lnskv_decode_workspace_size(C.byref(p), 32, 32, 4097, 256, C.byref(out)) == 0
+    assert out.value == 32 * 32 * 17 * (128 + 2) * 4
+    assert lib.lnskv_decode_workspace_size(C.byref(p), 4, 32, 200, 256, C.byref(out)) == 0
+    assert out.value == 0  # one partition: no partials
+
+
+@pytest.mark.parametrize("name", ["lnskv_last_error", "lnskv_version"])
+def test_string_entry_points(name):
+    assert isinstance(getattr(_lib.lib(), name)(), bytes)

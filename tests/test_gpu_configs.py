@@ -1,0 +1,69 @@
+"""The five benchmark configurations at full size, one step each, vs the oracle.
+
+Per config: the step (page copies, chunk appends, fused append + decode) runs
+on the GPU; the oracle replays it on a host copy of every page the step can
+touch.  Pages must match bit for bit; attention outputs must be within the
+row-normwise tolerance (1e-3 f16, 1e-5 f32) of the f64 oracle over the exact
+stored values, and within the same tolerance of the reference-order f32 scan
+(the reference CPU path)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_util import TOL, host_pages, rel_err, remap_tables, say
+from lnskv import NO_PAGE
+from lnskv.configs import make, used_pages
+from lnskv.device import sync
+from lnskv.step import StepRunner
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
+def test_config_step(gpu, name):
+    say("config", name, "build")
+    w = make(name)
+    r = StepRunner(w, gpu, n_layers=1, seed=17)
+    pk = r.layers[0]
+    pages = used_pages(w.tables)
+    if w.copies:
+        pages = np.union1d(pages, np.array(w.copies, np.uint32).ravel())
+    hp, remap = host_pages(pk, pages)
+    tables = remap_tables(w.tables, remap)
+
+    # oracle replay of the step on the host copy
+    if w.copies:
+        src = remap[np.array([c[0] for c in w.copies], np.uint32)]
+        dst = remap[np.array([c[1] for c in w.copies], np.uint32)]
+        O.page_copy(hp, src, dst)
+    cs, cp = w.chunk_tokens()
+    if len(cs):
+        assert O.append(hp, r.chunk_k.cpu().numpy(), r.chunk_v.cpu().numpy(), cs, cp, tables) == 0
+    rows = r.dec_rows
+    dec_tables = tables[rows]
+    kv_len = w.kv_len[rows]
+    assert O.append(hp, r.k_new.cpu().numpy(), r.v_new.cpu().numpy(), np.arange(len(rows), dtype=np.int32),
+                    kv_len - 1, dec_tables) == 0
+
+    say("config", name, "step on gpu")
+    out = r.run(0)
+    sync()
+    got, _ = host_pages(pk, pages)
+    assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8)), "K pages differ"
+    assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8)), "V pages differ"
+
+    q = r.q.cpu().numpy()
+    o = out.cpu().numpy()
+    assert np.isfinite(o).all()
+    ref = O.decode_f64(hp, q, dec_tables, kv_len, None, w.scale)
+    err = rel_err(o, ref)
+    say("config", name, "max rel err vs f64", float(err.max()))
+    assert err.max() < TOL[w.dtype]
+    if name in ("c1", "c2"):
+        scan = O.decode_refscan(hp, q, dec_tables, kv_len, None, w.scale)
+        assert rel_err(o, scan.astype(np.float64)).max() < TOL[w.dtype]
+    # pages outside the step's footprint are untouched: a second step is
+    # idempotent (same token rewritten to the same slot, same output)
+    out2 = r.run(0).cpu().numpy()
+    assert np.array_equal(out2, o)
+

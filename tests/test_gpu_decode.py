@@ -1,0 +1,175 @@
+"""GPU paged decode attention vs the oracle.
+
+Outputs are compared with the f64 oracle over the exact stored page values,
+row-normwise: max_i |o_i - r_i| / max_i |r_i| per (sequence, query head), with
+the tolerance 1e-3 for f16 pages and 1e-5 for f32 and Q8A pages (TOL).  Pages
+written by the fused append are compared bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import TOL, dev_f32, dev_i32, fill_pages, host_pages, rel_err, say
+from lnskv import DTYPE_F16, DTYPE_F32, DTYPE_Q8A, DTYPE_NAMES, NO_PAGE
+from lnskv.device import PagedKV, sync
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(gpu, dtype, d, rep, n_kv, lens, seed, num_pages=None, scale_vals=1.0):
+    rng = np.random.default_rng(seed)
+    pages_per = [(L + 15) // 16 for L in lens]
+    num_pages = num_pages or sum(pages_per) + 8
+    pk = PagedKV(num_pages, n_kv, d, dtype, gpu)
+    fill_pages(pk, seed=seed, scale=scale_vals)
+    perm = rng.permutation(num_pages).astype(np.uint32)
+    stride = max(pages_per) + 1
+    tables = np.full((len(lens), stride), NO_PAGE, np.uint32)
+    k = 0
+    for s, n in enumerate(pages_per):
+        tables[s, :n] = perm[k:k + n]
+        k += n
+    q = rng.standard_normal((len(lens), n_kv * rep, d)).astype(np.float32)
+    return pk, tables, np.array(lens, np.int32), q
+
+
+LENS = (1, 15, 16, 17, 100, 513, 1000)
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_Q8A])
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("rep", [1, 2, 4, 8])
+def test_decode_matrix(gpu, dtype, d, rep):
+    say("decode", DTYPE_NAMES[dtype], "d", d, "rep", rep)
+    n_kv = 2
+    pk, tables, kv_len, q = _case(gpu, dtype, d, rep, n_kv, LENS, seed=d * 10 + rep)
+    hp, _ = host_pages(pk)
+    scale = 1.0 / np.sqrt(d)
+    ref = O.decode_f64(hp, q, tables, kv_len, None, scale)
+    for split in (0, 64):
+        out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                        max_kv_len=int(kv_len.max()), scale=float(scale), split=split)
+        sync()
+        err = rel_err(out, ref)
+        assert err.max() < TOL[dtype], (split, err.max())
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_Q8A])
+def test_windows_empty_and_missing_pages(gpu, dtype):
+    say("windows", DTYPE_NAMES[dtype])
+    d, rep, n_kv = 128, 4, 2
+    lens = (0, 1, 40, 300, 300, 700, 64)
+    pk, tables, kv_len, q = _case(gpu, dtype, d, rep, n_kv, lens, seed=3)
+    p_start = np.array([0, 1, 5, 33, 300, 650, 17], np.int32)  # empty, empty, ..., empty(300=L)
+    tables[5, 3] = NO_PAGE            # a missing page inside a window: skipped
+    tables[6, 2] = 1 << 30            # an entry past the pool: skipped
+    hp, _ = host_pages(pk)
+    scale = 0.09
+    ref = O.decode_f64(hp, q, tables, kv_len, p_start, scale)
+    for split in (0, 16, 48):
+        out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=8,
+                        max_kv_len=700, scale=scale, p_start=dev_i32(p_start, gpu), split=split)
+        sync()
+        o = out.cpu().numpy()
+        assert not np.isnan(o).any()
+        assert (o[0] == 0).all() and (o[1] == 0).all() and (o[4] == 0).all()
+        assert rel_err(o[2:4], ref[2:4]).max() < TOL[dtype]
+        assert rel_err(o[5:], ref[5:]).max() < TOL[dtype]
+
+
+def test_single_token_returns_stored_v_exactly(gpu):
+    for dtype in (DTYPE_F32, DTYPE_F16):
+        say("single token", DTYPE_NAMES[dtype])
+        pk, tables, kv_len, q = _case(gpu, dtype, 128, 4, 2, (1, 1, 1), seed=4)
+        out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=8,
+                        max_kv_len=1, scale=0.1)
+        sync()
+        hp, _ = host_pages(pk)
+        V = O.stored_values(hp, True).astype(np.float32)
+        o = out.cpu().numpy()
+        for s in range(3):
+            for h in range(8):
+                assert np.array_equal(o[s, h], V[tables[s, 0] * 16, h // 4])
+
+
+def test_split_invariance_and_page_permutation(gpu):
+    say("split invariance / permutation")
+    d, rep, n_kv = 128, 4, 8
+    lens = (3000, 1, 777, 4096, 16)
+    pk, tables, kv_len, q = _case(gpu, DTYPE_F16, d, rep, n_kv, lens, seed=5, scale_vals=0.5)
+    hp, _ = host_pages(pk)
+    ref = O.decode_f64(hp, q, tables, kv_len, None, 0.0883883)
+    outs = {}
+    for split in (16, 32, 256, 512, 1024, 4096):
+        outs[split] = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=32,
+                                max_kv_len=4096, scale=0.0883883, split=split).cpu().numpy()
+        assert rel_err(outs[split], ref).max() < TOL[DTYPE_F16]
+    # physically permuting pages together with the table: bit-identical output
+    perm = torch.randperm(pk.num_pages, generator=torch.Generator().manual_seed(9)).to(gpu)
+    inv = torch.argsort(perm).cpu().numpy().astype(np.uint32)
+    pk2 = PagedKV(pk.num_pages, n_kv, d, DTYPE_F16, gpu)
+    pk2.k.copy_(pk.k[perm])
+    pk2.v.copy_(pk.v[perm])
+    t2 = tables.copy()
+    m = t2 != NO_PAGE
+    t2[m] = inv[t2[m]]
+    o2 = pk2.decode(dev_f32(q, gpu), dev_i32(t2, gpu), dev_i32(kv_len, gpu), n_heads=32, max_kv_len=4096,
+                    scale=0.0883883, split=256).cpu().numpy()
+    assert np.array_equal(o2, outs[256])
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_Q8A])
+@pytest.mark.parametrize("d,rep", [(64, 8), (128, 4), (256, 2)])
+def test_fused_append_decode(gpu, dtype, d, rep):
+    """append_decode == append then decode: pages bit-exact, output in tolerance."""
+    say("append_decode", DTYPE_NAMES[dtype], "d", d, "rep", rep)
+    n_kv = 4
+    ctx = (0, 15, 16, 31, 200, 511, 1200)
+    lens = tuple(c + 1 for c in ctx)
+    pk, tables, kv_len, q = _case(gpu, dtype, d, rep, n_kv, lens, seed=d + rep + dtype)
+    rng = np.random.default_rng(11)
+    k_new = (rng.standard_normal((len(lens), n_kv, d)) * 2).astype(np.float32)
+    v_new = (rng.standard_normal((len(lens), n_kv, d)) * 2).astype(np.float32)
+    p_start = np.array([0, 3, 0, 31, 100, 0, 1100], np.int32)
+    hp, _ = host_pages(pk)
+    O.append(hp, k_new, v_new, np.arange(len(lens), dtype=np.int32), kv_len - 1, tables)
+    scale = 1.0 / np.sqrt(d)
+    ref = O.decode_f64(hp, q, tables, kv_len, p_start, scale)
+    for split in (0, 32):
+        out = pk.append_decode(dev_f32(q, gpu), dev_f32(k_new, gpu), dev_f32(v_new, gpu), dev_i32(tables, gpu),
+                               dev_i32(kv_len, gpu), n_heads=n_kv * rep, max_kv_len=int(kv_len.max()),
+                               scale=float(scale), p_start=dev_i32(p_start, gpu), split=split)
+        sync()
+        got, _ = host_pages(pk)
+        assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8))
+        assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8))
+        if dtype == DTYPE_Q8A:
+            assert np.array_equal(got.ks, hp.ks) and np.array_equal(got.vs, hp.vs)
+        assert rel_err(out, ref).max() < TOL[dtype], split
+
+
+def test_reference_single_sequence_call_c1_shape(gpu):
+    """lnskv_attention_paged: the reference's encode_attention_paged_q8a call
+    (append token `pos`, attend [p_start, pos], scale rsqrt(d)), here on the
+    C1 shape (Hq32/Hkv4/d64, f32, 512 context tokens) and on Q8A with a window."""
+    for dtype, p_start in ((DTYPE_F32, 0), (DTYPE_Q8A, 300), (DTYPE_F16, 7)):
+        say("attention_paged", DTYPE_NAMES[dtype], "p_start", p_start)
+        rng = np.random.default_rng(0)
+        pk = PagedKV(64, 4, 64, dtype, gpu)
+        fill_pages(pk, seed=0)
+        perm = rng.permutation(64).astype(np.uint32)
+        bt = np.full(512, NO_PAGE, np.uint32)   # the reference's MAX_LOGICAL_PAGES table
+        bt[:33] = perm[:33]
+        q = rng.standard_normal((32, 64)).astype(np.float32)
+        k_in = rng.standard_normal(4 * 64).astype(np.float32)
+        v_in = rng.standard_normal(4 * 64).astype(np.float32)
+        hp, _ = host_pages(pk)
+        O.append(hp, k_in[None], v_in[None], np.zeros(1, np.int32), np.array([512], np.int32), bt[None])
+        ref = O.decode_f64(hp, q[None], bt[None], np.array([513], np.int32), np.array([p_start], np.int32),
+                           1.0 / np.sqrt(64.0))[0]
+        out = pk.attention_paged(dev_f32(q, gpu), dev_f32(k_in, gpu), dev_f32(v_in, gpu), dev_i32(bt, gpu),
+                                 pos=512, n_heads=32, p_start=p_start, dispatch=True)
+        got, _ = host_pages(pk)
+        assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8))
+        assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8))
+        assert rel_err(out, ref).max() < TOL[dtype]
