@@ -42,7 +42,32 @@ def parse():
     p.add_argument("--split", type=int, default=-1, help="split-K tokens (-1 = the config's choice)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample budget (0 = skip)")
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = all cores the process may use")
+    p.add_argument("--copy-mb", type=int, default=1024,
+                   help="size of the device-to-device copy that measures the copy ceiling (0 = skip)")
+    p.add_argument("--copy-only", action="store_true",
+                   help="run only the plain copy (the calibration kernel for HBM byte counters)")
     return p.parse_args()
+
+
+def copy_ceiling(dev, mb: int, reps: int = 20) -> dict:
+    """Same-run HBM ceiling: a plain device-to-device copy of `mb` MiB (reads
+    and writes mb MiB each), timed with HIP events; bytes moved = 2 * size."""
+    import torch
+
+    n = mb * (1 << 20) // 4
+    a = torch.empty(n, dtype=torch.float32, device=dev).uniform_()
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e.record()
+    torch.cuda.synchronize()
+    dt = s.elapsed_time(e) / 1e3 / reps
+    return {"bytes_per_copy": 2 * n * 4, "gb_per_s": round(2 * n * 4 / dt / 1e9, 1)}
 
 
 def cpu_baseline(w, runner, seconds: float, threads: int):
@@ -102,6 +127,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_only:
+        print(json.dumps({"copy_ceiling": copy_ceiling(dev, args.copy_mb or 1024)}), flush=True)
+        return
     w = make(args.config)
     if args.split >= 0:
         w.split = args.split
@@ -131,6 +159,7 @@ def main():
 
     gbs_wall = nb["total"] / wall / 1e9
     gbs_ev = nb["total"] / ev_mean / 1e9
+    copy = copy_ceiling(dev, args.copy_mb) if args.copy_mb > 0 else None
     cpu = None
     if args.cpu_seconds > 0:
         threads = args.cpu_threads or len(os.sched_getaffinity(0))
@@ -176,6 +205,8 @@ def main():
             "frac": round(gbs_ev / HBM_PEAK_GBS, 4),
             "traffic": None,
             "kernel": "append_decode step (decode_kernel + combine_kernel), HIP events per step",
+            "copy_ceiling_gbs": copy["gb_per_s"] if copy else None,
+            "frac_of_copy_ceiling": round(gbs_ev / copy["gb_per_s"], 4) if copy else None,
         },
         "cpu_baseline": cpu,
     }

@@ -117,7 +117,10 @@ int lnskv_append(const lnskv_pages* c, const float* k_new_dev, const float* v_ne
  *   split_tokens: tokens per split-K partition (multiple of 16), 0 = choose.
  *   workspace_dev/ws_bytes: device scratch of at least
  *   lnskv_decode_workspace_size(...) bytes, or NULL/0 to use a buffer the
- *   library keeps per device (grown with hipMalloc on demand).
+ *   library keeps per device (grown with hipMalloc on demand; calls that use
+ *   it must not overlap in time).  The workspace holds the split-K partials
+ *   of one call; nothing carries over between calls.  Calls that overlap in
+ *   time need distinct workspaces.
  * Pages in the window whose table entry is LNSKV_NO_PAGE or >= num_pages are
  * skipped (contribute nothing).  An empty window gives a zero output row.
  * ------------------------------------------------------------------------- */

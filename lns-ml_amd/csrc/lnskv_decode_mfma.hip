@@ -1,0 +1,507 @@
+// Decode kernel for f16 pages with head_dim 128 (Llama-3 / Mixtral shapes):
+// both products of the online softmax on the matrix cores, one wave per
+// (kv head, split-K partition, sequence).
+//
+// A wave streams the pages of its partition with two pages in flight: K of a
+// page goes straight to registers in the MFMA A-operand layout, V goes to a
+// two-slot LDS ring by LDS DMA (global_load_lds_dwordx4), so prefetched V
+// costs no registers.  Page loads are issued before q is prepared, so the
+// first HBM round trip overlaps the wave's set-up.  A single-wave workgroup
+// needs no barrier and frees its slot the moment it finishes.
+//
+// Lane (g, n) = (lane/16, lane%16).  For one page (16 tokens x 128 dims of
+// one kv head):
+//  Q.K^T  S^T[16 tok][16 col] = K[16 tok][128] . Qc[128][16 col] as four
+//         v_mfma_f32_16x16x32_f16.  Columns 0..REP-1 hold the query heads'
+//         f16 "hi" parts, columns REP..2REP-1 the "lo" remainders
+//         (q = hi + lo to ~2^-22 relative), and a DPP row shift adds the two,
+//         so scores keep f32-level accuracy with f16 operands.  Lane (g, n)
+//         loads token n, dims 32j + 8g + 0..7 for MFMA j (instruction j reads
+//         bytes [64j, 64j+64) of all 16 token rows).  Result: lane (g, n)
+//         holds S^T[token 4g+ii][col n], ii = 0..3.
+//  softmax  page max: in-lane max of 4, then permlane32/16 swaps (VALU); the
+//         running max is raised only when a page exceeds it by more than 8
+//         (log2 units), so rescaling is rare and p <= 2^8 otherwise.
+//  P.V    O[16 row][128] = P[16 row][16 tok] . V[16 tok][128] as eight
+//         v_mfma_f32_16x16x16_f16.  The A operand wants lane (g, n) to hold
+//         P[row n][tokens 4g..4g+3] -- exactly the lane's four softmax
+//         weights: rows 0..REP-1 are f16(p), rows REP..2REP-1 the f16
+//         remainders p - f16(p) (from lane n-REP by DPP).  The B operand
+//         comes from the V slot via ds_read_b64_tr_b16: within a 16-lane
+//         group q, lane 4b+c receives element c of the 8-byte chunks that
+//         lanes b, b+4, b+8, b+12 point at; pointing lane 16q+r at token
+//         4q + r/4, dims d0 + 4*(r%4) gives lane 16q+4b+c the values
+//         V[4q..4q+3][d0+4b+c], the B layout.  Rows r and r+REP (hi and lo
+//         of one head) are summed at the end of the partition.
+//
+// V slot layout: LDS DMA instruction j writes lane l's 16 bytes at 16*l, so
+// lane (g, n) lands in LDS row R = 4j+g, 16-byte chunk n; it fetches token
+// 4g+j, chunk n ^ sw(R) with sw(R) = 2*(((R>>2)&3) | ((R&1)<<2)).  The XOR
+// keeps every 4-lane group on one 64-byte global segment and spreads the 16
+// rows that one transposed read touches over distinct LDS banks.
+//
+// Fused append: the wave whose partition holds the newest token converts it
+// (f16, round to nearest even), stores it to its page slot, and substitutes
+// it into its own registers / V slot when it reaches that page, so the scan
+// never reads the slot back.  Partitions are merged by combine_kernel.
+#include "lnskv_device.h"
+
+namespace lnskv {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) half8 lds_half8;
+
+constexpr int kD = 128;
+constexpr int kRowBytes = kD * 2;         // one (token, kv head) row of f16
+constexpr int kVSlot = kPage * kRowBytes;  // one page of V in LDS (swizzled rows)
+constexpr float kRescaleSlack = 8.0f;     // log2 units the running max may lag
+// Buffer resource word 3 for raw dword access on gfx9-family parts
+// (DATA_FORMAT = 32-bit; no swizzle, no index stride).
+constexpr int kBufferFormat = 0x00020000;
+
+// permlane32_swap(x, x) yields (x[l & ~32], x[l | 32]), permlane16_swap(x, x)
+// yields (x[l & ~16], x[l | 16]): a max or sum of the pair reduces across
+// halves / across adjacent 16-lane rows on the VALU.
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+  return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+  return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+}
+
+// out[h] = x of lane h of this lane's 16-lane row, h < N (DPP row_newbcast).
+template <int N, int H = 0>
+__device__ __forceinline__ void row_broadcast(float x, float (&out)[N]) {
+  if constexpr (H < N) {
+    out[H] = dpp_mov<kDppRowNewBcast + H>(x);
+    row_broadcast<N, H + 1>(x, out);
+  }
+}
+
+__device__ __forceinline__ uint32_t v_swz(int R) { return 2u * (uint32_t)(((R >> 2) & 3) | ((R & 1) << 2)); }
+
+// Waits until at most N vector-memory loads of this wave are outstanding
+// (gfx9 s_waitcnt: vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left open).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int REP>
+struct WaveState {
+  half8 qb[4];      // B operand of Q.K^T per 32-dim block, column lane%16
+  float4v acc[8];   // P.V result: lane (g, n) holds O[row 4g+ii][16*nb + n]
+  float m;          // lanes with lane%16 < REP: running max of head lane%16
+  float l;          // partial softmax sum over this lane's tokens
+  float qexp;       // 2^E undoing the per-head normalisation of q
+};
+
+// Multiplies the result rows 4g+ii of this lane by their head's alpha: row r
+// belongs to head r % REP, whose alpha sits in lane (r % REP) of every
+// 16-lane row (all rows agree).
+template <int REP>
+__device__ __forceinline__ void scale_rows(WaveState<REP>& st, float alpha, int g) {
+  float ab[REP];
+  row_broadcast<REP>(alpha, ab);
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    float f;
+    if constexpr (REP <= 4) {
+      f = ab[ii % REP];
+    } else {
+      f = (g & 1) ? ab[4 + ii] : ab[ii];
+    }
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) st.acc[nb][ii] *= f;
+  }
+}
+
+// Per-wave constants of the page streaming.
+struct Stream {
+  const uint8_t* k_pages;
+  const uint8_t* v_pages;
+  lds_u8* vring;       // 2 slots of kVSlot bytes
+  uint32_t koff;       // K: token n row + 16g
+  uint32_t voff[4];    // V DMA, instruction j: token 4g+j row + 16*(n ^ sw(4j+g))
+  uint32_t vr_off;     // transposed read: row 4*(n>>2)+g, (chunk ^ sw) folded per nb
+  uint32_t vr_swz;     // sw of that row
+  uint32_t vr_half;    // 8 * (n & 1)
+  uint32_t vr_sub;     // (n & 3) >> 1: chunk within the 2-chunk pair
+  uint32_t num_pages;
+  uint32_t kvh_off;    // kvh * kRowBytes
+  uint32_t page_bytes; // 16 * n_kv * kRowBytes
+};
+
+// Issues the loads of page `ph` (physical id, wave-uniform): K into
+// registers, V by DMA into slot `slot`.  Returns the page validity.  Exactly
+// 8 vector-memory instructions.
+__device__ __forceinline__ bool issue_page(const Stream& sm, uint32_t ph, int slot, half8 (&k)[4]) {
+  const bool valid = ph < sm.num_pages;
+  // a missing page reads page 0 (in bounds) and all its tokens are masked
+  const size_t base = (size_t)(valid ? ph : 0u) * sm.page_bytes + sm.kvh_off;
+  const uint8_t* kb = sm.k_pages + base;
+  const uint8_t* vb = sm.v_pages + base;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) k[j] = *reinterpret_cast<const half8*>(kb + sm.koff + 64 * j);
+  // V goes through a buffer-resource DMA (MUBUF `lds` form) whose base is this
+  // page's row block (wave-uniform).  The FLAT form (global_load_lds) would
+  // make the compiler drain all vector loads before any dependent use, since
+  // it counts it as a flat access to both global memory and LDS.
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, (int)sm.page_bytes, kBufferFormat);
+  lds_u8* dst = sm.vring + slot * kVSlot;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(dst + 1024 * j), 16,
+                                             (int)sm.voff[j], 0, 0, 0);
+  return valid;
+}
+
+template <int REP, bool FULL>
+__device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& sm, const half8 (&k)[4], int slot,
+                                             int tok0, bool valid, int ta, int tb, int g, int n) {
+  lds_u8* vslot = sm.vring + slot * kVSlot;
+  if constexpr (!FULL) {
+    // rows of masked tokens (and of a missing page) must not carry NaN bits
+    // into the matrix product: zero them in the slot
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = tok0 + 4 * g + j;
+      if (!(valid && t >= ta && t < tb))
+        *(lds_u32x4*)(vslot + (4 * j + g) * kRowBytes + 16 * n) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  float4v sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[j], st.qb[j], sacc, 0, 0, 0);
+  float s[4];
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) s[ii] = (sacc[ii] + dpp_mov<kDppRowShl + REP>(sacc[ii])) * st.qexp;
+  if constexpr (!FULL) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int t = tok0 + 4 * g + ii;
+      if (!(valid && t >= ta && t < tb)) s[ii] = -INFINITY;
+    }
+  }
+  float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  mx = max_xor16(max_xor32(mx));
+  const bool need = n < REP && mx > st.m + kRescaleSlack;
+  if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform
+    const float m_new = need ? mx : st.m;
+    const float alpha = fast_exp2(st.m - m_new);
+    st.m = m_new;
+    st.l *= alpha;
+    scale_rows<REP>(st, alpha, g);
+  }
+  float pr[4];
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) pr[ii] = fast_exp2(s[ii] - st.m);
+  st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+
+  // A operand of P.V: row n < REP: f16(p) of head n; REP <= n < 2REP: the
+  // remainder of head n-REP; other rows zero.
+  half4 pa;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    const float from = dpp_mov<kDppRowShr + REP>(pr[ii]);  // lane n-REP
+    const float lo = from - (float)(_Float16)from;
+    const float v = n < REP ? pr[ii] : (n < 2 * REP ? lo : 0.0f);
+    pa[ii] = (_Float16)v;
+  }
+  // The transposed reads are issued as inline asm: the compiler cannot tell
+  // which slot an LDS DMA writes and would otherwise wait for every DMA in
+  // flight (the next page's too) before reading.  This slot's DMA is already
+  // complete (the caller's vmcnt wait); the lgkmcnt wait below, tied to the
+  // results, completes the reads before any use and before the next DMA
+  // into this slot is issued.
+  const uint32_t vbase = (uint32_t)(size_t)(vslot + sm.vr_off + sm.vr_half);
+  short4v bv[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    const uint32_t chunk = ((uint32_t)(2 * nb) + sm.vr_sub) ^ sm.vr_swz;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[nb]) : "v"(vbase + 16u * chunk) : "memory");
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]), "+v"(bv[4]), "+v"(bv[5]), "+v"(bv[6]),
+                 "+v"(bv[7])
+               :
+               : "memory");
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+    st.acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]), st.acc[nb], 0, 0, 0);
+}
+
+template <int REP, bool FUSED>
+__global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
+  static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
+  __shared__ __attribute__((aligned(16))) uint8_t vring_[2 * kVSlot];
+  __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
+  lds_u8* vring = (lds_u8*)vring_;
+  lds_u8* newtok = (lds_u8*)newtok_;
+  const int kvh = blockIdx.x, part = blockIdx.y, s = blockIdx.z;
+  const SeqWindow w = seq_window<FUSED>(a, s);
+  if (part >= w.nparts) return;  // wave-uniform
+  const int jp = w.jf + part;
+  const int ta = max(w.p0, jp * a.split);
+  const int tb = min(w.L, (jp + 1) * a.split);
+  const int lane = threadIdx.x;
+  const int g = lane >> 4, n = lane & 15;
+
+  Stream sm;
+  sm.k_pages = a.k_pages;
+  sm.v_pages = a.v_pages;
+  sm.vring = vring;
+  sm.num_pages = a.num_pages;
+  sm.kvh_off = (uint32_t)kvh * kRowBytes;
+  const uint32_t rs = (uint32_t)a.n_kv * kRowBytes;  // bytes between token rows
+  sm.page_bytes = kPage * rs;
+  sm.koff = (uint32_t)n * rs + 16u * g;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sm.voff[j] = (uint32_t)(4 * g + j) * rs + 16u * ((uint32_t)n ^ v_swz(4 * j + g));
+  {
+    const int R = 4 * (n >> 2) + g;  // transposed read: token 4g + n/4 lives in row 4*(n/4) + g
+    sm.vr_off = (uint32_t)R * kRowBytes;
+    sm.vr_swz = v_swz(R);
+    sm.vr_half = 8u * (n & 1);
+    sm.vr_sub = (uint32_t)((n & 3) >> 1);
+  }
+
+  // The partition's block-table entries, lane i = page pg_first + i (one
+  // coalesced load per 64 pages), then read per page with v_readlane.
+  const uint32_t* bt_row = a.bt + (size_t)s * a.bt_stride;
+  const int pg_first = ta / kPage;
+  const int npg = ta < tb ? (tb - 1) / kPage - pg_first + 1 : 0;
+  uint32_t btv = lane < npg ? bt_row[pg_first + lane] : 0u;
+  auto phys_of = [&](int i) -> uint32_t {
+    if ((i & 63) == 0 && i > 0) {  // next 64 entries; drains the loads in flight (once per 64 pages)
+      btv = lane + i < npg ? bt_row[pg_first + i + lane] : 0u;
+      wait_vmcnt<0>();
+    }
+    return __builtin_amdgcn_readlane(btv, i & 63);
+  };
+
+  // Loads are issued oldest-first in the order they are needed: the table
+  // window, q, the new token, then the first two pages, so that waiting for
+  // an early load never drains the page loads behind it.
+  const bool qcol = n < 2 * REP;
+  float4v qv[8];
+  {
+    const int hq = qcol ? (n < REP ? n : n - REP) : 0;  // other columns load head 0 and drop it
+    const float4v* qh = reinterpret_cast<const float4v*>(a.q + ((size_t)s * a.n_heads + (size_t)kvh * REP + hq) * kD + 8 * g);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qv[2 * j] = qh[8 * j];
+      qv[2 * j + 1] = qh[8 * j + 1];
+    }
+  }
+  const int pos = w.L - 1;
+  const bool append = FUSED && part == w.nparts - 1 && w.L > 0;
+  // Every partition of a fused call loads the new token's row (the same
+  // 1 KiB per sequence and kv head, so the repeats hit L2): a load under a
+  // branch would make the compiler wait for it right there.
+  float2v knew = {0.0f, 0.0f}, vnew = {0.0f, 0.0f};
+  if constexpr (FUSED) {
+    const size_t src = ((size_t)s * a.n_kv + kvh) * kD + 2 * lane;
+    knew = *reinterpret_cast<const float2v*>(a.k_new + src);
+    vnew = *reinterpret_cast<const float2v*>(a.v_new + src);
+  }
+
+  // Keeps the loads above ahead of the page loads (the scheduler would sink
+  // them towards their uses, behind the pages).
+  asm volatile("" : "+v"(btv) : : "memory");
+
+  // The first two pages are issued unconditionally, for the same reason: a
+  // partition with fewer pages loads pool page 0 as a stand-in (in bounds,
+  // never consumed; drained before the epilogue).
+  half8 kA[4], kB[4];
+  bool vA = issue_page(sm, phys_of(0), 0, kA) && npg > 0;
+  bool vB = issue_page(sm, phys_of(1), 1, kB) && npg > 1;
+  // Uses of q and of the new token start here, with the pages in flight.
+  asm volatile(""
+               : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(qv[4]), "+v"(qv[5]), "+v"(qv[6]),
+                 "+v"(qv[7]), "+v"(knew), "+v"(vnew));
+
+  // Fused append: the partition holding position L-1 converts the new token,
+  // stores it to its page slot, and stages it in LDS for substitution.
+  if constexpr (FUSED) {
+    if (append) {
+      const uint32_t kb = to_f16_bits(knew.x) | (to_f16_bits(knew.y) << 16);
+      const uint32_t vb = to_f16_bits(vnew.x) | (to_f16_bits(vnew.y) << 16);
+      ((__attribute__((address_space(3))) uint32_t*)newtok)[lane] = kb;
+      ((__attribute__((address_space(3))) uint32_t*)(newtok + kRowBytes))[lane] = vb;
+      const int ip = pos / kPage - pg_first;  // the page is normally in the table window
+      const uint32_t ph = ip >= 0 && ip < 64 && ip < npg ? __builtin_amdgcn_readlane(btv, ip) : bt_row[pos / kPage];
+      if (ph < a.num_pages) {
+        const size_t row = ((size_t)ph * kPage + (size_t)(pos % kPage)) * a.n_kv + kvh;
+        *reinterpret_cast<uint32_t*>(a.k_pages_w + row * kRowBytes + 4 * lane) = kb;
+        *reinterpret_cast<uint32_t*>(a.v_pages_w + row * kRowBytes + 4 * lane) = vb;
+      }
+    }
+  }
+  const bool attend_new = append && pos >= ta;
+
+  // q -> B operand: column n < REP is hi of head n, REP <= n < 2REP lo of head
+  // n-REP, others zero.  Each head is first scaled by 2^-E (E from its max
+  // |q*scale|) so hi/lo stay in f16 range; the scores are scaled back by 2^E.
+  WaveState<REP> st;
+  {
+    float x[4][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float qe = qv[2 * j + (e >> 2)][e & 3];
+        x[j][e] = qcol ? qe * a.scale_log2 : 0.0f;
+        amax = fmaxf(amax, fabsf(x[j][e]));
+      }
+    amax = max_xor16(max_xor32(amax));
+    int E = 0;
+    if (amax > 0.0f && amax < INFINITY) (void)frexpf(amax, &E);
+    const float inv = ldexpf(1.0f, -E);
+    st.qexp = ldexpf(1.0f, E);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = x[j][e] * inv;
+        const _Float16 hi = (_Float16)y;
+        const _Float16 lo = (_Float16)(y - (float)hi);
+        st.qb[j][e] = n < REP ? hi : (qcol ? lo : (_Float16)0.0f);
+      }
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) st.acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    st.m = kMInit;
+    st.l = 0.0f;
+  }
+
+  // Page i: wait for its loads (the 8 of page i+1 may stay in flight), patch
+  // in the new token if it lives there, consume, refill the slot with i+2.
+  // `steady` asserts pages i+1 and i+2 exist, which lets the compiler's wait
+  // counting see exactly two pages in flight.
+  auto step = [&](int i, half8(&k)[4], bool& valid, int slot, bool steady) {
+    if (steady || i + 1 < npg) wait_vmcnt<8>(); else wait_vmcnt<0>();
+    const int tok0 = (pg_first + i) * kPage;
+    if (attend_new && pos / kPage == pg_first + i) {
+      const int t = pos % kPage;
+      if (n == t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) k[j] = *(lds_half8*)(newtok + 64 * j + 16 * g);
+      }
+      const int R = 4 * (t & 3) + (t >> 2);
+      if (g == (R & 3)) {
+        lds_u8* vslot = vring + slot * kVSlot;
+        *(lds_u32x4*)(vslot + R * kRowBytes + 16 * n) = *(lds_u32x4*)(newtok + kRowBytes + 16 * ((uint32_t)n ^ v_swz(R)));
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (valid && tok0 >= ta && tok0 + kPage <= tb)
+      consume_page<REP, true>(st, sm, k, slot, tok0, valid, ta, tb, g, n);
+    else
+      consume_page<REP, false>(st, sm, k, slot, tok0, valid, ta, tb, g, n);
+    if (steady || i + 2 < npg) valid = issue_page(sm, phys_of(i + 2), slot, k);
+  };
+  int i = 0;
+  for (; i + 3 < npg; i += 2) {
+    step(i, kA, vA, 0, true);
+    step(i + 1, kB, vB, 1, true);
+  }
+  // the last one to three pages
+  if (i < npg) step(i, kA, vA, 0, false);
+  if (i + 1 < npg) step(i + 1, kB, vB, 1, false);
+  if (i + 2 < npg) step(i + 2, kA, vA, 0, false);
+  wait_vmcnt<0>();  // stand-in pages of a partition with fewer than two pages
+
+  // Denominators: sum this head's lanes over the four 16-lane rows.
+  st.l = sum_xor16(sum_xor32(st.l));
+  // Numerators: result row r (hi) and r + REP (lo) belong to head r.  After
+  // the sums, lanes g == 0 hold heads 0..min(REP,4)-1 and, for REP == 8,
+  // lanes g == 1 hold heads 4..7, at dims 16*nb + n.
+  constexpr int NH = REP < 4 ? REP : 4;
+  float o[NH][8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    if constexpr (REP == 1) {
+      o[0][nb] = st.acc[nb][0] + st.acc[nb][1];
+    } else if constexpr (REP == 2) {
+      o[0][nb] = st.acc[nb][0] + st.acc[nb][2];
+      o[1][nb] = st.acc[nb][1] + st.acc[nb][3];
+    } else if constexpr (REP == 4) {  // hi rows in lanes g=0, lo rows in g=1
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) o[ii][nb] = sum_xor16(st.acc[nb][ii]);
+    } else {  // REP == 8: hi rows in g=0,1, lo rows in g=2,3
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) o[ii][nb] = sum_xor32(st.acc[nb][ii]);
+    }
+  }
+  // l of the heads this lane writes (REP == 8: lanes g == 1 hold heads 4..7)
+  float lb[REP];
+  row_broadcast<REP>(st.l, lb);
+  float mb[REP];
+  row_broadcast<REP>(st.m, mb);
+  const bool single = w.nparts == 1;
+  if (g == 0 || (REP == 8 && g == 1)) {
+    const int hb = REP == 8 ? 4 * g : 0;
+#pragma unroll
+    for (int ii = 0; ii < NH; ++ii) {
+      const float lh = (REP == 8 && g == 1) ? lb[(4 + ii) % REP] : lb[ii];
+      const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + hb + ii;
+      if (single) {
+        const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) a.out[hrow * kD + 16 * nb + n] = o[ii][nb] * inv;
+      } else {
+        const size_t pidx = hrow * a.max_parts + part;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) a.ws_acc[pidx * kD + 16 * nb + n] = o[ii][nb];
+        if (n == 0) {
+          const float mh = (REP == 8 && g == 1) ? mb[(4 + ii) % REP] : mb[ii];
+          a.ws_ml[pidx * 2 + 0] = mh;
+          a.ws_ml[pidx * 2 + 1] = lh;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+template <bool FUSED>
+int launch_decode_mfma_f16_d128(const DecodeArgs& a, int rep, int n_seq, hipStream_t st) {
+  const dim3 grid((unsigned)a.n_kv, (unsigned)a.max_parts, (unsigned)n_seq);
+  switch (rep) {
+    case 1: decode_mfma_kernel<1, FUSED><<<grid, kWave, 0, st>>>(a); launch_combine<1, kD, FUSED>(a, n_seq, st); break;
+    case 2: decode_mfma_kernel<2, FUSED><<<grid, kWave, 0, st>>>(a); launch_combine<2, kD, FUSED>(a, n_seq, st); break;
+    case 4: decode_mfma_kernel<4, FUSED><<<grid, kWave, 0, st>>>(a); launch_combine<4, kD, FUSED>(a, n_seq, st); break;
+    case 8: decode_mfma_kernel<8, FUSED><<<grid, kWave, 0, st>>>(a); launch_combine<8, kD, FUSED>(a, n_seq, st); break;
+    default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
+  }
+  return hip_check("decode kernel launch");
+}
+
+template int launch_decode_mfma_f16_d128<false>(const DecodeArgs&, int, int, hipStream_t);
+template int launch_decode_mfma_f16_d128<true>(const DecodeArgs&, int, int, hipStream_t);
+
+}  // namespace lnskv

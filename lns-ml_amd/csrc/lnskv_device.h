@@ -1,0 +1,269 @@
+// Device-side pieces shared by the decode kernels of liblnskv (gfx950).
+//
+// Reference semantics (lns-metal/src/shaders/lns_decode.metal):
+//   slot math                :541-545   slot = block_table[pos/16]*16 + pos%16
+//   Q8A append (K, V)        :547-593   absmax scale, round-half-away, clamp 127
+//   f16 append               :284-287   (half)x, round to nearest even
+//   online softmax scan      :595-645   m=-1e38, alpha/beta recurrence, acc/l
+//   GQA head mapping         :536-537   kv_h = hid / (n_heads / n_kv_heads)
+// The reference scans one query head per threadgroup, token by token, with two
+// barriers per token; here one workgroup owns (sequence, kv head, split-K
+// partition), holds all query heads of the group, and streams whole pages.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "lnskv_internal.h"
+
+namespace lnskv {
+
+constexpr int kPage = LNSKV_PAGE_SIZE;
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr float kLog2e = 1.4426950408889634f;
+// Running-max start value, finite like the reference's -1e38 (metal:600) so
+// that an all-masked page leaves alpha = exp2(0) = 1 instead of NaN.
+constexpr float kMInit = -1e30f;
+
+// ---------------------------------------------------------------------------
+// Storage traits: bytes per element.
+template <int DT> struct Storage;
+template <> struct Storage<LNSKV_DTYPE_F32> { static constexpr int kBytes = 4; };
+template <> struct Storage<LNSKV_DTYPE_F16> { static constexpr int kBytes = 2; };
+template <> struct Storage<LNSKV_DTYPE_Q8A> { static constexpr int kBytes = 1; };
+
+// ---------------------------------------------------------------------------
+// Cross-lane helpers.  DPP moves stay inside 16-lane rows; quad_perm and the
+// two mirrors make a butterfly whose every lane ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+constexpr int kDppRowShl = 0x100;     // + n: lane i reads lane i+n of its row
+constexpr int kDppRowShr = 0x110;     // + n: lane i reads lane i-n of its row
+constexpr int kDppRowNewBcast = 0x150;  // + n: every lane reads lane n of its row
+
+// Sum over aligned groups of N lanes (N = 1..64, power of two).
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp_mov<kDppXor1>(x);
+  if constexpr (N >= 4) x += dpp_mov<kDppXor2>(x);
+  if constexpr (N >= 8) x += dpp_mov<kDppHalfMirror>(x);
+  if constexpr (N >= 16) x += dpp_mov<kDppMirror>(x);
+  if constexpr (N >= 32) x += __shfl_xor(x, 16);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32);
+  return x;
+}
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+  if constexpr (N >= 2) x = fmaxf(x, dpp_mov<kDppXor1>(x));
+  if constexpr (N >= 4) x = fmaxf(x, dpp_mov<kDppXor2>(x));
+  if constexpr (N >= 8) x = fmaxf(x, dpp_mov<kDppHalfMirror>(x));
+  if constexpr (N >= 16) x = fmaxf(x, dpp_mov<kDppMirror>(x));
+  if constexpr (N >= 32) x = fmaxf(x, __shfl_xor(x, 16));
+  if constexpr (N >= 64) x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+// Sum / max across lanes that are STRIDE apart (STRIDE power of two): combines
+// the rows of a wave that share a column.
+template <int STRIDE>
+__device__ __forceinline__ float cross_sum(float x) {
+#pragma unroll
+  for (int o = STRIDE; o < kWave; o <<= 1) x += __shfl_xor(x, o);
+  return x;
+}
+template <int STRIDE>
+__device__ __forceinline__ float cross_max(float x) {
+#pragma unroll
+  for (int o = STRIDE; o < kWave; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Converts one f32 to the page dtype's bits; Q8A needs the head's scale.
+// f16: v_cvt_f16_f32 under the default round-to-nearest-even mode.
+// Q8A: IEEE division (HIP's correctly rounded f32 divide), roundf = half away
+// from zero, clamp to [-127, 127] (metal:562-567).
+__device__ __forceinline__ uint32_t to_f16_bits(float x) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+__device__ __forceinline__ int32_t to_q8(float x, float sc) {
+  float r = roundf(x / sc);
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return (int32_t)r;
+}
+
+// ---------------------------------------------------------------------------
+struct DecodeArgs {
+  const uint8_t* k_pages;
+  const uint8_t* v_pages;
+  const float* k_scales;
+  const float* v_scales;
+  uint8_t* k_pages_w;  // fused append writes (same pools)
+  uint8_t* v_pages_w;
+  float* k_scales_w;
+  float* v_scales_w;
+  const float* q;
+  float* out;
+  const float* k_new;
+  const float* v_new;
+  const uint32_t* bt;
+  const int32_t* kv_len;
+  const int32_t* p_start;
+  float* ws_acc;        // [n_seq][n_heads][max_parts][D] partial numerators
+  float* ws_ml;         // [n_seq][n_heads][max_parts][2] partial (max, sum)
+  int32_t kv_len_scalar;   // used when kv_len == nullptr
+  int32_t p_start_scalar;  // used when p_start == nullptr
+  int32_t bt_stride;
+  int32_t n_kv;
+  int32_t n_heads;
+  int32_t split;
+  int32_t max_parts;
+  int32_t max_kv_len;
+  uint32_t num_pages;
+  float scale_log2;  // softmax scale * log2(e): scores live in the exp2 domain
+};
+
+struct SeqWindow {
+  int L;       // kv_len clamped to what the grid and the table can address
+  int p0;      // window start
+  int jf;      // first partition index
+  int nparts;  // partitions of this sequence
+};
+
+template <bool FUSED>
+__device__ __forceinline__ SeqWindow seq_window(const DecodeArgs& a, int s) {
+  SeqWindow w;
+  int L = a.kv_len ? a.kv_len[s] : a.kv_len_scalar;
+  L = min(max(L, 0), min(a.max_kv_len, a.bt_stride * kPage));
+  int p0 = a.p_start ? a.p_start[s] : a.p_start_scalar;
+  p0 = min(max(p0, 0), L);
+  int lo = p0;
+  if (FUSED && L > 0) lo = min(lo, L - 1);
+  if (L <= lo) {
+    w.jf = 0;
+    w.nparts = 1;
+  } else {
+    w.jf = lo / a.split;
+    w.nparts = (L - 1) / a.split - w.jf + 1;
+  }
+  w.L = L;
+  w.p0 = p0;
+  return w;
+}
+
+// ---------------------------------------------------------------------------
+// Block epilogue shared by the decode kernels.  On entry the LDS arrays hold,
+// per wave, the running max m (log2 domain), the sum l and the numerator acc
+// of every query head of the group, and a __syncthreads() has passed.
+//  - one partition: out = sum_w 2^(m_w-M) acc_w / sum_w 2^(m_w-M) l_w
+//  - several: the block's (M, L, A) goes to the workspace and combine_kernel
+//    (launched next on the same stream) merges the partitions of each
+//    (sequence, kv head) with the same log-sum-exp weights.
+// (Merging in the last-finishing block instead needs an agent-scope release
+// per block, i.e. an L2 writeback on every XCD, which measured slower than a
+// second launch.)
+template <int REP, int D>
+struct EpilogueLds {
+  float acc[kWavesPerBlock][REP][D];
+  float m[kWavesPerBlock][REP];
+  float l[kWavesPerBlock][REP];
+};
+
+template <int REP, int D>
+__device__ __forceinline__ void finish_block(const DecodeArgs& a, EpilogueLds<REP, D>& sm, const SeqWindow& w,
+                                             int s, int kvh, int part) {
+  const int h0 = kvh * REP;
+  const bool single = w.nparts == 1;
+  for (int idx = threadIdx.x; idx < REP * D; idx += kBlock) {
+    const int h = idx / D, i = idx % D;
+    float M = sm.m[0][h];
+#pragma unroll
+    for (int q = 1; q < kWavesPerBlock; ++q) M = fmaxf(M, sm.m[q][h]);
+    float A = 0.0f, Ls = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kWavesPerBlock; ++q) {
+      const float wq = fast_exp2(sm.m[q][h] - M);
+      A = fmaf(wq, sm.acc[q][h][i], A);
+      Ls = fmaf(wq, sm.l[q][h], Ls);
+    }
+    const size_t hrow = (size_t)s * a.n_heads + h0 + h;
+    if (single) {
+      a.out[hrow * D + i] = Ls > 0.0f ? A / Ls : 0.0f;
+    } else {
+      const size_t pidx = hrow * a.max_parts + part;
+      a.ws_acc[pidx * D + i] = A;
+      if (i == 0) {
+        a.ws_ml[pidx * 2 + 0] = M;
+        a.ws_ml[pidx * 2 + 1] = Ls;
+      }
+    }
+  }
+}
+
+// Split-K combine: block (kv head, sequence) merges the partitions of its
+// REP query heads, threads over (head, dim).  One pass with a running max;
+// partials are read CHUNK partitions at a time so their loads overlap.
+template <int REP, int D, bool FUSED>
+__global__ __launch_bounds__(kBlock) void combine_kernel(DecodeArgs a) {
+  constexpr int CHUNK = 8;
+  const int kvh = blockIdx.x, s = blockIdx.y;
+  const SeqWindow w = seq_window<FUSED>(a, s);
+  if (w.nparts <= 1) return;
+  const int np = min(w.nparts, a.max_parts);
+  for (int idx = threadIdx.x; idx < REP * D; idx += kBlock) {
+    const int h = idx / D, i = idx % D;
+    const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + h;
+    const float2* ml = reinterpret_cast<const float2*>(a.ws_ml + hrow * a.max_parts * 2);
+    const float* acc = a.ws_acc + hrow * a.max_parts * D + i;
+    float M = kMInit, A = 0.0f, Ls = 0.0f;
+    for (int j0 = 0; j0 < np; j0 += CHUNK) {
+      float2 pm[CHUNK];
+      float pa[CHUNK];
+#pragma unroll
+      for (int u = 0; u < CHUNK; ++u) {
+        const bool in = j0 + u < np;
+        pm[u] = in ? ml[j0 + u] : make_float2(kMInit, 0.0f);
+        pa[u] = in ? acc[(size_t)(j0 + u) * D] : 0.0f;
+      }
+      float Mc = M;
+#pragma unroll
+      for (int u = 0; u < CHUNK; ++u) Mc = fmaxf(Mc, pm[u].x);
+      const float r = fast_exp2(M - Mc);
+      A *= r;
+      Ls *= r;
+#pragma unroll
+      for (int u = 0; u < CHUNK; ++u) {
+        const float wj = fast_exp2(pm[u].x - Mc);
+        A = fmaf(wj, pa[u], A);
+        Ls = fmaf(wj, pm[u].y, Ls);
+      }
+      M = Mc;
+    }
+    a.out[hrow * D + i] = Ls > 0.0f ? A / Ls : 0.0f;
+  }
+}
+
+template <int REP, int D, bool FUSED>
+inline void launch_combine(const DecodeArgs& a, int n_seq, hipStream_t st) {
+  if (a.max_parts > 1) combine_kernel<REP, D, FUSED><<<dim3((unsigned)a.n_kv, (unsigned)n_seq), kBlock, 0, st>>>(a);
+}
+
+// Launchers (defined in the decode translation units).
+template <int DT, bool FUSED>
+int launch_decode_valu(const DecodeArgs& a, int d, int rep, int n_seq, hipStream_t st);
+template <bool FUSED>
+int launch_decode_mfma_f16_d128(const DecodeArgs& a, int rep, int n_seq, hipStream_t st);
+
+int hip_check(const char* what);
+
+}  // namespace lnskv

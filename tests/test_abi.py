@@ -74,7 +74,7 @@ def test_workspace_size_formula():
     p = Pages(None, None, None, None, 16384, 8, 128, _lib.DTYPE_F16)
     out = C.c_size_t()
     assert lib.lnskv_decode_workspace_size(C.byref(p), 32, 32, 4097, 256, C.byref(out)) == 0
-    assert out.value == 32 * 32 * 17 * (128 + 2) * 4
+    assert out.value == 32 * 32 * 17 * (128 + 2) * 4  # partial numerators + (max, sum)
     assert lib.lnskv_decode_workspace_size(C.byref(p), 4, 32, 200, 256, C.byref(out)) == 0
     assert out.value == 0  # one partition: no partials
 

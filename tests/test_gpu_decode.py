@@ -148,6 +148,53 @@ def test_fused_append_decode(gpu, dtype, d, rep):
         assert rel_err(out, ref).max() < TOL[dtype], split
 
 
+@pytest.mark.parametrize("force_valu", ["0", "1"])
+def test_f16_d128_both_kernels(gpu, monkeypatch, force_valu):
+    """f16 / head_dim 128 runs the MFMA kernel; LNSKV_FORCE_VALU=1 the generic
+    one.  Both against the f64 oracle, fused and unfused, rep 1/2/4/8."""
+    monkeypatch.setenv("LNSKV_FORCE_VALU", force_valu)
+    for rep in (1, 2, 4, 8):
+        say("f16 d128 force_valu", force_valu, "rep", rep)
+        n_kv = 2
+        lens = (1, 2, 16, 17, 33, 255, 256, 257, 700, 2049)
+        pk, tables, kv_len, q = _case(gpu, DTYPE_F16, 128, rep, n_kv, lens, seed=40 + rep)
+        rng = np.random.default_rng(rep)
+        k_new = rng.standard_normal((len(lens), n_kv, 128)).astype(np.float32)
+        v_new = rng.standard_normal((len(lens), n_kv, 128)).astype(np.float32)
+        hp, _ = host_pages(pk)
+        ref0 = O.decode_f64(hp, q, tables, kv_len, None, 0.0883883)
+        out0 = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                         max_kv_len=2049, scale=0.0883883, split=64)
+        sync()
+        assert rel_err(out0, ref0).max() < TOL[DTYPE_F16]
+        O.append(hp, k_new, v_new, np.arange(len(lens), dtype=np.int32), kv_len - 1, tables)
+        ref1 = O.decode_f64(hp, q, tables, kv_len, None, 0.0883883)
+        for split in (0, 256):
+            out1 = pk.append_decode(dev_f32(q, gpu), dev_f32(k_new, gpu), dev_f32(v_new, gpu),
+                                    dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                                    max_kv_len=2049, scale=0.0883883, split=split)
+            sync()
+            got, _ = host_pages(pk)
+            assert np.array_equal(got.k, hp.k) and np.array_equal(got.v, hp.v)
+            assert rel_err(out1, ref1).max() < TOL[DTYPE_F16], (rep, split)
+
+
+def test_large_query_values_keep_precision(gpu):
+    """q entries far outside f16 range: the MFMA path rescales each head by a
+    power of two before splitting it into f16 hi/lo parts."""
+    say("large q")
+    pk, tables, kv_len, q = _case(gpu, DTYPE_F16, 128, 4, 2, (40, 300), seed=77)
+    q = (q * 1e6).astype(np.float32)
+    q[1] *= 1e-12
+    hp, _ = host_pages(pk)
+    scale = 1e-6
+    ref = O.decode_f64(hp, q, tables, kv_len, None, scale)
+    out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=8, max_kv_len=300,
+                    scale=scale)
+    sync()
+    assert rel_err(out, ref).max() < TOL[DTYPE_F16]
+
+
 def test_reference_single_sequence_call_c1_shape(gpu):
     """lnskv_attention_paged: the reference's encode_attention_paged_q8a call
     (append token `pos`, attend [p_start, pos], scale rsqrt(d)), here on the
