@@ -44,6 +44,9 @@
 // (f16, round to nearest even), stores it to its page slot, and substitutes
 // it into its own registers / V slot when it reaches that page, so the scan
 // never reads the slot back.  Partitions are merged by combine_kernel.
+#include <map>
+#include <mutex>
+#include <tuple>
 #include "lnskv_device.h"
 
 namespace lnskv {
@@ -64,6 +67,7 @@ constexpr int kD = 128;
 constexpr int kRowBytes = kD * 2;         // one (token, kv head) row of f16
 constexpr int kVSlot = kPage * kRowBytes;  // one page of V in LDS (swizzled rows)
 constexpr float kRescaleSlack = 8.0f;     // log2 units the running max may lag
+constexpr int kSkMinPages = 4;            // stream-K: fewest pages per wave
 // Buffer resource word 3 for raw dword access on gfx9-family parts
 // (DATA_FORMAT = 32-bit; no swizzle, no index stride).
 constexpr int kBufferFormat = 0x00020000;
@@ -253,21 +257,68 @@ __device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& s
     st.acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]), st.acc[nb], 0, 0, 0);
 }
 
+// Loads of one piece that do not depend on the sequence's length, issued
+// oldest first in the order they are needed: the table window (64 entries
+// from table index `tbl`), q and, for a fused call, the new token's row.
+template <int REP>
+struct PieceLoads {
+  uint32_t btv;  // lane j: block-table entry tbl + j (0 past the row's end)
+  int tbl;
+  float4v qv[8];
+  float2v knew, vnew;
+};
+
 template <int REP, bool FUSED>
-__global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
-  static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
-  __shared__ __attribute__((aligned(16))) uint8_t vring_[2 * kVSlot];
-  __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
-  lds_u8* vring = (lds_u8*)vring_;
-  lds_u8* newtok = (lds_u8*)newtok_;
-  const int kvh = blockIdx.x, part = blockIdx.y, s = blockIdx.z;
-  const SeqWindow w = seq_window<FUSED>(a, s);
-  if (part >= w.nparts) return;  // wave-uniform
-  const int jp = w.jf + part;
-  const int ta = max(w.p0, jp * a.split);
-  const int tb = min(w.L, (jp + 1) * a.split);
+__device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh, int tbl, PieceLoads<REP>& pl) {
   const int lane = threadIdx.x;
   const int g = lane >> 4, n = lane & 15;
+  const int e = tbl + lane;
+  pl.btv = e < a.bt_stride ? a.bt[(size_t)s * a.bt_stride + e] : 0u;
+  pl.tbl = tbl;
+  const bool qcol = n < 2 * REP;
+  const int hq = qcol ? (n < REP ? n : n - REP) : 0;  // other columns load head 0 and drop it
+  const float4v* qh =
+      reinterpret_cast<const float4v*>(a.q + ((size_t)s * a.n_heads + (size_t)kvh * REP + hq) * kD + 8 * g);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    pl.qv[2 * j] = qh[8 * j];
+    pl.qv[2 * j + 1] = qh[8 * j + 1];
+  }
+  // Every piece of a fused call loads the new token's row (the same 1 KiB
+  // per sequence and kv head, so the repeats hit L2): a load under a branch
+  // would make the compiler wait for it right there.
+  pl.knew = float2v{0.0f, 0.0f};
+  pl.vnew = float2v{0.0f, 0.0f};
+  if constexpr (FUSED) {
+    const size_t src = ((size_t)s * a.n_kv + kvh) * kD + 2 * lane;
+    pl.knew = *reinterpret_cast<const float2v*>(a.k_new + src);
+    pl.vnew = *reinterpret_cast<const float2v*>(a.v_new + src);
+  }
+}
+
+// Where a piece's result goes: the normalised output rows, or partial rows
+// (numerator, running max, sum) for a later merge, head hh of the group in
+// partial row pbase + hh * pstride.
+struct PieceOut {
+  bool final;
+  size_t pbase;
+  int pstride;
+};
+
+// Attends tokens [ta, tb) of sequence s for the REP query heads of kv head
+// kvh, streaming the pages through the 2-slot LDS ring, and writes the
+// result as `po` says.  `append` (fused calls): this piece holds position
+// pos = L-1; it stores the new token to its page slot and substitutes it in
+// the page data it reads.  `tbl_ok`: pl.btv holds the table window from
+// pl.tbl; the window is reloaded when that is not so or does not cover the
+// piece's first page.
+template <int REP, bool FUSED>
+__device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, lds_u8* newtok, PieceLoads<REP>& pl,
+                                          bool tbl_ok, int s, int kvh, int ta, int tb, bool append, int pos,
+                                          const PieceOut& po) {
+  const int lane = threadIdx.x;
+  const int g = lane >> 4, n = lane & 15;
+  const bool qcol = n < 2 * REP;
 
   Stream sm;
   sm.k_pages = a.k_pages;
@@ -288,71 +339,60 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
     sm.vr_sub = (uint32_t)((n & 3) >> 1);
   }
 
-  // The partition's block-table entries, lane i = page pg_first + i (one
-  // coalesced load per 64 pages), then read per page with v_readlane.
+  // Table window: btv lane j holds entry base + win + j; pages are read from
+  // it with v_readlane and the next 64 entries are loaded when the walk
+  // leaves the window.
   const uint32_t* bt_row = a.bt + (size_t)s * a.bt_stride;
   const int pg_first = ta / kPage;
   const int npg = ta < tb ? (tb - 1) / kPage - pg_first + 1 : 0;
-  uint32_t btv = lane < npg ? bt_row[pg_first + lane] : 0u;
+  int base = pl.tbl;
+  int win = 0;
+  auto load_window = [&]() {
+    const int e = base + win + lane;
+    pl.btv = e < a.bt_stride ? bt_row[e] : 0u;
+    wait_vmcnt<0>();  // rare: a sliding window, or a piece of more than 64 pages
+  };
+  if (!tbl_ok || pg_first < base || pg_first - base >= 64) {
+    base = pg_first;
+    load_window();
+  }
+  const int off = pg_first - base;  // first page of the piece within the window
   auto phys_of = [&](int i) -> uint32_t {
-    if ((i & 63) == 0 && i > 0) {  // next 64 entries; drains the loads in flight (once per 64 pages)
-      btv = lane + i < npg ? bt_row[pg_first + i + lane] : 0u;
-      wait_vmcnt<0>();
+    int idx = off + i - win;
+    if (idx >= 64) {
+      win += 64;
+      idx -= 64;
+      load_window();
     }
-    return __builtin_amdgcn_readlane(btv, i & 63);
+    return __builtin_amdgcn_readlane(pl.btv, idx);
   };
 
-  // Loads are issued oldest-first in the order they are needed: the table
-  // window, q, the new token, then the first two pages, so that waiting for
-  // an early load never drains the page loads behind it.
-  const bool qcol = n < 2 * REP;
-  float4v qv[8];
-  {
-    const int hq = qcol ? (n < REP ? n : n - REP) : 0;  // other columns load head 0 and drop it
-    const float4v* qh = reinterpret_cast<const float4v*>(a.q + ((size_t)s * a.n_heads + (size_t)kvh * REP + hq) * kD + 8 * g);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      qv[2 * j] = qh[8 * j];
-      qv[2 * j + 1] = qh[8 * j + 1];
-    }
-  }
-  const int pos = w.L - 1;
-  const bool append = FUSED && part == w.nparts - 1 && w.L > 0;
-  // Every partition of a fused call loads the new token's row (the same
-  // 1 KiB per sequence and kv head, so the repeats hit L2): a load under a
-  // branch would make the compiler wait for it right there.
-  float2v knew = {0.0f, 0.0f}, vnew = {0.0f, 0.0f};
-  if constexpr (FUSED) {
-    const size_t src = ((size_t)s * a.n_kv + kvh) * kD + 2 * lane;
-    knew = *reinterpret_cast<const float2v*>(a.k_new + src);
-    vnew = *reinterpret_cast<const float2v*>(a.v_new + src);
-  }
-
-  // Keeps the loads above ahead of the page loads (the scheduler would sink
-  // them towards their uses, behind the pages).
-  asm volatile("" : "+v"(btv) : : "memory");
+  // Keeps the loads of piece_loads ahead of the page loads (the scheduler
+  // would sink them towards their uses, behind the pages).
+  asm volatile("" : "+v"(pl.btv) : : "memory");
 
   // The first two pages are issued unconditionally, for the same reason: a
-  // partition with fewer pages loads pool page 0 as a stand-in (in bounds,
-  // never consumed; drained before the epilogue).
+  // piece with fewer pages loads pool page 0 as a stand-in (in bounds, never
+  // consumed; drained before the epilogue).
   half8 kA[4], kB[4];
   bool vA = issue_page(sm, phys_of(0), 0, kA) && npg > 0;
   bool vB = issue_page(sm, phys_of(1), 1, kB) && npg > 1;
   // Uses of q and of the new token start here, with the pages in flight.
   asm volatile(""
-               : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(qv[4]), "+v"(qv[5]), "+v"(qv[6]),
-                 "+v"(qv[7]), "+v"(knew), "+v"(vnew));
+               : "+v"(pl.qv[0]), "+v"(pl.qv[1]), "+v"(pl.qv[2]), "+v"(pl.qv[3]), "+v"(pl.qv[4]), "+v"(pl.qv[5]),
+                 "+v"(pl.qv[6]), "+v"(pl.qv[7]), "+v"(pl.knew), "+v"(pl.vnew));
 
-  // Fused append: the partition holding position L-1 converts the new token,
-  // stores it to its page slot, and stages it in LDS for substitution.
+  // Fused append: convert the new token, store it to its page slot, and
+  // stage it in LDS for substitution.
   if constexpr (FUSED) {
     if (append) {
-      const uint32_t kb = to_f16_bits(knew.x) | (to_f16_bits(knew.y) << 16);
-      const uint32_t vb = to_f16_bits(vnew.x) | (to_f16_bits(vnew.y) << 16);
+      const uint32_t kb = to_f16_bits(pl.knew.x) | (to_f16_bits(pl.knew.y) << 16);
+      const uint32_t vb = to_f16_bits(pl.vnew.x) | (to_f16_bits(pl.vnew.y) << 16);
       ((__attribute__((address_space(3))) uint32_t*)newtok)[lane] = kb;
       ((__attribute__((address_space(3))) uint32_t*)(newtok + kRowBytes))[lane] = vb;
-      const int ip = pos / kPage - pg_first;  // the page is normally in the table window
-      const uint32_t ph = ip >= 0 && ip < 64 && ip < npg ? __builtin_amdgcn_readlane(btv, ip) : bt_row[pos / kPage];
+      const int ip = pos / kPage - base - win;  // the page is normally in the table window
+      const uint32_t ph = ip >= 0 && ip < 64 && pos / kPage - pg_first < npg ? __builtin_amdgcn_readlane(pl.btv, ip)
+                                                                              : bt_row[pos / kPage];
       if (ph < a.num_pages) {
         const size_t row = ((size_t)ph * kPage + (size_t)(pos % kPage)) * a.n_kv + kvh;
         *reinterpret_cast<uint32_t*>(a.k_pages_w + row * kRowBytes + 4 * lane) = kb;
@@ -373,7 +413,7 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float qe = qv[2 * j + (e >> 2)][e & 3];
+        const float qe = pl.qv[2 * j + (e >> 2)][e & 3];
         x[j][e] = qcol ? qe * a.scale_log2 : 0.0f;
         amax = fmaxf(amax, fabsf(x[j][e]));
       }
@@ -432,7 +472,9 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
   if (i < npg) step(i, kA, vA, 0, false);
   if (i + 1 < npg) step(i + 1, kB, vB, 1, false);
   if (i + 2 < npg) step(i + 2, kA, vA, 0, false);
-  wait_vmcnt<0>();  // stand-in pages of a partition with fewer than two pages
+  wait_vmcnt<0>();  // stand-in pages of a piece with fewer than two pages
+  // the slots and the staged token are reused by the next piece
+  __builtin_amdgcn_wave_barrier();
 
   // Denominators: sum this head's lanes over the four 16-lane rows.
   st.l = sum_xor16(sum_xor32(st.l));
@@ -456,24 +498,23 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
       for (int ii = 0; ii < 4; ++ii) o[ii][nb] = sum_xor32(st.acc[nb][ii]);
     }
   }
-  // l of the heads this lane writes (REP == 8: lanes g == 1 hold heads 4..7)
+  // l and m of the heads this lane writes (REP == 8: lanes g == 1 hold heads 4..7)
   float lb[REP];
   row_broadcast<REP>(st.l, lb);
   float mb[REP];
   row_broadcast<REP>(st.m, mb);
-  const bool single = w.nparts == 1;
   if (g == 0 || (REP == 8 && g == 1)) {
     const int hb = REP == 8 ? 4 * g : 0;
 #pragma unroll
     for (int ii = 0; ii < NH; ++ii) {
       const float lh = (REP == 8 && g == 1) ? lb[(4 + ii) % REP] : lb[ii];
-      const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + hb + ii;
-      if (single) {
+      if (po.final) {
+        const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + hb + ii;
         const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) a.out[hrow * kD + 16 * nb + n] = o[ii][nb] * inv;
       } else {
-        const size_t pidx = hrow * a.max_parts + part;
+        const size_t pidx = po.pbase + (size_t)(hb + ii) * po.pstride;
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) a.ws_acc[pidx * kD + 16 * nb + n] = o[ii][nb];
         if (n == 0) {
@@ -483,6 +524,174 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
         }
       }
     }
+  }
+}
+
+// Split-K schedule: block (kv head, partition, sequence) attends one
+// partition of `split` tokens.  Partial rows: [sequence][head][partition].
+template <int REP, bool FUSED>
+__global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
+  static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
+  __shared__ __attribute__((aligned(16))) uint8_t vring_[2 * kVSlot];
+  __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
+  const int kvh = blockIdx.x, part = blockIdx.y, s = blockIdx.z;
+  // The table window guesses that the partitions start at position 0 (no
+  // sliding window), so that every load of the piece is issued before the
+  // sequence's length is known; a wrong guess reloads it.
+  PieceLoads<REP> pl;
+  piece_loads<REP, FUSED>(a, s, kvh, part * (a.split / kPage), pl);
+  const SeqWindow w = seq_window<FUSED>(a, s);
+  if (part >= w.nparts) return;  // wave-uniform
+  const int jp = w.jf + part;
+  const int ta = max(w.p0, jp * a.split);
+  const int tb = min(w.L, (jp + 1) * a.split);
+  PieceOut po;
+  po.final = w.nparts == 1;
+  po.pbase = ((size_t)s * a.n_heads + (size_t)kvh * REP) * a.max_parts + part;
+  po.pstride = a.max_parts;
+  run_piece<REP, FUSED>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, w.jf == 0, s, kvh, ta, tb,
+                        FUSED && part == w.nparts - 1 && w.L > 0, w.L - 1, po);
+}
+
+// ---------------------------------------------------------------------------
+// Stream-K schedule.  The units of work are the (sequence, kv head, page)
+// triples of every sequence's attention window, ordered by sequence, then kv
+// head, then page: each (sequence, kv head) is a contiguous segment.  Wave w
+// of W takes units [w*C, (w+1)*C) with C = max(kSkMinPages, ceil(T/W)), so
+// all waves carry the same load and the launch fills the GPU exactly once.
+// A wave's run of a segment is a piece; a piece that is a whole segment
+// writes the output, the others leave partial rows (slot 0: the wave's first
+// piece, slot 1: its last) that combine_sk_kernel merges.
+
+// Per-lane view of sequence `lane` (lanes past n_seq are empty).
+struct SkSeq {
+  int L;     // length, clamped as seq_window clamps it
+  int p0;    // window start
+  int lo;    // first position that owns a page of the segment
+  int np;    // pages per (sequence, kv head) segment
+  int cnt;   // units of the sequence: np * n_kv
+  int incl;  // inclusive prefix sum of cnt over the lanes
+};
+
+template <bool FUSED>
+__device__ __forceinline__ SkSeq sk_seqs(const DecodeArgs& a, int n_seq) {
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  SkSeq q;
+  int L = 0, p0 = 0;
+  if (lane < n_seq) {
+    L = a.kv_len ? a.kv_len[lane] : a.kv_len_scalar;
+    p0 = a.p_start ? a.p_start[lane] : a.p_start_scalar;
+  }
+  L = min(max(L, 0), min(a.max_kv_len, a.bt_stride * kPage));
+  p0 = min(max(p0, 0), L);
+  int lo = p0;
+  if (FUSED && L > 0) lo = min(lo, L - 1);
+  q.L = L;
+  q.p0 = p0;
+  q.lo = lo;
+  q.np = L > lo ? (L - 1) / kPage - lo / kPage + 1 : 0;
+  q.cnt = q.np * a.n_kv;
+  int x = q.cnt;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int y = __shfl_up(x, d, kWave);
+    if (lane >= d) x += y;
+  }
+  q.incl = x;
+  return q;
+}
+
+__device__ __forceinline__ int sk_chunk(int total, int n_waves) {
+  return max(kSkMinPages, (total + n_waves - 1) / n_waves);
+}
+
+template <int REP, bool FUSED>
+__global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
+  static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
+  __shared__ __attribute__((aligned(16))) uint8_t vring_[2 * kVSlot];
+  __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
+  const int wv = blockIdx.x;
+  const SkSeq q = sk_seqs<FUSED>(a, n_seq);
+  const int total = __builtin_amdgcn_readlane(q.incl, kWave - 1);
+  const int chunk = sk_chunk(total, n_waves);
+  int cur = wv * chunk;
+  const int end = min(total, cur + chunk);
+  int slot = 0;
+  while (cur < end) {  // wave-uniform
+    // the sequence holding unit cur: lanes whose inclusive prefix is <= cur
+    const int s = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(q.incl <= cur));
+    const int np = __builtin_amdgcn_readlane(q.np, s);
+    const int L = __builtin_amdgcn_readlane(q.L, s);
+    const int p0 = __builtin_amdgcn_readlane(q.p0, s);
+    const int pg0 = __builtin_amdgcn_readlane(q.lo, s) / kPage;  // the segment's first page
+    const int sbase = __builtin_amdgcn_readlane(q.incl, s) - __builtin_amdgcn_readlane(q.cnt, s);
+    const int kvh = (cur - sbase) / np;
+    const int seg0 = sbase + kvh * np;
+    const int pend = min(end, seg0 + np);
+    const int i0 = cur - seg0, i1 = pend - seg0;  // pages [i0, i1) of the segment
+    PieceLoads<REP> pl;
+    piece_loads<REP, FUSED>(a, s, kvh, pg0 + i0, pl);
+    PieceOut po;
+    po.final = i0 == 0 && i1 == np;
+    po.pbase = ((size_t)wv * 2 + slot) * REP;
+    po.pstride = 1;
+    run_piece<REP, FUSED>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh, max(p0, (pg0 + i0) * kPage),
+                          min(L, (pg0 + i1) * kPage), FUSED && i1 == np && L > 0, L - 1, po);
+    cur = pend;
+    slot = 1;
+  }
+}
+
+// Merges the pieces of each (sequence, kv head) segment that spans several
+// waves, and writes zeros for empty segments.  Block (kv head, sequence),
+// threads over (head, dim); every wave recomputes the layout.
+template <int REP, bool FUSED>
+__global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
+  constexpr int CHUNK = 8;
+  const int kvh = blockIdx.x, s = blockIdx.y;
+  const SkSeq q = sk_seqs<FUSED>(a, n_seq);
+  const int total = __builtin_amdgcn_readlane(q.incl, kWave - 1);
+  const int np = __builtin_amdgcn_readlane(q.np, s);
+  const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP) * kD;
+  if (np == 0) {
+    for (int idx = threadIdx.x; idx < REP * kD; idx += kBlock) a.out[orow + idx] = 0.0f;
+    return;
+  }
+  const int chunk = sk_chunk(total, n_waves);
+  const int seg0 = __builtin_amdgcn_readlane(q.incl, s) - __builtin_amdgcn_readlane(q.cnt, s) + kvh * np;
+  const int wa = seg0 / chunk, wb = (seg0 + np - 1) / chunk;
+  if (wa == wb) return;  // one piece: the decode kernel wrote the output
+  const int first_slot = seg0 == wa * chunk ? 0 : 1;  // the piece of wave wa is its first unless it starts inside
+  const int nw = wb - wa + 1;
+  for (int idx = threadIdx.x; idx < REP * kD; idx += kBlock) {
+    const int h = idx / kD, i = idx % kD;
+    float M = kMInit, A = 0.0f, Ls = 0.0f;
+    for (int j0 = 0; j0 < nw; j0 += CHUNK) {
+      float2 pm[CHUNK];
+      float pa[CHUNK];
+#pragma unroll
+      for (int u = 0; u < CHUNK; ++u) {
+        const int j = j0 + u;
+        const size_t pidx = ((size_t)(wa + j) * 2 + (j == 0 ? first_slot : 0)) * REP + h;
+        const bool in = j < nw;
+        pm[u] = in ? reinterpret_cast<const float2*>(a.ws_ml)[pidx] : make_float2(kMInit, 0.0f);
+        pa[u] = in ? a.ws_acc[pidx * kD + i] : 0.0f;
+      }
+      float Mc = M;
+#pragma unroll
+      for (int u = 0; u < CHUNK; ++u) Mc = fmaxf(Mc, pm[u].x);
+      const float r = fast_exp2(M - Mc);
+      A *= r;
+      Ls *= r;
+#pragma unroll
+      for (int u = 0; u < CHUNK; ++u) {
+        const float wj = fast_exp2(pm[u].x - Mc);
+        A = fmaf(wj, pa[u], A);
+        Ls = fmaf(wj, pm[u].y, Ls);
+      }
+      M = Mc;
+    }
+    a.out[orow + idx] = Ls > 0.0f ? A / Ls : 0.0f;
   }
 }
 
@@ -503,5 +712,74 @@ int launch_decode_mfma_f16_d128(const DecodeArgs& a, int rep, int n_seq, hipStre
 
 template int launch_decode_mfma_f16_d128<false>(const DecodeArgs&, int, int, hipStream_t);
 template int launch_decode_mfma_f16_d128<true>(const DecodeArgs&, int, int, hipStream_t);
+
+namespace {
+template <int REP, bool FUSED>
+int sk_waves_of(int cus, int* waves) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED>, kWave, 0) != hipSuccess ||
+      per_cu <= 0)
+    return fail(LNSKV_ERR_HIP, "occupancy query of the stream-K decode kernel failed");
+  *waves = cus * per_cu;
+  return LNSKV_OK;
+}
+}  // namespace
+
+int mfma_sk_waves(int rep, bool fused, int* waves) {
+  // resident single-wave blocks of the kernel on the current device, kept per
+  // (device, rep, fused)
+  static std::mutex mu;
+  static std::map<std::tuple<int, int, bool>, int> cache;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(dev, rep, fused);
+  const auto it = cache.find(key);
+  if (it != cache.end()) {
+    *waves = it->second;
+    return LNSKV_OK;
+  }
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return fail(LNSKV_ERR_HIP, "compute-unit count query failed");
+  int rc = LNSKV_ERR_UNSUPPORTED;
+  switch (rep) {
+    case 1: rc = fused ? sk_waves_of<1, true>(cus, waves) : sk_waves_of<1, false>(cus, waves); break;
+    case 2: rc = fused ? sk_waves_of<2, true>(cus, waves) : sk_waves_of<2, false>(cus, waves); break;
+    case 4: rc = fused ? sk_waves_of<4, true>(cus, waves) : sk_waves_of<4, false>(cus, waves); break;
+    case 8: rc = fused ? sk_waves_of<8, true>(cus, waves) : sk_waves_of<8, false>(cus, waves); break;
+    default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
+  }
+  if (rc == LNSKV_OK) cache[key] = *waves;
+  return rc;
+}
+
+template <bool FUSED>
+int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, hipStream_t st) {
+  if (n_seq > kWave) return fail(LNSKV_ERR_INVALID, "stream-K decode serves at most %d sequences", kWave);
+  const dim3 cgrid((unsigned)a.n_kv, (unsigned)n_seq);
+  switch (rep) {
+    case 1:
+      decode_sk_kernel<1, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+      combine_sk_kernel<1, FUSED><<<cgrid, kBlock, 0, st>>>(a, n_seq, n_waves);
+      break;
+    case 2:
+      decode_sk_kernel<2, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+      combine_sk_kernel<2, FUSED><<<cgrid, kBlock, 0, st>>>(a, n_seq, n_waves);
+      break;
+    case 4:
+      decode_sk_kernel<4, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+      combine_sk_kernel<4, FUSED><<<cgrid, kBlock, 0, st>>>(a, n_seq, n_waves);
+      break;
+    case 8:
+      decode_sk_kernel<8, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+      combine_sk_kernel<8, FUSED><<<cgrid, kBlock, 0, st>>>(a, n_seq, n_waves);
+      break;
+    default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
+  }
+  return hip_check("stream-K decode kernel launch");
+}
+
+template int launch_decode_mfma_sk<false>(const DecodeArgs&, int, int, int, hipStream_t);
+template int launch_decode_mfma_sk<true>(const DecodeArgs&, int, int, int, hipStream_t);
 
 }  // namespace lnskv

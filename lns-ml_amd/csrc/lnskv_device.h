@@ -263,6 +263,12 @@ template <int DT, bool FUSED>
 int launch_decode_valu(const DecodeArgs& a, int d, int rep, int n_seq, hipStream_t st);
 template <bool FUSED>
 int launch_decode_mfma_f16_d128(const DecodeArgs& a, int rep, int n_seq, hipStream_t st);
+// Stream-K schedule of the MFMA kernel (n_seq <= 64): n_waves single-wave
+// blocks, workspace of n_waves * 2 * rep partial rows.
+template <bool FUSED>
+int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, hipStream_t st);
+// Waves of the stream-K kernel resident at once on the current device.
+int mfma_sk_waves(int rep, bool fused, int* waves);
 
 int hip_check(const char* what);
 

@@ -199,9 +199,11 @@ bool force_valu() {
 
 // The MFMA kernel serves f16 pages with head_dim 128 (the Llama/Mixtral
 // shapes); every other combination runs the generic VALU kernel.
+bool mfma_path(int dtype, int d, int rep);
+
 template <bool FUSED>
 int launch_decode(const DecodeArgs& a, int dtype, int d, int rep, int n_seq, hipStream_t st) {
-  if (dtype == LNSKV_DTYPE_F16 && d == 128 && rep <= 8 && !force_valu())
+  if (mfma_path(dtype, d, rep))
     return launch_decode_mfma_f16_d128<FUSED>(a, rep, n_seq, st);
   switch (dtype) {
     case LNSKV_DTYPE_F32: return launch_decode_valu<LNSKV_DTYPE_F32, FUSED>(a, d, rep, n_seq, st);
@@ -228,6 +230,47 @@ int choose_split(int n_seq, int n_kv, int max_kv_len) {
 size_t workspace_bytes(int n_seq, int n_heads, int d, int max_parts) {
   if (max_parts <= 1) return 0;
   return (size_t)n_seq * n_heads * max_parts * ((size_t)d + 2) * sizeof(float);
+}
+
+bool mfma_path(int dtype, int d, int rep) {
+  return dtype == LNSKV_DTYPE_F16 && d == 128 && (rep == 1 || rep == 2 || rep == 4 || rep == 8) && !force_valu();
+}
+
+// How one decode call runs.  Stream-K (one wave per resident slot, each
+// taking an equal share of all pages) when the caller leaves the split to
+// the library, the MFMA kernel serves the pages and there are at most 64
+// sequences; split-K partitions of `split` tokens otherwise.
+struct DecodePlan {
+  int split = 0;      // split-K: tokens per partition
+  int max_parts = 1;  // split-K: partitions of the longest sequence
+  int sk_waves = 0;   // > 0: stream-K with this many waves
+  size_t ws_bytes = 0;
+};
+
+int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, int split_tokens, int fused,
+                DecodePlan* p) {
+  const int n_kv = (int)c->n_kv_heads, d = (int)c->head_dim, rep = n_heads / n_kv;
+  *p = DecodePlan{};
+  const int64_t units = (int64_t)n_seq * n_kv * ((int64_t)max_kv_len / kPage + 1);
+  if (split_tokens == 0 && mfma_path((int)c->dtype, d, rep) && n_seq <= kWave && units < ((int64_t)1 << 30)) {
+    // fused < 0: either kind (the workspace query), sized for the larger
+    int w0 = 0, w1 = 0;
+    if (fused <= 0)
+      if (int rc = mfma_sk_waves(rep, false, &w0)) return rc;
+    if (fused != 0)
+      if (int rc = mfma_sk_waves(rep, true, &w1)) return rc;
+    p->sk_waves = std::max(w0, w1);
+    p->ws_bytes = (size_t)p->sk_waves * 2 * rep * ((size_t)d + 2) * sizeof(float);
+    return LNSKV_OK;
+  }
+  p->split = split_tokens ? split_tokens : choose_split(n_seq, n_kv, max_kv_len);
+  if (p->split < kPage || p->split % kPage != 0)
+    return fail(LNSKV_ERR_INVALID, "split_tokens %d must be a positive multiple of 16", p->split);
+  p->max_parts = std::max(1, (max_kv_len + p->split - 1) / p->split);
+  if (p->max_parts > 65535)
+    return fail(LNSKV_ERR_INVALID, "max_kv_len %d needs more than 65535 partitions", max_kv_len);
+  p->ws_bytes = workspace_bytes(n_seq, n_heads, d, p->max_parts);
+  return LNSKV_OK;
 }
 
 // Library-kept workspace per device, grown on demand.
@@ -278,13 +321,11 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
   if (bt_stride <= 0) return fail(LNSKV_ERR_INVALID, "bt_stride %d must be positive", bt_stride);
   if (max_kv_len < 0) return fail(LNSKV_ERR_INVALID, "max_kv_len %d is negative", max_kv_len);
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(LNSKV_ERR_INVALID, "scale must be positive and finite");
-  if (split == 0) split = choose_split(n_seq, (int)c->n_kv_heads, max_kv_len);
-  if (split < kPage || split % kPage != 0)
-    return fail(LNSKV_ERR_INVALID, "split_tokens %d must be a positive multiple of 16", split);
+  if (split < 0) return fail(LNSKV_ERR_INVALID, "split_tokens %d is negative", split);
   const int rep = n_heads / (int)c->n_kv_heads;
-  const int max_parts = std::max(1, (max_kv_len + split - 1) / split);
-  if (max_parts > 65535) return fail(LNSKV_ERR_INVALID, "max_kv_len %d needs more than 65535 partitions", max_kv_len);
-  const size_t need = workspace_bytes(n_seq, n_heads, (int)c->head_dim, max_parts);
+  DecodePlan plan;
+  if (int rc = plan_decode(c, n_seq, n_heads, max_kv_len, split, FUSED ? 1 : 0, &plan)) return rc;
+  const size_t need = plan.ws_bytes;
   if (need > 0) {
     if (ws == nullptr) {
       if (int rc = library_workspace(need, &ws)) return rc;
@@ -313,14 +354,19 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
   a.bt_stride = bt_stride;
   a.n_kv = (int32_t)c->n_kv_heads;
   a.n_heads = n_heads;
-  a.split = split;
-  a.max_parts = max_parts;
+  a.split = plan.split;
+  a.max_parts = plan.max_parts;
   a.max_kv_len = max_kv_len;
   a.num_pages = c->num_pages;
   a.scale_log2 = scale * kLog2e;
+  if (plan.sk_waves > 0) {
+    a.ws_acc = static_cast<float*>(ws);
+    a.ws_ml = a.ws_acc + (size_t)plan.sk_waves * 2 * rep * c->head_dim;
+    return launch_decode_mfma_sk<FUSED>(a, rep, n_seq, plan.sk_waves, (hipStream_t)stream);
+  }
   if (need > 0) {
     a.ws_acc = static_cast<float*>(ws);
-    a.ws_ml = a.ws_acc + (size_t)n_seq * n_heads * max_parts * c->head_dim;
+    a.ws_ml = a.ws_acc + (size_t)n_seq * n_heads * plan.max_parts * c->head_dim;
   }
   return launch_decode<FUSED>(a, c->dtype, (int)c->head_dim, rep, n_seq, (hipStream_t)stream);
 }
@@ -422,12 +468,11 @@ int lnskv_decode_workspace_size(const lnskv_pages* c, int32_t n_seq, int32_t n_h
   if (!bytes) return fail(LNSKV_ERR_INVALID, "bytes is NULL");
   *bytes = 0;
   if (int rc = check_geometry(c)) return rc;
-  if (n_seq <= 0 || n_heads <= 0 || max_kv_len < 0) return fail(LNSKV_ERR_INVALID, "bad shape");
-  const int split = split_tokens ? split_tokens : choose_split(n_seq, (int)c->n_kv_heads, max_kv_len);
-  if (split < kPage || split % kPage) return fail(LNSKV_ERR_INVALID, "split_tokens %d", split_tokens);
-  const int max_parts = std::max(1, (max_kv_len + split - 1) / split);
-  if (max_parts > 65535) return fail(LNSKV_ERR_INVALID, "max_kv_len %d needs more than 65535 partitions", max_kv_len);
-  *bytes = workspace_bytes(n_seq, n_heads, (int)c->head_dim, max_parts);
+  if (n_seq <= 0 || n_heads <= 0 || max_kv_len < 0 || split_tokens < 0 || n_heads % (int)c->n_kv_heads != 0)
+    return fail(LNSKV_ERR_INVALID, "bad shape");
+  DecodePlan plan;
+  if (int rc = plan_decode(c, n_seq, n_heads, max_kv_len, split_tokens, -1, &plan)) return rc;
+  *bytes = plan.ws_bytes;
   return LNSKV_OK;
 }
 

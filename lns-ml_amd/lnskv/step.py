@@ -63,7 +63,7 @@ class StepRunner:
         self.copy_src = _i32(np.array([c[0] for c in w.copies], np.uint32), self.dev)
         self.copy_dst = _i32(np.array([c[1] for c in w.copies], np.uint32), self.dev)
         ws = self.layers[0].workspace_size(max(self.n_dec, 1), hq, self.max_kv_len, w.split)
-        self.workspace = torch.zeros(max(ws, 4), dtype=torch.uint8, device=self.dev)  # split-K counters start at 0
+        self.workspace = torch.zeros(max(ws, 4), dtype=torch.uint8, device=self.dev)
 
     def fill(self, pk: PagedKV, seed: int) -> None:
         g = torch.Generator(device=self.dev)

@@ -220,3 +220,72 @@ def test_reference_single_sequence_call_c1_shape(gpu):
         assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8))
         assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8))
         assert rel_err(out, ref).max() < TOL[dtype]
+
+
+def _sk_lens(n, seed):
+    """Lengths for a stream-K batch: empty, sub-page, page-edge and long
+    sequences, so that waves hold several pieces and segments span waves."""
+    rng = np.random.default_rng(seed)
+    base = [0, 1, 15, 16, 17, 31, 33, 3000, 4096, 2047]
+    lens = base + list(rng.integers(1, 2500, n - len(base)))
+    return tuple(int(x) for x in lens[:n])
+
+
+@pytest.mark.parametrize("rep", [1, 2, 4, 8])
+def test_stream_k_schedule(gpu, rep):
+    """split_tokens = 0 on the MFMA path runs the stream-K schedule (every
+    wave an equal share of all pages; pieces merged by combine_sk_kernel).
+    64 sequences (its limit) with empty, short and long lengths, windows,
+    a missing page; unfused and fused, against the f64 oracle and against
+    the split-K schedule."""
+    say("stream-K rep", rep)
+    n_kv, d = 8, 128
+    lens = _sk_lens(64, seed=rep)
+    pk, tables, kv_len, q = _case(gpu, DTYPE_F16, d, rep, n_kv, lens, seed=90 + rep)
+    tables[5, 0] = NO_PAGE  # a missing page: its tokens are skipped
+    rng = np.random.default_rng(rep + 7)
+    p_start = np.zeros(len(lens), np.int32)
+    p_start[7:12] = [10, 2900, 0, 17, 1000]
+    hp, _ = host_pages(pk)
+    scale = 1.0 / np.sqrt(d)
+    ref = O.decode_f64(hp, q, tables, kv_len, p_start, scale)
+    for split in (0, 128):
+        out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                        max_kv_len=int(kv_len.max()), scale=float(scale), p_start=dev_i32(p_start, gpu),
+                        split=split)
+        sync()
+        err = rel_err(out, ref)
+        assert err.max() < TOL[DTYPE_F16], (split, err.max())
+        assert np.all(out.cpu().numpy()[0] == 0.0)  # empty sequence
+    # fused: every sequence gains one token
+    kv1 = np.minimum(kv_len + 1, (tables.shape[1]) * 16).astype(np.int32)
+    k_new = rng.standard_normal((len(lens), n_kv, d)).astype(np.float32)
+    v_new = rng.standard_normal((len(lens), n_kv, d)).astype(np.float32)
+    O.append(hp, k_new, v_new, np.arange(len(lens), dtype=np.int32), kv1 - 1, tables)
+    ref1 = O.decode_f64(hp, q, tables, kv1, p_start, scale)
+    out1 = pk.append_decode(dev_f32(q, gpu), dev_f32(k_new, gpu), dev_f32(v_new, gpu), dev_i32(tables, gpu),
+                            dev_i32(kv1, gpu), n_heads=n_kv * rep, max_kv_len=int(kv1.max()), scale=float(scale),
+                            p_start=dev_i32(p_start, gpu), split=0)
+    sync()
+    got, _ = host_pages(pk)
+    assert np.array_equal(got.k, hp.k) and np.array_equal(got.v, hp.v)
+    assert rel_err(out1, ref1).max() < TOL[DTYPE_F16]
+
+
+def test_stream_k_caller_workspace_and_fallback(gpu):
+    """A caller-provided workspace of exactly the queried size serves the
+    stream-K schedule; 65 sequences fall back to split-K; one short sequence
+    leaves most waves idle."""
+    say("stream-K workspace / fallback")
+    n_kv, d, rep = 8, 128, 4
+    for lens in (_sk_lens(64, 3), _sk_lens(65, 4), (5,), (1,) * 64):
+        pk, tables, kv_len, q = _case(gpu, DTYPE_F16, d, rep, n_kv, lens, seed=len(lens))
+        hp, _ = host_pages(pk)
+        ref = O.decode_f64(hp, q, tables, kv_len, None, 0.0883883)
+        mkv = int(kv_len.max())
+        nbytes = pk.workspace_size(len(lens), n_kv * rep, mkv, 0)
+        ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=gpu)
+        out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                        max_kv_len=mkv, scale=0.0883883, split=0, workspace=ws)
+        sync()
+        assert rel_err(out, ref).max() < TOL[DTYPE_F16], len(lens)
