@@ -3,8 +3,9 @@
 
 One step = one layer's work for the whole batch of the chosen configuration
 (default c2, the Llama-3-8B-shaped B=32 ragged batch): page copies and chunk
-appends where the config has them, then the fused 1-token append + split-K
-paged decode attention.  Inputs are resident in HBM before timing starts.
+appends where the config has them, then the fused 1-token append + paged
+decode attention (one lnskv_append_decode call: the stream-K decode kernel and
+its combine kernel for c2).  Inputs are resident in HBM before timing starts.
 Steps cycle through --layers independent pools (4 by default, 4 GB for c2) so
 that no step finds the previous step's pages in the 256 MB last-level cache,
 as in a real multi-layer decode.
@@ -15,6 +16,10 @@ page copies) / wall time per step; `roofline` divides the same bytes by the
 HIP-event duration of the step's kernels, measured live on their stream;
 `cpu_baseline` times the oracle's reference-order CPU scan (append + online
 softmax per query head, OpenMP over sequence x kv head) on this host.
+`roofline.traffic` is the HBM bytes per step that rocprofv3's FETCH_SIZE and
+WRITE_SIZE counters gave for the same workload, scaled by what they read for
+a plain copy of known size; it is read from profiles/<config>_traffic.json
+(written from those counter runs) and is null when that file is absent.
 """
 from __future__ import annotations
 
@@ -44,6 +49,9 @@ def parse():
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = all cores the process may use")
     p.add_argument("--copy-mb", type=int, default=1024,
                    help="size of the device-to-device copy that measures the copy ceiling (0 = skip)")
+    p.add_argument("--graph", type=int, default=0,
+                   help="1: replay each layer's step from a captured HIP graph (no per-step host launch work); "
+                        "0: launch eagerly from Python")
     p.add_argument("--copy-only", action="store_true",
                    help="run only the plain copy (the calibration kernel for HBM byte counters)")
     return p.parse_args()
@@ -68,6 +76,16 @@ def copy_ceiling(dev, mb: int, reps: int = 20) -> dict:
     torch.cuda.synchronize()
     dt = s.elapsed_time(e) / 1e3 / reps
     return {"bytes_per_copy": 2 * n * 4, "gb_per_s": round(2 * n * 4 / dt / 1e9, 1)}
+
+
+def measured_traffic(name: str):
+    """HBM bytes per step from the committed counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return int(t["hbm_bytes_per_step"])
 
 
 def cpu_baseline(w, runner, seconds: float, threads: int):
@@ -138,24 +156,28 @@ def main():
     nb = w.algorithmic_bytes()
     stream = torch.cuda.current_stream(dev)
 
+    if args.graph:
+        graphs = [runner.capture(layer) for layer in range(args.layers)]
+        step = lambda i: graphs[i % args.layers].replay()  # noqa: E731  (slower than eager on ROCm 7: measured)
+    else:
+        step = lambda i: runner.run(i % args.layers)  # noqa: E731
     for i in range(args.warmup):
-        runner.run(i % args.layers)
+        step(i)
     torch.cuda.synchronize()
 
-    # timed region: exactly K steps, synchronized on both sides
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    # timed region: exactly K steps, synchronized on both sides; one pair of
+    # HIP events on the kernels' stream brackets the K steps (an event pair
+    # per step would add its own gaps between the steps)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    start.record(stream)
     for i in range(args.steps):
-        starts[i].record(stream)
-        runner.run(i % args.layers)
-        ends[i].record(stream)
+        step(i)
+    end.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / args.steps
-    ev = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))  # ms, on the kernels' stream
-    ev_mean = sum(ev) / len(ev) / 1e3
-    ev_med = ev[len(ev) // 2] / 1e3
+    ev_mean = start.elapsed_time(end) / 1e3 / args.steps
 
     gbs_wall = nb["total"] / wall / 1e9
     gbs_ev = nb["total"] / ev_mean / 1e9
@@ -175,7 +197,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(wall * 1e3, 5),
         "us_per_step": round(wall * 1e6, 2),
-        "us_per_step_event_median": round(ev_med * 1e6, 2),
+        "us_per_step_events": round(ev_mean * 1e6, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -193,6 +215,7 @@ def main():
             "tokens_attended": int(w.kv_len[w.decode].sum()),
             "split_tokens": int(w.split),
             "layers_cycled": args.layers,
+            "launch": "HIP graph replay per step" if args.graph else "eager launches from Python",
             "algorithmic_bytes_per_step": int(nb["total"]),
             "bytes_breakdown": {k: int(v) for k, v in nb.items() if k != "total"},
             "parallelism": "single GPU",
@@ -203,8 +226,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs_ev / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "append_decode step (decode_kernel + combine_kernel), HIP events per step",
+            "traffic": measured_traffic(w.name),
+            "kernel": ("one step's kernels on their stream (c2: decode_sk_kernel + combine_sk_kernel "
+                       "of one lnskv_append_decode call), mean HIP-event duration per step"),
             "copy_ceiling_gbs": copy["gb_per_s"] if copy else None,
             "frac_of_copy_ceiling": round(gbs_ev / copy["gb_per_s"], 4) if copy else None,
         },

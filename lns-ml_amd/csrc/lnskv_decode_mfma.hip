@@ -44,6 +44,7 @@
 // (f16, round to nearest even), stores it to its page slot, and substitutes
 // it into its own registers / V slot when it reaches that page, so the scan
 // never reads the slot back.  Partitions are merged by combine_kernel.
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -144,7 +145,7 @@ __device__ __forceinline__ void scale_rows(WaveState<REP>& st, float alpha, int 
 struct Stream {
   const uint8_t* k_pages;
   const uint8_t* v_pages;
-  lds_u8* vring;       // 2 slots of kVSlot bytes
+  lds_u8* vring;       // ring of page slots of kVSlot bytes
   uint32_t koff;       // K: token n row + 16g
   uint32_t voff[4];    // V DMA, instruction j: token 4g+j row + 16*(n ^ sw(4j+g))
   uint32_t vr_off;     // transposed read: row 4*(n>>2)+g, (chunk ^ sw) folded per nb
@@ -306,13 +307,14 @@ struct PieceOut {
 };
 
 // Attends tokens [ta, tb) of sequence s for the REP query heads of kv head
-// kvh, streaming the pages through the 2-slot LDS ring, and writes the
+// kvh, streaming the pages with DEPTH of them in flight (K in registers, V
+// in a DEPTH-slot LDS ring), and writes the
 // result as `po` says.  `append` (fused calls): this piece holds position
 // pos = L-1; it stores the new token to its page slot and substitutes it in
 // the page data it reads.  `tbl_ok`: pl.btv holds the table window from
 // pl.tbl; the window is reloaded when that is not so or does not cover the
 // piece's first page.
-template <int REP, bool FUSED>
+template <int REP, bool FUSED, int DEPTH>
 __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, lds_u8* newtok, PieceLoads<REP>& pl,
                                           bool tbl_ok, int s, int kvh, int ta, int tb, bool append, int pos,
                                           const PieceOut& po) {
@@ -371,12 +373,13 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
   // would sink them towards their uses, behind the pages).
   asm volatile("" : "+v"(pl.btv) : : "memory");
 
-  // The first two pages are issued unconditionally, for the same reason: a
+  // The first DEPTH pages are issued unconditionally, for the same reason: a
   // piece with fewer pages loads pool page 0 as a stand-in (in bounds, never
   // consumed; drained before the epilogue).
-  half8 kA[4], kB[4];
-  bool vA = issue_page(sm, phys_of(0), 0, kA) && npg > 0;
-  bool vB = issue_page(sm, phys_of(1), 1, kB) && npg > 1;
+  half8 kbuf[DEPTH][4];
+  bool vld[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) vld[d] = issue_page(sm, phys_of(d), d, kbuf[d]) && npg > d;
   // Uses of q and of the new token start here, with the pages in flight.
   asm volatile(""
                : "+v"(pl.qv[0]), "+v"(pl.qv[1]), "+v"(pl.qv[2]), "+v"(pl.qv[3]), "+v"(pl.qv[4]), "+v"(pl.qv[5]),
@@ -437,12 +440,17 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
     st.l = 0.0f;
   }
 
-  // Page i: wait for its loads (the 8 of page i+1 may stay in flight), patch
-  // in the new token if it lives there, consume, refill the slot with i+2.
-  // `steady` asserts pages i+1 and i+2 exist, which lets the compiler's wait
-  // counting see exactly two pages in flight.
+  // Page i: wait for its loads (those of the pages issued after it may stay
+  // in flight), patch in the new token if it lives there, consume, refill the
+  // slot with page i + DEPTH.  `steady` asserts pages i+1 .. i+DEPTH exist,
+  // which lets the compiler's wait counting see exactly DEPTH pages in
+  // flight; the other steps use the masked consume only.
   auto step = [&](int i, half8(&k)[4], bool& valid, int slot, bool steady) {
-    if (steady || i + 1 < npg) wait_vmcnt<8>(); else wait_vmcnt<0>();
+    const int ahead = steady ? DEPTH - 1 : min(npg - 1 - i, DEPTH - 1);  // pages issued after page i
+    if (ahead >= 3) wait_vmcnt<24>();
+    else if (ahead == 2) wait_vmcnt<16>();
+    else if (ahead == 1) wait_vmcnt<8>();
+    else wait_vmcnt<0>();
     const int tok0 = (pg_first + i) * kPage;
     if (attend_new && pos / kPage == pg_first + i) {
       const int t = pos % kPage;
@@ -457,22 +465,22 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
       }
       __builtin_amdgcn_wave_barrier();
     }
-    if (valid && tok0 >= ta && tok0 + kPage <= tb)
+    if (steady && valid && tok0 >= ta && tok0 + kPage <= tb)
       consume_page<REP, true>(st, sm, k, slot, tok0, valid, ta, tb, g, n);
     else
       consume_page<REP, false>(st, sm, k, slot, tok0, valid, ta, tb, g, n);
-    if (steady || i + 2 < npg) valid = issue_page(sm, phys_of(i + 2), slot, k);
+    if (steady || i + DEPTH < npg) valid = issue_page(sm, phys_of(i + DEPTH), slot, k);
   };
   int i = 0;
-  for (; i + 3 < npg; i += 2) {
-    step(i, kA, vA, 0, true);
-    step(i + 1, kB, vB, 1, true);
+  for (; i + 2 * DEPTH - 1 < npg; i += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) step(i + d, kbuf[d], vld[d], d, true);
   }
-  // the last one to three pages
-  if (i < npg) step(i, kA, vA, 0, false);
-  if (i + 1 < npg) step(i + 1, kB, vB, 1, false);
-  if (i + 2 < npg) step(i + 2, kA, vA, 0, false);
-  wait_vmcnt<0>();  // stand-in pages of a piece with fewer than two pages
+  // the last one to 2*DEPTH-1 pages
+#pragma unroll
+  for (int d = 0; d < 2 * DEPTH - 1; ++d)
+    if (i + d < npg) step(i + d, kbuf[d % DEPTH], vld[d % DEPTH], d % DEPTH, false);
+  wait_vmcnt<0>();  // stand-in pages of a piece with fewer than DEPTH pages
   // the slots and the staged token are reused by the next piece
   __builtin_amdgcn_wave_barrier();
 
@@ -549,7 +557,7 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
   po.final = w.nparts == 1;
   po.pbase = ((size_t)s * a.n_heads + (size_t)kvh * REP) * a.max_parts + part;
   po.pstride = a.max_parts;
-  run_piece<REP, FUSED>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, w.jf == 0, s, kvh, ta, tb,
+  run_piece<REP, FUSED, 2>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, w.jf == 0, s, kvh, ta, tb,
                         FUSED && part == w.nparts - 1 && w.L > 0, w.L - 1, po);
 }
 
@@ -605,10 +613,10 @@ __device__ __forceinline__ int sk_chunk(int total, int n_waves) {
   return max(kSkMinPages, (total + n_waves - 1) / n_waves);
 }
 
-template <int REP, bool FUSED>
+template <int REP, bool FUSED, int DEPTH>
 __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
-  __shared__ __attribute__((aligned(16))) uint8_t vring_[2 * kVSlot];
+  __shared__ __attribute__((aligned(16))) uint8_t vring_[DEPTH * kVSlot];
   __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
   const int wv = blockIdx.x;
   const SkSeq q = sk_seqs<FUSED>(a, n_seq);
@@ -635,7 +643,7 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
     po.final = i0 == 0 && i1 == np;
     po.pbase = ((size_t)wv * 2 + slot) * REP;
     po.pstride = 1;
-    run_piece<REP, FUSED>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh, max(p0, (pg0 + i0) * kPage),
+    run_piece<REP, FUSED, DEPTH>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh, max(p0, (pg0 + i0) * kPage),
                           min(L, (pg0 + i1) * kPage), FUSED && i1 == np && L > 0, L - 1, po);
     cur = pend;
     slot = 1;
@@ -714,19 +722,33 @@ template int launch_decode_mfma_f16_d128<false>(const DecodeArgs&, int, int, hip
 template int launch_decode_mfma_f16_d128<true>(const DecodeArgs&, int, int, hipStream_t);
 
 namespace {
+// Stream-K launch shape: two pages in flight per wave and four waves per CU
+// (one per SIMD).  Measured on the c2 shape: one wave per SIMD matches two
+// (2-4 pages in flight each) within noise, and avoids the older-wave-first
+// issue arbitration that runs the second wave of a SIMD about 30% slower.
+constexpr int kSkDepth = 2;
+constexpr int kSkWavesPerCu = 4;
+
 template <int REP, bool FUSED>
 int sk_waves_of(int cus, int* waves) {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED>, kWave, 0) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, kSkDepth>, kWave, 0) !=
+          hipSuccess ||
       per_cu <= 0)
     return fail(LNSKV_ERR_HIP, "occupancy query of the stream-K decode kernel failed");
-  *waves = cus * per_cu;
+  *waves = cus * std::min(per_cu, kSkWavesPerCu);
   return LNSKV_OK;
+}
+
+template <int REP, bool FUSED>
+void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, hipStream_t st) {
+  decode_sk_kernel<REP, FUSED, kSkDepth><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+  combine_sk_kernel<REP, FUSED><<<dim3((unsigned)a.n_kv, (unsigned)n_seq), kBlock, 0, st>>>(a, n_seq, n_waves);
 }
 }  // namespace
 
 int mfma_sk_waves(int rep, bool fused, int* waves) {
-  // resident single-wave blocks of the kernel on the current device, kept per
+  // resident waves used per launch on the current device, kept per
   // (device, rep, fused)
   static std::mutex mu;
   static std::map<std::tuple<int, int, bool>, int> cache;
@@ -756,24 +778,11 @@ int mfma_sk_waves(int rep, bool fused, int* waves) {
 template <bool FUSED>
 int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, hipStream_t st) {
   if (n_seq > kWave) return fail(LNSKV_ERR_INVALID, "stream-K decode serves at most %d sequences", kWave);
-  const dim3 cgrid((unsigned)a.n_kv, (unsigned)n_seq);
   switch (rep) {
-    case 1:
-      decode_sk_kernel<1, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
-      combine_sk_kernel<1, FUSED><<<cgrid, kBlock, 0, st>>>(a, n_seq, n_waves);
-      break;
-    case 2:
-      decode_sk_kernel<2, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
-      combine_sk_kernel<2, FUSED><<<cgrid, kBlock, 0, st>>>(a, n_seq, n_waves);
-      break;
-    case 4:
-      decode_sk_kernel<4, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
-      combine_sk_kernel<4, FUSED><<<cgrid, kBlock, 0, st>>>(a, n_seq, n_waves);
-      break;
-    case 8:
-      decode_sk_kernel<8, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
-      combine_sk_kernel<8, FUSED><<<cgrid, kBlock, 0, st>>>(a, n_seq, n_waves);
-      break;
+    case 1: launch_sk_rep<1, FUSED>(a, n_seq, n_waves, st); break;
+    case 2: launch_sk_rep<2, FUSED>(a, n_seq, n_waves, st); break;
+    case 4: launch_sk_rep<4, FUSED>(a, n_seq, n_waves, st); break;
+    case 8: launch_sk_rep<8, FUSED>(a, n_seq, n_waves, st); break;
     default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
   }
   return hip_check("stream-K decode kernel launch");

@@ -10,7 +10,8 @@ once and then runs, per step:
   3. lnskv_append_decode for the decoding sequences (append 1 token + attend).
 `n_layers` pools of identical geometry let a benchmark cycle through layers so
 consecutive steps do not find the previous step's pages in the 256 MB
-last-level cache.
+last-level cache.  capture() records one layer's step in a HIP graph, as a
+serving loop would replay it, so that replays cost no host-side launch work.
 """
 from __future__ import annotations
 
@@ -89,3 +90,14 @@ class StepRunner:
                              n_heads=w.n_heads, max_kv_len=self.max_kv_len, scale=w.scale, split=w.split,
                              workspace=self.workspace, out=self.out)
         return self.out
+
+    def capture(self, layer: int = 0) -> "torch.cuda.CUDAGraph":
+        """One layer's step recorded in a HIP graph (run it eagerly first, so
+        the library's per-device caches are filled before the capture)."""
+        self.run(layer)
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.run(layer)
+        torch.cuda.synchronize(self.dev)
+        return g
