@@ -114,12 +114,17 @@ int lnskv_append(const lnskv_pages* c, const float* k_new_dev, const float* v_ne
  *   and p_start is kv_p_start, engine.rs:3008-3013).
  *   out = softmax(scale * q.K^T) . V, by online softmax (metal:595-645).
  *   max_kv_len: host upper bound of kv_len over the batch (sizes the grid).
- *   split_tokens: tokens per split-K partition (multiple of 16), 0 = choose.
+ *   split_tokens: tokens per split-K partition (multiple of 16), or 0 to let
+ *   the library schedule: f16 pages with head_dim 128 and at most 64
+ *   sequences then run stream-K (every resident wave of the device takes an
+ *   equal share of all the batch's pages; a second kernel merges the pieces),
+ *   other shapes split-K with a partition size chosen from the batch.
  *   workspace_dev/ws_bytes: device scratch of at least
- *   lnskv_decode_workspace_size(...) bytes, or NULL/0 to use a buffer the
+ *   lnskv_decode_workspace_size(...) bytes (same n_seq, n_heads, max_kv_len
+ *   and split_tokens, same current device), or NULL/0 to use a buffer the
  *   library keeps per device (grown with hipMalloc on demand; calls that use
- *   it must not overlap in time).  The workspace holds the split-K partials
- *   of one call; nothing carries over between calls.  Calls that overlap in
+ *   it must not overlap in time).  The workspace holds the partial results of
+ *   one call; nothing carries over between calls.  Calls that overlap in
  *   time need distinct workspaces.
  * Pages in the window whose table entry is LNSKV_NO_PAGE or >= num_pages are
  * skipped (contribute nothing).  An empty window gives a zero output row.
