@@ -109,6 +109,12 @@ def lib() -> C.CDLL:
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build it with `make -C lns-ml_amd` or "
                 "`python -c 'import __graft_entry__ as g; g.build()'` (no CPU fallback exists)")
+        # torch first: its HIP runtime (soname libamdhip64.so.7, loaded by torch
+        # under the name libamdhip64.so) then satisfies this library's
+        # dependency, so the process has one runtime.  Loaded the other way
+        # round, torch brings a second runtime and ours sees no device.
+        import torch  # noqa: F401
+
         handle = C.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)
