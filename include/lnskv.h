@@ -97,14 +97,17 @@ int lnskv_clear(const lnskv_pages* c, lnskv_stream_t stream);
  * Append: token t's K and V (k_new_dev/v_new_dev [n_tok][n_kv_heads][head_dim],
  * f32) are converted to the page dtype and written to the slot of position
  * tok_pos_dev[t] in sequence tok_seq_dev[t] (row tok_seq_dev[t] of
- * block_tables_dev).  Tokens may straddle pages and any number of sequences.
- * A token whose page entry is LNSKV_NO_PAGE or >= num_pages is not written.
+ * block_tables_dev, which has n_rows rows of bt_stride entries).  Tokens may
+ * straddle pages and any number of sequences.  A token whose sequence is
+ * outside [0, n_rows), whose position is outside [0, 16*bt_stride), or whose
+ * page entry is LNSKV_NO_PAGE or >= num_pages is not written.
  * Replaces the write half of flash_attention_paged_q8a (metal:541-593),
  * performed once per (token, kv head) instead of once per query head.
  * ------------------------------------------------------------------------- */
 int lnskv_append(const lnskv_pages* c, const float* k_new_dev, const float* v_new_dev,
                  const int32_t* tok_seq_dev, const int32_t* tok_pos_dev, int32_t n_tok,
-                 const uint32_t* block_tables_dev, int32_t bt_stride, lnskv_stream_t stream);
+                 const uint32_t* block_tables_dev, int32_t bt_stride, int32_t n_rows,
+                 lnskv_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Single-query paged decode attention over a batch of sequences.
@@ -115,7 +118,7 @@ int lnskv_append(const lnskv_pages* c, const float* k_new_dev, const float* v_ne
  *   out = softmax(scale * q.K^T) . V, by online softmax (metal:595-645).
  *   max_kv_len: host upper bound of kv_len over the batch (sizes the grid).
  *   split_tokens: tokens per split-K partition (multiple of 16), or 0 to let
- *   the library schedule: f16 pages with head_dim 128 and at most 64
+ *   the library schedule: f16 pages with head_dim 128 and at most 4096
  *   sequences then run stream-K (every resident wave of the device takes an
  *   equal share of all the batch's pages; a second kernel merges the pieces),
  *   other shapes split-K with a partition size chosen from the batch.

@@ -571,24 +571,24 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
 // writes the output, the others leave partial rows (slot 0: the wave's first
 // piece, slot 1: its last) that combine_sk_kernel merges.
 
-// Per-lane view of sequence `lane` (lanes past n_seq are empty).
+// Sequences are taken 64 at a time: group g holds sequences 64g .. 64g+63,
+// one per lane.  Per-lane view of sequence 64g + lane (past n_seq: empty).
 struct SkSeq {
   int L;     // length, clamped as seq_window clamps it
   int p0;    // window start
   int lo;    // first position that owns a page of the segment
   int np;    // pages per (sequence, kv head) segment
   int cnt;   // units of the sequence: np * n_kv
-  int incl;  // inclusive prefix sum of cnt over the lanes
+  int incl;  // units of every sequence up to and including this one
 };
 
 template <bool FUSED>
-__device__ __forceinline__ SkSeq sk_seqs(const DecodeArgs& a, int n_seq) {
-  const int lane = (int)(threadIdx.x & (kWave - 1));
+__device__ __forceinline__ SkSeq sk_fields(const DecodeArgs& a, int s, int n_seq) {
   SkSeq q;
   int L = 0, p0 = 0;
-  if (lane < n_seq) {
-    L = a.kv_len ? a.kv_len[lane] : a.kv_len_scalar;
-    p0 = a.p_start ? a.p_start[lane] : a.p_start_scalar;
+  if (s < n_seq) {
+    L = a.kv_len ? a.kv_len[s] : a.kv_len_scalar;
+    p0 = a.p_start ? a.p_start[s] : a.p_start_scalar;
   }
   L = min(max(L, 0), min(a.max_kv_len, a.bt_stride * kPage));
   p0 = min(max(p0, 0), L);
@@ -599,14 +599,57 @@ __device__ __forceinline__ SkSeq sk_seqs(const DecodeArgs& a, int n_seq) {
   q.lo = lo;
   q.np = L > lo ? (L - 1) / kPage - lo / kPage + 1 : 0;
   q.cnt = q.np * a.n_kv;
-  int x = q.cnt;
+  q.incl = 0;
+  return q;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  const int lane = (int)(threadIdx.x & (kWave - 1));
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
     const int y = __shfl_up(x, d, kWave);
     if (lane >= d) x += y;
   }
-  q.incl = x;
+  return x;
+}
+
+// Group g with `base` units before it.
+template <bool FUSED>
+__device__ __forceinline__ SkSeq sk_group(const DecodeArgs& a, int n_seq, int g, int base) {
+  SkSeq q = sk_fields<FUSED>(a, g * kWave + (int)(threadIdx.x & (kWave - 1)), n_seq);
+  q.incl = base + wave_incl_scan(q.cnt);
   return q;
+}
+
+// More than 64 sequences: lane g (< number of groups, at most 64) returns the
+// units before group g; *total gets all units.  Eight groups' lengths are
+// loaded together.
+template <bool FUSED>
+__device__ __forceinline__ int sk_group_bases(const DecodeArgs& a, int n_seq, int* total) {
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  const int G = (n_seq + kWave - 1) / kWave;
+  int mine = 0;
+  for (int g0 = 0; g0 < G; g0 += 8) {
+    int c[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) c[u] = sk_fields<FUSED>(a, (g0 + u) * kWave + lane, n_seq).cnt;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      int t = c[u];
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) t += __shfl_xor(t, o, kWave);
+      if (lane == g0 + u) mine = t;
+    }
+  }
+  const int incl = wave_incl_scan(mine);
+  *total = __builtin_amdgcn_readlane(incl, kWave - 1);
+  return incl - mine;
+}
+
+// The group holding unit cur (cur < total): the last one whose base is <= cur.
+__device__ __forceinline__ int sk_find_group(int gb, int n_groups, int cur) {
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  return (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < n_groups && gb <= cur)) - 1;
 }
 
 __device__ __forceinline__ int sk_chunk(int total, int n_waves) {
@@ -619,20 +662,37 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
   __shared__ __attribute__((aligned(16))) uint8_t vring_[DEPTH * kVSlot];
   __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
   const int wv = blockIdx.x;
-  const SkSeq q = sk_seqs<FUSED>(a, n_seq);
-  const int total = __builtin_amdgcn_readlane(q.incl, kWave - 1);
+  const int n_groups = (n_seq + kWave - 1) / kWave;
+  int total = 0, gb = 0, g = 0;
+  SkSeq q;
+  if (n_groups == 1) {
+    q = sk_group<FUSED>(a, n_seq, 0, 0);
+    total = __builtin_amdgcn_readlane(q.incl, kWave - 1);
+  } else {
+    gb = sk_group_bases<FUSED>(a, n_seq, &total);
+  }
   const int chunk = sk_chunk(total, n_waves);
   int cur = wv * chunk;
   const int end = min(total, cur + chunk);
+  if (n_groups > 1 && cur < end) {
+    g = sk_find_group(gb, n_groups, cur);
+    q = sk_group<FUSED>(a, n_seq, g, __builtin_amdgcn_readlane(gb, g));
+  }
   int slot = 0;
   while (cur < end) {  // wave-uniform
     // the sequence holding unit cur: lanes whose inclusive prefix is <= cur
-    const int s = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(q.incl <= cur));
-    const int np = __builtin_amdgcn_readlane(q.np, s);
-    const int L = __builtin_amdgcn_readlane(q.L, s);
-    const int p0 = __builtin_amdgcn_readlane(q.p0, s);
-    const int pg0 = __builtin_amdgcn_readlane(q.lo, s) / kPage;  // the segment's first page
-    const int sbase = __builtin_amdgcn_readlane(q.incl, s) - __builtin_amdgcn_readlane(q.cnt, s);
+    int si = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(q.incl <= cur));
+    if (si == kWave) {  // cur is past this group (more than 64 sequences only)
+      g = sk_find_group(gb, n_groups, cur);
+      q = sk_group<FUSED>(a, n_seq, g, __builtin_amdgcn_readlane(gb, g));
+      si = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(q.incl <= cur));
+    }
+    const int s = g * kWave + si;
+    const int np = __builtin_amdgcn_readlane(q.np, si);
+    const int L = __builtin_amdgcn_readlane(q.L, si);
+    const int p0 = __builtin_amdgcn_readlane(q.p0, si);
+    const int pg0 = __builtin_amdgcn_readlane(q.lo, si) / kPage;  // the segment's first page
+    const int sbase = __builtin_amdgcn_readlane(q.incl, si) - __builtin_amdgcn_readlane(q.cnt, si);
     const int kvh = (cur - sbase) / np;
     const int seg0 = sbase + kvh * np;
     const int pend = min(end, seg0 + np);
@@ -651,56 +711,31 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
 }
 
 // Merges the pieces of each (sequence, kv head) segment that spans several
-// waves, and writes zeros for empty segments.  Block (kv head, sequence),
-// threads over (head, dim); every wave recomputes the layout.
+// waves, and writes zeros for empty segments.  Block (kv head, sequence, query
+// head of the group); every wave recomputes the layout.
 template <int REP, bool FUSED>
 __global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
-  constexpr int CHUNK = 8;
-  const int kvh = blockIdx.x, s = blockIdx.y;
-  const SkSeq q = sk_seqs<FUSED>(a, n_seq);
-  const int total = __builtin_amdgcn_readlane(q.incl, kWave - 1);
-  const int np = __builtin_amdgcn_readlane(q.np, s);
-  const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP) * kD;
+  const int kvh = blockIdx.x, s = blockIdx.y, h = blockIdx.z;
+  const int n_groups = (n_seq + kWave - 1) / kWave, g = s / kWave, si = s % kWave;
+  int total = 0, base = 0;
+  if (n_groups > 1) base = __builtin_amdgcn_readlane(sk_group_bases<FUSED>(a, n_seq, &total), g);
+  const SkSeq q = sk_group<FUSED>(a, n_seq, g, base);
+  if (n_groups == 1) total = __builtin_amdgcn_readlane(q.incl, kWave - 1);
+  const int np = __builtin_amdgcn_readlane(q.np, si);
+  const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * kD;
   if (np == 0) {
-    for (int idx = threadIdx.x; idx < REP * kD; idx += kBlock) a.out[orow + idx] = 0.0f;
+    for (int i = threadIdx.x; i < kD; i += kBlock) a.out[orow + i] = 0.0f;
     return;
   }
   const int chunk = sk_chunk(total, n_waves);
-  const int seg0 = __builtin_amdgcn_readlane(q.incl, s) - __builtin_amdgcn_readlane(q.cnt, s) + kvh * np;
+  const int seg0 = __builtin_amdgcn_readlane(q.incl, si) - __builtin_amdgcn_readlane(q.cnt, si) + kvh * np;
   const int wa = seg0 / chunk, wb = (seg0 + np - 1) / chunk;
   if (wa == wb) return;  // one piece: the decode kernel wrote the output
-  const int first_slot = seg0 == wa * chunk ? 0 : 1;  // the piece of wave wa is its first unless it starts inside
-  const int nw = wb - wa + 1;
-  for (int idx = threadIdx.x; idx < REP * kD; idx += kBlock) {
-    const int h = idx / kD, i = idx % kD;
-    float M = kMInit, A = 0.0f, Ls = 0.0f;
-    for (int j0 = 0; j0 < nw; j0 += CHUNK) {
-      float2 pm[CHUNK];
-      float pa[CHUNK];
-#pragma unroll
-      for (int u = 0; u < CHUNK; ++u) {
-        const int j = j0 + u;
-        const size_t pidx = ((size_t)(wa + j) * 2 + (j == 0 ? first_slot : 0)) * REP + h;
-        const bool in = j < nw;
-        pm[u] = in ? reinterpret_cast<const float2*>(a.ws_ml)[pidx] : make_float2(kMInit, 0.0f);
-        pa[u] = in ? a.ws_acc[pidx * kD + i] : 0.0f;
-      }
-      float Mc = M;
-#pragma unroll
-      for (int u = 0; u < CHUNK; ++u) Mc = fmaxf(Mc, pm[u].x);
-      const float r = fast_exp2(M - Mc);
-      A *= r;
-      Ls *= r;
-#pragma unroll
-      for (int u = 0; u < CHUNK; ++u) {
-        const float wj = fast_exp2(pm[u].x - Mc);
-        A = fmaf(wj, pa[u], A);
-        Ls = fmaf(wj, pm[u].y, Ls);
-      }
-      M = Mc;
-    }
-    a.out[orow + idx] = Ls > 0.0f ? A / Ls : 0.0f;
-  }
+  // the piece of wave wa is its first (slot 0) unless the segment starts inside its range
+  const int first_slot = seg0 == wa * chunk ? 0 : 1;
+  merge_partials<kD>(reinterpret_cast<const float2*>(a.ws_ml), a.ws_acc, wb - wa + 1,
+                     [=](int j) { return ((size_t)(wa + j) * 2 + (j == 0 ? first_slot : 0)) * REP + h; },
+                     a.out + orow);
 }
 
 }  // namespace
@@ -743,7 +778,7 @@ int sk_waves_of(int cus, int* waves) {
 template <int REP, bool FUSED>
 void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, hipStream_t st) {
   decode_sk_kernel<REP, FUSED, kSkDepth><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
-  combine_sk_kernel<REP, FUSED><<<dim3((unsigned)a.n_kv, (unsigned)n_seq), kBlock, 0, st>>>(a, n_seq, n_waves);
+  combine_sk_kernel<REP, FUSED><<<dim3((unsigned)a.n_kv, (unsigned)n_seq, REP), kBlock, 0, st>>>(a, n_seq, n_waves);
 }
 }  // namespace
 
@@ -777,7 +812,8 @@ int mfma_sk_waves(int rep, bool fused, int* waves) {
 
 template <bool FUSED>
 int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, hipStream_t st) {
-  if (n_seq > kWave) return fail(LNSKV_ERR_INVALID, "stream-K decode serves at most %d sequences", kWave);
+  if (n_seq > kSkMaxSeqs)
+    return fail(LNSKV_ERR_INVALID, "stream-K decode serves at most %d sequences", kSkMaxSeqs);
   switch (rep) {
     case 1: launch_sk_rep<1, FUSED>(a, n_seq, n_waves, st); break;
     case 2: launch_sk_rep<2, FUSED>(a, n_seq, n_waves, st); break;

@@ -27,6 +27,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Running-max start value, finite like the reference's -1e38 (metal:600) so
 // that an all-masked page leaves alpha = exp2(0) = 1 instead of NaN.
 constexpr float kMInit = -1e30f;
+constexpr int kSkMaxSeqs = kWave * kWave;  // stream-K: 64 groups of 64 sequences
 
 // ---------------------------------------------------------------------------
 // Storage traits: bytes per element.
@@ -210,52 +211,92 @@ __device__ __forceinline__ void finish_block(const DecodeArgs& a, EpilogueLds<RE
   }
 }
 
-// Split-K combine: block (kv head, sequence) merges the partitions of its
-// REP query heads, threads over (head, dim).  One pass with a running max;
-// partials are read CHUNK partitions at a time so their loads overlap.
-template <int REP, int D, bool FUSED>
-__global__ __launch_bounds__(kBlock) void combine_kernel(DecodeArgs a) {
-  constexpr int CHUNK = 8;
-  const int kvh = blockIdx.x, s = blockIdx.y;
-  const SeqWindow w = seq_window<FUSED>(a, s);
-  if (w.nparts <= 1) return;
-  const int np = min(w.nparts, a.max_parts);
-  for (int idx = threadIdx.x; idx < REP * D; idx += kBlock) {
-    const int h = idx / D, i = idx % D;
-    const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + h;
-    const float2* ml = reinterpret_cast<const float2*>(a.ws_ml + hrow * a.max_parts * 2);
-    const float* acc = a.ws_acc + hrow * a.max_parts * D + i;
-    float M = kMInit, A = 0.0f, Ls = 0.0f;
-    for (int j0 = 0; j0 < np; j0 += CHUNK) {
-      float2 pm[CHUNK];
-      float pa[CHUNK];
+// Merges np partial rows (m, l) = ml[row(j)], acc = acc[row(j) * D ...] of
+// one query head into out[D]; one block of kBlock threads.  Wave w takes
+// partials w, w+4, w+8, ..., CHUNK of them per round with all their loads in
+// flight together; lane l holds columns l + 64c.  The four waves' (M, L, A)
+// then merge through LDS with the same log-sum-exp weights.  A head whose
+// partials are all empty (l = 0) gets zeros.
+template <int D, class Row>
+__device__ __forceinline__ void merge_partials(const float2* ml, const float* acc, int np, Row row,
+                                               float* out) {
+  constexpr int CHUNK = 16, C = D / kWave;
+  __shared__ float s_acc[kWavesPerBlock][D];
+  __shared__ float s_m[kWavesPerBlock], s_l[kWavesPerBlock];
+  const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  float M = kMInit, Ls = 0.0f, A[C];
 #pragma unroll
-      for (int u = 0; u < CHUNK; ++u) {
-        const bool in = j0 + u < np;
-        pm[u] = in ? ml[j0 + u] : make_float2(kMInit, 0.0f);
-        pa[u] = in ? acc[(size_t)(j0 + u) * D] : 0.0f;
-      }
-      float Mc = M;
+  for (int c = 0; c < C; ++c) A[c] = 0.0f;
+  for (int j0 = wv; j0 < np; j0 += kWavesPerBlock * CHUNK) {
+    float2 pm[CHUNK];
+    float pa[CHUNK][C];
 #pragma unroll
-      for (int u = 0; u < CHUNK; ++u) Mc = fmaxf(Mc, pm[u].x);
-      const float r = fast_exp2(M - Mc);
-      A *= r;
-      Ls *= r;
+    for (int u = 0; u < CHUNK; ++u) {
+      const int j = j0 + u * kWavesPerBlock;
+      const bool in = j < np;
+      const size_t r = in ? row(j) : 0;
+      pm[u] = in ? ml[r] : make_float2(kMInit, 0.0f);
 #pragma unroll
-      for (int u = 0; u < CHUNK; ++u) {
-        const float wj = fast_exp2(pm[u].x - Mc);
-        A = fmaf(wj, pa[u], A);
-        Ls = fmaf(wj, pm[u].y, Ls);
-      }
-      M = Mc;
+      for (int c = 0; c < C; ++c) pa[u][c] = in ? acc[r * D + c * kWave + lane] : 0.0f;
     }
-    a.out[hrow * D + i] = Ls > 0.0f ? A / Ls : 0.0f;
+    float Mc = M;
+#pragma unroll
+    for (int u = 0; u < CHUNK; ++u) Mc = fmaxf(Mc, pm[u].x);
+    const float r = fast_exp2(M - Mc);
+    Ls *= r;
+#pragma unroll
+    for (int c = 0; c < C; ++c) A[c] *= r;
+#pragma unroll
+    for (int u = 0; u < CHUNK; ++u) {
+      const float wj = fast_exp2(pm[u].x - Mc);
+      Ls = fmaf(wj, pm[u].y, Ls);
+#pragma unroll
+      for (int c = 0; c < C; ++c) A[c] = fmaf(wj, pa[u][c], A[c]);
+    }
+    M = Mc;
+  }
+#pragma unroll
+  for (int c = 0; c < C; ++c) s_acc[wv][c * kWave + lane] = A[c];
+  if (lane == 0) {
+    s_m[wv] = M;
+    s_l[wv] = Ls;
+  }
+  __syncthreads();
+  if (wv != 0) return;
+  float Mt = s_m[0];
+#pragma unroll
+  for (int q = 1; q < kWavesPerBlock; ++q) Mt = fmaxf(Mt, s_m[q]);
+  float wq[kWavesPerBlock], Lt = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kWavesPerBlock; ++q) {
+    wq[q] = fast_exp2(s_m[q] - Mt);
+    Lt = fmaf(wq[q], s_l[q], Lt);
+  }
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    float At = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kWavesPerBlock; ++q) At = fmaf(wq[q], s_acc[q][c * kWave + lane], At);
+    out[c * kWave + lane] = Lt > 0.0f ? At / Lt : 0.0f;
   }
 }
 
 template <int REP, int D, bool FUSED>
+__global__ __launch_bounds__(kBlock) void combine_kernel(DecodeArgs a) {
+  const int kvh = blockIdx.x, s = blockIdx.y, h = blockIdx.z;
+  const SeqWindow w = seq_window<FUSED>(a, s);
+  if (w.nparts <= 1) return;  // block-uniform: the decode kernel wrote the output
+  const int np = min(w.nparts, a.max_parts);
+  const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + h;
+  const size_t base = hrow * a.max_parts;
+  merge_partials<D>(reinterpret_cast<const float2*>(a.ws_ml), a.ws_acc, np,
+                    [base](int j) { return base + (size_t)j; }, a.out + hrow * D);
+}
+
+template <int REP, int D, bool FUSED>
 inline void launch_combine(const DecodeArgs& a, int n_seq, hipStream_t st) {
-  if (a.max_parts > 1) combine_kernel<REP, D, FUSED><<<dim3((unsigned)a.n_kv, (unsigned)n_seq), kBlock, 0, st>>>(a);
+  if (a.max_parts > 1)
+    combine_kernel<REP, D, FUSED><<<dim3((unsigned)a.n_kv, (unsigned)n_seq, REP), kBlock, 0, st>>>(a);
 }
 
 // Launchers (defined in the decode translation units).
@@ -263,7 +304,7 @@ template <int DT, bool FUSED>
 int launch_decode_valu(const DecodeArgs& a, int d, int rep, int n_seq, hipStream_t st);
 template <bool FUSED>
 int launch_decode_mfma_f16_d128(const DecodeArgs& a, int rep, int n_seq, hipStream_t st);
-// Stream-K schedule of the MFMA kernel (n_seq <= 64): n_waves single-wave
+// Stream-K schedule of the MFMA kernel (n_seq <= kSkMaxSeqs): n_waves single-wave
 // blocks, workspace of n_waves * 2 * rep partial rows.
 template <bool FUSED>
 int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, hipStream_t st);

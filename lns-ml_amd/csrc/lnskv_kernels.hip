@@ -44,6 +44,7 @@ struct AppendArgs {
   const int32_t* tok_pos;
   const uint32_t* bt;
   int32_t bt_stride;
+  int32_t n_rows;
   int32_t n_tok;
   int32_t n_kv;
   uint32_t num_pages;
@@ -84,7 +85,7 @@ __global__ __launch_bounds__(kBlock) void append_kernel(AppendArgs a) {
   if (item >= (int64_t)a.n_tok * a.n_kv) return;  // wave-uniform
   const int t = (int)(item / a.n_kv), h = (int)(item % a.n_kv);
   const int seq = a.tok_seq[t], pos = a.tok_pos[t];
-  if (seq < 0 || pos < 0 || pos / kPage >= a.bt_stride) return;
+  if (seq < 0 || seq >= a.n_rows || pos < 0 || pos / kPage >= a.bt_stride) return;
   const uint32_t phys = a.bt[(size_t)seq * a.bt_stride + pos / kPage];
   if (phys >= a.num_pages) return;  // LNSKV_NO_PAGE or outside the pool
   const size_t slot = (size_t)phys * kPage + (size_t)(pos % kPage);
@@ -238,8 +239,8 @@ bool mfma_path(int dtype, int d, int rep) {
 
 // How one decode call runs.  Stream-K (one wave per resident slot, each
 // taking an equal share of all pages) when the caller leaves the split to
-// the library, the MFMA kernel serves the pages and there are at most 64
-// sequences; split-K partitions of `split` tokens otherwise.
+// the library, the MFMA kernel serves the pages and there are at most
+// kSkMaxSeqs sequences; split-K partitions of `split` tokens otherwise.
 struct DecodePlan {
   int split = 0;      // split-K: tokens per partition
   int max_parts = 1;  // split-K: partitions of the longest sequence
@@ -252,7 +253,7 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
   const int n_kv = (int)c->n_kv_heads, d = (int)c->head_dim, rep = n_heads / n_kv;
   *p = DecodePlan{};
   const int64_t units = (int64_t)n_seq * n_kv * ((int64_t)max_kv_len / kPage + 1);
-  if (split_tokens == 0 && mfma_path((int)c->dtype, d, rep) && n_seq <= kWave && units < ((int64_t)1 << 30)) {
+  if (split_tokens == 0 && mfma_path((int)c->dtype, d, rep) && n_seq <= kSkMaxSeqs && units < ((int64_t)1 << 30)) {
     // fused < 0: either kind (the workspace query), sized for the larger
     int w0 = 0, w1 = 0;
     if (fused <= 0)
@@ -430,7 +431,7 @@ int lnskv_clear(const lnskv_pages* c, lnskv_stream_t stream) {
 
 int lnskv_append(const lnskv_pages* c, const float* k_new, const float* v_new,
                  const int32_t* tok_seq, const int32_t* tok_pos, int32_t n_tok,
-                 const uint32_t* bt, int32_t bt_stride, lnskv_stream_t stream) {
+                 const uint32_t* bt, int32_t bt_stride, int32_t n_rows, lnskv_stream_t stream) {
   clear_error();
   if (int rc = check_pages(c)) return rc;
   if (n_tok < 0) return fail(LNSKV_ERR_INVALID, "n_tok %d is negative", n_tok);
@@ -438,6 +439,7 @@ int lnskv_append(const lnskv_pages* c, const float* k_new, const float* v_new,
   if (!k_new || !v_new || !tok_seq || !tok_pos || !bt)
     return fail(LNSKV_ERR_INVALID, "append arguments must be non-null");
   if (bt_stride <= 0) return fail(LNSKV_ERR_INVALID, "bt_stride %d must be positive", bt_stride);
+  if (n_rows < 0) return fail(LNSKV_ERR_INVALID, "n_rows %d is negative", n_rows);
   if ((int64_t)n_tok * c->n_kv_heads > (int64_t)1 << 33)
     return fail(LNSKV_ERR_INVALID, "too many tokens (%d)", n_tok);
   AppendArgs a{};
@@ -451,6 +453,7 @@ int lnskv_append(const lnskv_pages* c, const float* k_new, const float* v_new,
   a.tok_pos = tok_pos;
   a.bt = bt;
   a.bt_stride = bt_stride;
+  a.n_rows = n_rows;
   a.n_tok = n_tok;
   a.n_kv = (int32_t)c->n_kv_heads;
   a.num_pages = c->num_pages;

@@ -63,7 +63,7 @@ SIGNATURES = {
     "lnskv_pages_alloc": (C.c_int, [_P]),
     "lnskv_pages_free": (C.c_int, [_P]),
     "lnskv_clear": (C.c_int, [_P, _vp]),
-    "lnskv_append": (C.c_int, [_P, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
+    "lnskv_append": (C.c_int, [_P, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp]),
     "lnskv_decode_workspace_size": (C.c_int, [_P, _i32, _i32, _i32, _i32, C.POINTER(_sz)]),
     "lnskv_decode": (C.c_int, [_P, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _sz, _vp]),
     "lnskv_append_decode": (

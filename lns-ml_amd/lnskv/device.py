@@ -87,12 +87,10 @@ class PagedKV:
         if tables.dim() != 2:
             raise ValueError("block tables must be 2-D")
         _need(tables, "block_tables", tables.dtype, tables.numel(), self.device)
-        n_rows = int(tables.shape[0])
-        if n_tok and (int(tok_seq.min()) < 0 or int(tok_seq.max()) >= n_rows):
-            raise ValueError("tok_seq names a row outside the block tables")
+        # rows outside the table are skipped by the kernel (no host sync here)
         check(lib().lnskv_append(C.byref(self.desc), _ptr(k_new), _ptr(v_new), _ptr(tok_seq),
                                  _ptr(tok_pos), n_tok, _ptr(tables), int(tables.shape[1]),
-                                 _stream(self.device)))
+                                 int(tables.shape[0]), _stream(self.device)))
 
     def workspace_size(self, n_seq: int, n_heads: int, max_kv_len: int, split: int = 0) -> int:
         out = C.c_size_t()

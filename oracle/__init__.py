@@ -61,7 +61,7 @@ def lib() -> C.CDLL:
             "orc_ensure_kv_page": (i32, [vp, vp, C.POINTER(i32), i32, i32]),
             "orc_evict_kv_pages": (None, [vp, vp, i32, i32, i32]),
             "orc_kv_p_start": (i32, [i32, i32]),
-            "orc_append": (i32, [P, vp, vp, vp, vp, i32, vp, i32]),
+            "orc_append": (i32, [P, vp, vp, vp, vp, i32, vp, i32, i32]),
             "orc_gather": (i32, [P, vp, i32, i32, vp, vp, vp, vp]),
             "orc_page_copy": (None, [P, vp, vp, i32]),
             "orc_decode_refscan": (None, [P, vp, vp, vp, i32, vp, vp, i32, i32, C.c_float, i32]),
@@ -153,7 +153,7 @@ def append(pages: HostPages, k_new, v_new, tok_seq, tok_pos, tables) -> int:
     tok_pos = np.ascontiguousarray(tok_pos, np.int32)
     tables = np.ascontiguousarray(tables, np.uint32)
     return lib().orc_append(C.byref(pages.desc), _p(k_new), _p(v_new), _p(tok_seq), _p(tok_pos),
-                            len(tok_seq), _p(tables), tables.shape[1])
+                            len(tok_seq), _p(tables), tables.shape[1], tables.shape[0])
 
 
 def gather(pages: HostPages, bt_row, start: int, n_tok: int):

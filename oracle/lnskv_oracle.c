@@ -234,10 +234,14 @@ static void store_head(const orc_pages* c, int which_v, uint32_t slot, int h, co
  * slot = block_table[write_lp]*16 + write_off); batched over tokens. */
 int orc_append(const orc_pages* c, const float* k_new, const float* v_new,
                const int32_t* tok_seq, const int32_t* tok_pos, int n_tok,
-               const uint32_t* bt, int bt_stride) {
+               const uint32_t* bt, int bt_stride, int n_rows) {
   const int nkv = (int)c->n_kv_heads, d = (int)c->head_dim;
   int skipped = 0;
   for (int t = 0; t < n_tok; ++t) {
+    if (tok_seq[t] < 0 || tok_seq[t] >= n_rows) {
+      skipped++;
+      continue;
+    }
     const uint32_t* row = bt + (size_t)tok_seq[t] * (size_t)bt_stride;
     uint32_t slot;
     if (tok_pos[t] < 0 || tok_pos[t] / ORC_PAGE_SIZE >= bt_stride || slot_of(c, row, tok_pos[t], &slot)) {

@@ -71,10 +71,11 @@ typedef struct {
 
 /* Write token t's K/V ([n_tok][n_kv][d] f32) into slot
  * bt[tok_seq[t]][tok_pos[t]/16]*16 + tok_pos[t]%16.  Returns the number of
- * tokens whose page entry was missing or outside the pool (skipped). */
+ * tokens skipped: sequence outside [0, n_rows), position outside the table
+ * row, or page entry missing or outside the pool. */
 int orc_append(const orc_pages* c, const float* k_new, const float* v_new,
                const int32_t* tok_seq, const int32_t* tok_pos, int n_tok,
-               const uint32_t* bt, int bt_stride);
+               const uint32_t* bt, int bt_stride, int n_rows);
 /* Copy tokens [start, start+n_tok) of one sequence into contiguous
  * [n_tok][n_kv][d] arrays in page dtype (+ [n_tok][n_kv] scales for Q8A). */
 int orc_gather(const orc_pages* c, const uint32_t* bt_row, int start, int n_tok,

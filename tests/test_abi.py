@@ -61,7 +61,7 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     rc, _ = _status(lib.lnskv_decode, C.byref(good), None, 1, 1, 4, 1, None, 1, 32, 16, 0.1, 0, None, 0, None)
     assert rc == _lib.ERR_INVALID
     q8_no_scales = Pages(1, 1, None, None, 64, 4, 64, _lib.DTYPE_Q8A)
-    rc, msg = _status(lib.lnskv_append, C.byref(q8_no_scales), 1, 1, 1, 1, 1, 1, 4, None)
+    rc, msg = _status(lib.lnskv_append, C.byref(q8_no_scales), 1, 1, 1, 1, 1, 1, 4, 1, None)
     assert rc == _lib.ERR_INVALID and "scales" in msg
     rc, msg = _status(lib.lnskv_attention_paged, 1, 1, 1, C.byref(good), 1, 1, 10, 128, 32, 4, 0, None)
     assert rc == _lib.ERR_INVALID and "differ" in msg

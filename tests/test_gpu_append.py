@@ -37,13 +37,14 @@ def test_append_bit_exact(gpu, dtype, d):
     tables = _tables(rng, n_seq, 8, num_pages, [6, 8, 3])
     # seq 0: 41-token chunk from 37 (pages 2..4); seq 1: single token at 127;
     # seq 2: 5 tokens from 14 (straddles pages 0/1); plus a token on a missing page
-    tok_seq = np.array([0] * 41 + [1] + [2] * 5 + [2], np.int32)
-    tok_pos = np.array(list(range(37, 78)) + [127] + list(range(14, 19)) + [100], np.int32)
+    # and two naming rows outside the table (-1 and n_seq), all skipped
+    tok_seq = np.array([0] * 41 + [1] + [2] * 5 + [2, -1, n_seq], np.int32)
+    tok_pos = np.array(list(range(37, 78)) + [127] + list(range(14, 19)) + [100, 5, 5], np.int32)
     n = len(tok_seq)
     k_new = (rng.standard_normal((n, n_kv, d)) * 3).astype(np.float32)
     v_new = (rng.standard_normal((n, n_kv, d)) * 3).astype(np.float32)
     hp, _ = host_pages(pk)
-    assert O.append(hp, k_new, v_new, tok_seq, tok_pos, tables) == 1
+    assert O.append(hp, k_new, v_new, tok_seq, tok_pos, tables) == 3
     pk.append(dev_f32(k_new, gpu), dev_f32(v_new, gpu), dev_i32(tok_seq, gpu), dev_i32(tok_pos, gpu),
               dev_i32(tables, gpu))
     sync()

@@ -274,11 +274,15 @@ def test_stream_k_schedule(gpu, rep):
 
 def test_stream_k_caller_workspace_and_fallback(gpu):
     """A caller-provided workspace of exactly the queried size serves the
-    stream-K schedule; 65 sequences fall back to split-K; one short sequence
-    leaves most waves idle."""
+    stream-K schedule (its size does not depend on the batch up to 4096
+    sequences; 4097 fall back to split-K); 65 sequences take two groups of
+    64; one short sequence leaves most waves idle."""
     say("stream-K workspace / fallback")
     n_kv, d, rep = 8, 128, 4
-    for lens in (_sk_lens(64, 3), _sk_lens(65, 4), (5,), (1,) * 64):
+    pk0 = PagedKV(16, n_kv, d, DTYPE_F16, gpu)
+    sizes = [pk0.workspace_size(n, n_kv * rep, 4096, 0) for n in (1, 64, 4096, 4097)]
+    assert sizes[0] == sizes[1] == sizes[2] != sizes[3], sizes
+    for lens in (_sk_lens(64, 3), _sk_lens(65, 4), (5,), (1,) * 64, (3,) * 4097):
         pk, tables, kv_len, q = _case(gpu, DTYPE_F16, d, rep, n_kv, lens, seed=len(lens))
         hp, _ = host_pages(pk)
         ref = O.decode_f64(hp, q, tables, kv_len, None, 0.0883883)
@@ -289,3 +293,39 @@ def test_stream_k_caller_workspace_and_fallback(gpu):
                         max_kv_len=mkv, scale=0.0883883, split=0, workspace=ws)
         sync()
         assert rel_err(out, ref).max() < TOL[DTYPE_F16], len(lens)
+
+
+@pytest.mark.parametrize("n_seq", [130, 4096])
+def test_stream_k_many_sequences(gpu, n_seq):
+    """More than 64 sequences on the stream-K schedule (groups of 64, one
+    lane per sequence): a whole group of empty sequences, ragged lengths and
+    windows, unfused and fused, against the f64 oracle."""
+    say("stream-K n_seq", n_seq)
+    n_kv, d, rep = 8, 128, 4
+    rng = np.random.default_rng(n_seq)
+    hi = 700 if n_seq < 1000 else 48
+    lens = [int(x) for x in rng.integers(0, hi, n_seq)]
+    lens[64:128] = [0] * 64  # group 1 holds no units
+    lens[0], lens[-1] = hi, 1
+    pk, tables, kv_len, q = _case(gpu, DTYPE_F16, d, rep, n_kv, tuple(lens), seed=n_seq)
+    p_start = np.minimum(rng.integers(0, 40, n_seq), kv_len).astype(np.int32)
+    hp, _ = host_pages(pk)
+    scale = 1.0 / np.sqrt(d)
+    ref = O.decode_f64(hp, q, tables, kv_len, p_start, scale)
+    out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                    max_kv_len=int(kv_len.max()), scale=float(scale), p_start=dev_i32(p_start, gpu), split=0)
+    sync()
+    assert rel_err(out, ref).max() < TOL[DTYPE_F16]
+    assert np.all(out.cpu().numpy()[64:128] == 0.0)
+    kv1 = np.minimum(kv_len + 1, tables.shape[1] * 16).astype(np.int32)
+    k_new = rng.standard_normal((n_seq, n_kv, d)).astype(np.float32)
+    v_new = rng.standard_normal((n_seq, n_kv, d)).astype(np.float32)
+    O.append(hp, k_new, v_new, np.arange(n_seq, dtype=np.int32), kv1 - 1, tables)
+    ref1 = O.decode_f64(hp, q, tables, kv1, p_start, scale)
+    out1 = pk.append_decode(dev_f32(q, gpu), dev_f32(k_new, gpu), dev_f32(v_new, gpu), dev_i32(tables, gpu),
+                            dev_i32(kv1, gpu), n_heads=n_kv * rep, max_kv_len=int(kv1.max()), scale=float(scale),
+                            p_start=dev_i32(p_start, gpu), split=0)
+    sync()
+    got, _ = host_pages(pk)
+    assert np.array_equal(got.k, hp.k) and np.array_equal(got.v, hp.v)
+    assert rel_err(out1, ref1).max() < TOL[DTYPE_F16]

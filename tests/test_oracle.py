@@ -191,6 +191,9 @@ def test_append_skips_missing_pages():
     x = RNG.standard_normal((2, 2, 64)).astype(np.float32)
     assert O.append(hp, x, x, np.zeros(2, np.int32), np.array([3, 17], np.int32), tables) == 2
     assert np.array_equal(hp.k, before.k)
+    tables[0, 0] = 1  # a real page, but the rows named below are outside the table
+    assert O.append(hp, x, x, np.array([-1, 1], np.int32), np.array([3, 3], np.int32), tables) == 2
+    assert np.array_equal(hp.k, before.k)
 
 
 @pytest.mark.parametrize("dtype", [O.F32, O.F16, O.Q8A])
