@@ -122,7 +122,7 @@ int lnskv_append(const lnskv_pages* c, const float* k_new_dev, const float* v_ne
  *   sequences then run stream-K (every resident wave of the device takes an
  *   equal share of all the batch's pages; a second kernel merges the pieces),
  *   other shapes split-K with a partition size chosen from the batch.
- *   workspace_dev/ws_bytes: device scratch of at least
+ *   workspace_dev/ws_bytes: 16-byte aligned device scratch of at least
  *   lnskv_decode_workspace_size(...) bytes (same n_seq, n_heads, max_kv_len
  *   and split_tokens, same current device), or NULL/0 to use a buffer the
  *   library keeps per device (grown with hipMalloc on demand; calls that use

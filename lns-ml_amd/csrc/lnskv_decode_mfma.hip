@@ -679,6 +679,10 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
     q = sk_group<FUSED>(a, n_seq, g, __builtin_amdgcn_readlane(gb, g));
   }
   int slot = 0;
+  // the segment that this wave's first piece closes when it began in an
+  // earlier wave: (sequence, kv head, its first wave, 2 * waves + slot of
+  // that wave's piece); w = 0: none
+  int4 desc = make_int4(0, 0, 0, 0);
   while (cur < end) {  // wave-uniform
     // the sequence holding unit cur: lanes whose inclusive prefix is <= cur
     int si = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(q.incl <= cur));
@@ -697,6 +701,10 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
     const int seg0 = sbase + kvh * np;
     const int pend = min(end, seg0 + np);
     const int i0 = cur - seg0, i1 = pend - seg0;  // pages [i0, i1) of the segment
+    if (slot == 0 && i0 > 0 && i1 == np) {
+      const int wa = seg0 / chunk;
+      desc = make_int4(s, kvh, wa, (wv - wa + 1) * 2 + (seg0 == wa * chunk ? 0 : 1));
+    }
     PieceLoads<REP> pl;
     piece_loads<REP, FUSED>(a, s, kvh, pg0 + i0, pl);
     PieceOut po;
@@ -708,34 +716,33 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
     cur = pend;
     slot = 1;
   }
+  if ((threadIdx.x & (kWave - 1)) == 0) a.sk_desc[wv] = desc;
 }
 
-// Merges the pieces of each (sequence, kv head) segment that spans several
-// waves, and writes zeros for empty segments.  Block (kv head, sequence, query
-// head of the group); every wave recomputes the layout.
+// Block w merges the segment whose last piece is wave w's first piece, when
+// that segment began in an earlier wave (the descriptor the decode kernel
+// left), and writes zeros for the empty windows of sequences w, w + W, ...
+// Wave h of the block merges query heads h, h + 4, ... of the segment.
 template <int REP, bool FUSED>
 __global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
-  const int kvh = blockIdx.x, s = blockIdx.y, h = blockIdx.z;
-  const int n_groups = (n_seq + kWave - 1) / kWave, g = s / kWave, si = s % kWave;
-  int total = 0, base = 0;
-  if (n_groups > 1) base = __builtin_amdgcn_readlane(sk_group_bases<FUSED>(a, n_seq, &total), g);
-  const SkSeq q = sk_group<FUSED>(a, n_seq, g, base);
-  if (n_groups == 1) total = __builtin_amdgcn_readlane(q.incl, kWave - 1);
-  const int np = __builtin_amdgcn_readlane(q.np, si);
-  const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * kD;
-  if (np == 0) {
-    for (int i = threadIdx.x; i < kD; i += kBlock) a.out[orow + i] = 0.0f;
-    return;
+  constexpr int C = kD / kWave;
+  const int w = blockIdx.x, wv = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int4 d = a.sk_desc[w];
+  for (int s = w; s < n_seq; s += n_waves) {  // block-uniform
+    if (sk_fields<FUSED>(a, s, n_seq).np == 0)
+      for (int i = threadIdx.x; i < a.n_heads * kD; i += kBlock) a.out[(size_t)s * a.n_heads * kD + i] = 0.0f;
   }
-  const int chunk = sk_chunk(total, n_waves);
-  const int seg0 = __builtin_amdgcn_readlane(q.incl, si) - __builtin_amdgcn_readlane(q.cnt, si) + kvh * np;
-  const int wa = seg0 / chunk, wb = (seg0 + np - 1) / chunk;
-  if (wa == wb) return;  // one piece: the decode kernel wrote the output
-  // the piece of wave wa is its first (slot 0) unless the segment starts inside its range
-  const int first_slot = seg0 == wa * chunk ? 0 : 1;
-  merge_partials<kD>(reinterpret_cast<const float2*>(a.ws_ml), a.ws_acc, wb - wa + 1,
-                     [=](int j) { return ((size_t)(wa + j) * 2 + (j == 0 ? first_slot : 0)) * REP + h; },
-                     a.out + orow);
+  if (d.w == 0) return;
+  const int s = d.x, kvh = d.y, wa = d.z, nw = d.w >> 1, first_slot = d.w & 1;
+  for (int h = wv; h < REP; h += kWavesPerBlock) {
+    float M, Ls, A[C];
+    merge_wave<kD, 1, 8>(reinterpret_cast<const float2*>(a.ws_ml), a.ws_acc, 0, nw,
+                         [=](int j) { return ((size_t)(wa + j) * 2 + (j == 0 ? first_slot : 0)) * REP + h; },
+                         M, Ls, A);
+    float* out = a.out + ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * kD;
+#pragma unroll
+    for (int c = 0; c < C; ++c) out[c * kWave + lane] = Ls > 0.0f ? A[c] / Ls : 0.0f;
+  }
 }
 
 }  // namespace
@@ -778,7 +785,7 @@ int sk_waves_of(int cus, int* waves) {
 template <int REP, bool FUSED>
 void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, hipStream_t st) {
   decode_sk_kernel<REP, FUSED, kSkDepth><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
-  combine_sk_kernel<REP, FUSED><<<dim3((unsigned)a.n_kv, (unsigned)n_seq, REP), kBlock, 0, st>>>(a, n_seq, n_waves);
+  combine_sk_kernel<REP, FUSED><<<n_waves, kBlock, 0, st>>>(a, n_seq, n_waves);
 }
 }  // namespace
 

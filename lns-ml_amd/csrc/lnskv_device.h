@@ -122,6 +122,7 @@ struct DecodeArgs {
   const int32_t* p_start;
   float* ws_acc;        // [n_seq][n_heads][max_parts][D] partial numerators
   float* ws_ml;         // [n_seq][n_heads][max_parts][2] partial (max, sum)
+  int4* sk_desc;        // stream-K: per wave, the segment its first piece closes
   int32_t kv_len_scalar;   // used when kv_len == nullptr
   int32_t p_start_scalar;  // used when p_start == nullptr
   int32_t bt_stride;
@@ -217,22 +218,23 @@ __device__ __forceinline__ void finish_block(const DecodeArgs& a, EpilogueLds<RE
 // flight together; lane l holds columns l + 64c.  The four waves' (M, L, A)
 // then merge through LDS with the same log-sum-exp weights.  A head whose
 // partials are all empty (l = 0) gets zeros.
-template <int D, class Row>
-__device__ __forceinline__ void merge_partials(const float2* ml, const float* acc, int np, Row row,
-                                               float* out) {
-  constexpr int CHUNK = 16, C = D / kWave;
-  __shared__ float s_acc[kWavesPerBlock][D];
-  __shared__ float s_m[kWavesPerBlock], s_l[kWavesPerBlock];
-  const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
-  float M = kMInit, Ls = 0.0f, A[C];
+// One wave's share: partials first, first + STEP, ... below np, CHUNK per
+// round of loads; lane l accumulates columns l + 64c into (M, Ls, A).
+template <int D, int STEP, int CHUNK, class Row>
+__device__ __forceinline__ void merge_wave(const float2* ml, const float* acc, int first, int np, Row row,
+                                           float& M, float& Ls, float (&A)[D / kWave]) {
+  constexpr int C = D / kWave;
+  const int lane = threadIdx.x % kWave;
+  M = kMInit;
+  Ls = 0.0f;
 #pragma unroll
   for (int c = 0; c < C; ++c) A[c] = 0.0f;
-  for (int j0 = wv; j0 < np; j0 += kWavesPerBlock * CHUNK) {
+  for (int j0 = first; j0 < np; j0 += STEP * CHUNK) {
     float2 pm[CHUNK];
     float pa[CHUNK][C];
 #pragma unroll
     for (int u = 0; u < CHUNK; ++u) {
-      const int j = j0 + u * kWavesPerBlock;
+      const int j = j0 + u * STEP;
       const bool in = j < np;
       const size_t r = in ? row(j) : 0;
       pm[u] = in ? ml[r] : make_float2(kMInit, 0.0f);
@@ -255,6 +257,17 @@ __device__ __forceinline__ void merge_partials(const float2* ml, const float* ac
     }
     M = Mc;
   }
+}
+
+template <int D, class Row>
+__device__ __forceinline__ void merge_partials(const float2* ml, const float* acc, int np, Row row,
+                                               float* out) {
+  constexpr int C = D / kWave;
+  __shared__ float s_acc[kWavesPerBlock][D];
+  __shared__ float s_m[kWavesPerBlock], s_l[kWavesPerBlock];
+  const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  float M, Ls, A[C];
+  merge_wave<D, kWavesPerBlock, 16>(ml, acc, wv, np, row, M, Ls, A);
 #pragma unroll
   for (int c = 0; c < C; ++c) s_acc[wv][c * kWave + lane] = A[c];
   if (lane == 0) {

@@ -261,7 +261,9 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
     if (fused != 0)
       if (int rc = mfma_sk_waves(rep, true, &w1)) return rc;
     p->sk_waves = std::max(w0, w1);
-    p->ws_bytes = (size_t)p->sk_waves * 2 * rep * ((size_t)d + 2) * sizeof(float);
+    // partial rows (acc, then (m, l)) of two pieces per wave, then one
+    // 16-byte descriptor per wave
+    p->ws_bytes = (size_t)p->sk_waves * (2 * rep * ((size_t)d + 2) * sizeof(float) + 16);
     return LNSKV_OK;
   }
   p->split = split_tokens ? split_tokens : choose_split(n_seq, n_kv, max_kv_len);
@@ -332,6 +334,8 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
       if (int rc = library_workspace(need, &ws)) return rc;
     } else if (ws_bytes < need) {
       return fail(LNSKV_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed", ws_bytes, need);
+    } else if (reinterpret_cast<uintptr_t>(ws) % 16 != 0) {
+      return fail(LNSKV_ERR_WORKSPACE, "workspace must be 16-byte aligned");
     }
   }
   DecodeArgs a{};
@@ -363,6 +367,7 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
   if (plan.sk_waves > 0) {
     a.ws_acc = static_cast<float*>(ws);
     a.ws_ml = a.ws_acc + (size_t)plan.sk_waves * 2 * rep * c->head_dim;
+    a.sk_desc = reinterpret_cast<int4*>(a.ws_ml + (size_t)plan.sk_waves * 2 * rep * 2);
     return launch_decode_mfma_sk<FUSED>(a, rep, n_seq, plan.sk_waves, (hipStream_t)stream);
   }
   if (need > 0) {

@@ -11,6 +11,7 @@ import torch
 import oracle as O
 from gpu_util import TOL, dev_f32, dev_i32, fill_pages, host_pages, rel_err, say
 from lnskv import DTYPE_F16, DTYPE_F32, DTYPE_Q8A, DTYPE_NAMES, NO_PAGE
+from lnskv._lib import ERR_WORKSPACE, LnskvError
 from lnskv.device import PagedKV, sync
 
 pytestmark = pytest.mark.gpu
@@ -293,6 +294,15 @@ def test_stream_k_caller_workspace_and_fallback(gpu):
                         max_kv_len=mkv, scale=0.0883883, split=0, workspace=ws)
         sync()
         assert rel_err(out, ref).max() < TOL[DTYPE_F16], len(lens)
+    # a workspace that is large enough but not 16-byte aligned is refused
+    pk, tables, kv_len, q = _case(gpu, DTYPE_F16, d, rep, n_kv, _sk_lens(64, 3), seed=64)
+    mkv = int(kv_len.max())
+    nbytes = pk.workspace_size(64, n_kv * rep, mkv, 0)
+    ws = torch.empty(nbytes + 64, dtype=torch.uint8, device=gpu)[4:]
+    with pytest.raises(LnskvError) as e:
+        pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                  max_kv_len=mkv, scale=0.0883883, split=0, workspace=ws)
+    assert e.value.status == ERR_WORKSPACE
 
 
 @pytest.mark.parametrize("n_seq", [130, 4096])
