@@ -95,6 +95,44 @@ __global__ __launch_bounds__(kBlock) void append_kernel(AppendArgs a) {
   store_head_row<DT, D>(a.v_pages, a.v_scales, row, slot * a.n_kv + h, a.v_new + src, lane);
 }
 
+// Append for f32 and f16 pages: a token's K (and V) values for all its kv
+// heads, n_kv*D of them, are contiguous both in k_new/v_new and in the page
+// slot, so thread i of a token converts elements [8i, 8i+8) of K and of V with
+// 32-byte loads and 16-byte (f16) or 32-byte (f32) stores.  Needs k_new and
+// v_new 16-byte aligned (the host checks; the per-row kernel serves the rest).
+template <int DT>
+__global__ __launch_bounds__(kBlock) void append_vec_kernel(AppendArgs a, int row_elems) {
+  const int per_tok = row_elems / 8;
+  const int64_t gid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t t = gid / per_tok;
+  if (t >= a.n_tok) return;
+  const int e = (int)(gid - t * per_tok) * 8;
+  const int seq = a.tok_seq[t], pos = a.tok_pos[t];
+  if (seq < 0 || seq >= a.n_rows || pos < 0 || pos / kPage >= a.bt_stride) return;
+  const uint32_t phys = a.bt[(size_t)seq * a.bt_stride + pos / kPage];
+  if (phys >= a.num_pages) return;  // LNSKV_NO_PAGE or outside the pool
+  const size_t dst = ((size_t)phys * kPage + (size_t)(pos % kPage)) * row_elems + e;
+  const size_t src = (size_t)t * row_elems + e;
+  const float4 k0 = *reinterpret_cast<const float4*>(a.k_new + src);
+  const float4 k1 = *reinterpret_cast<const float4*>(a.k_new + src + 4);
+  const float4 v0 = *reinterpret_cast<const float4*>(a.v_new + src);
+  const float4 v1 = *reinterpret_cast<const float4*>(a.v_new + src + 4);
+  if constexpr (DT == LNSKV_DTYPE_F32) {
+    float4* kd = reinterpret_cast<float4*>(reinterpret_cast<float*>(a.k_pages) + dst);
+    float4* vd = reinterpret_cast<float4*>(reinterpret_cast<float*>(a.v_pages) + dst);
+    kd[0] = k0;
+    kd[1] = k1;
+    vd[0] = v0;
+    vd[1] = v1;
+  } else {
+    auto pack = [](float lo, float hi) { return to_f16_bits(lo) | (to_f16_bits(hi) << 16); };
+    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(a.k_pages) + dst) =
+        make_uint4(pack(k0.x, k0.y), pack(k0.z, k0.w), pack(k1.x, k1.y), pack(k1.z, k1.w));
+    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(a.v_pages) + dst) =
+        make_uint4(pack(v0.x, v0.y), pack(v0.z, v0.w), pack(v1.x, v1.y), pack(v1.z, v1.w));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Page copy: block (pair, pool) copies one page with 16-byte moves; pool 0/1 =
 // K/V data, 2/3 = K/V scales (Q8A).
@@ -181,6 +219,15 @@ __global__ __launch_bounds__(kBlock) void zero_kernel(uint4* p, size_t n16) {
 // Host-side dispatch.
 template <int DT>
 int launch_append_dt(const AppendArgs& a, int d, hipStream_t st) {
+  if constexpr (DT != LNSKV_DTYPE_Q8A) {
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a.k_new) | reinterpret_cast<uintptr_t>(a.v_new)) & 15) == 0;
+    if (aligned && (d == 64 || d == 128 || d == 256)) {
+      const int row_elems = a.n_kv * d;
+      const int64_t threads = (int64_t)a.n_tok * (row_elems / 8);
+      append_vec_kernel<DT><<<(unsigned)((threads + kBlock - 1) / kBlock), kBlock, 0, st>>>(a, row_elems);
+      return hip_check("append kernel launch");
+    }
+  }
   const unsigned blocks = (unsigned)(((int64_t)a.n_tok * a.n_kv + kWavesPerBlock - 1) / kWavesPerBlock);
   switch (d) {
     case 64: append_kernel<DT, 64><<<blocks, kBlock, 0, st>>>(a); break;
