@@ -113,19 +113,25 @@ def cpu_baseline(w, runner, seconds: float, threads: int):
     kv_len = w.kv_len[rows]
     q = runner.q.cpu().numpy()
     k_new, v_new = runner.k_new.cpu().numpy(), runner.v_new.cpu().numpy()
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        O.append_decode_refscan(hp, q, k_new, v_new, tables, kv_len, None, w.scale, n_threads=threads)
-        n += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = (time.perf_counter() - t0) / n
+    def timed(n_threads: int, budget: float):
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            O.append_decode_refscan(hp, q, k_new, v_new, tables, kv_len, None, w.scale, n_threads=n_threads)
+            n += 1
+            if time.perf_counter() - t0 >= budget:
+                break
+        return (time.perf_counter() - t0) / n, n
+
+    dt, n = timed(threads, seconds)
+    dt1, n1 = timed(1, 0.0) if threads > 1 else (dt, n)  # one whole step on one thread
     return {"value": round(dt * 1e6, 1), "unit": "µs/step", "cores": threads, "kind": "port",
             "sample": f"{n} whole {w.name} steps (append + reference-order f32 scan of all "
                       f"{len(rows)} decoding sequences), {threads} OpenMP threads, "
                       f"{dt * n:.1f} s; nproc={os.cpu_count()}",
-            "gb_per_s": round(w.algorithmic_bytes()["total"] / dt / 1e9, 2)}
+            "gb_per_s": round(w.algorithmic_bytes()["total"] / dt / 1e9, 2),
+            "value_1_thread": round(dt1 * 1e6, 1),
+            "sample_1_thread": f"{n1} whole {w.name} step(s) on 1 thread"}
 
 
 def main():
