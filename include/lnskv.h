@@ -155,6 +155,55 @@ int lnskv_append_decode(const lnskv_pages* c, const float* q_dev, const float* k
                         lnskv_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * RoPE fused into the append.  The reference rotates q and k in place with
+ * rope_with_freqs (lns_decode.metal:154-191; angle_i = pos * inv_freqs[i], the
+ * first rotary_dim elements of a head taken as two halves) just before
+ * encode_attention_paged_q8a (engine.rs:1700-1720).  These entry points take q
+ * and the new K before the rotation and apply it where the values are
+ * converted and stored, so rotated K never goes back to memory as f32.  The
+ * caller's q and k_new buffers are left as they are.
+ * ------------------------------------------------------------------------- */
+typedef enum lnskv_rope_mode {
+  LNSKV_ROPE_DEFAULT = 0,  /* params {scaling_factor} */
+  LNSKV_ROPE_LINEAR = 1,   /* params {factor} */
+  LNSKV_ROPE_LLAMA3 = 2,   /* params {factor, original_max_pos, low_freq_factor, high_freq_factor} */
+  LNSKV_ROPE_YARN = 3      /* params {factor, original_max_pos, beta_fast, beta_slow} */
+} lnskv_rope_mode;
+
+/* Rotary width the engine derives (engine.rs:826-833): round(head_dim *
+ * partial_rotary_factor) when that lies in [2, head_dim), else head_dim. */
+int32_t lnskv_rope_dim(int32_t head_dim, float partial_rotary_factor);
+
+/* Host computation of the rotary_dim/2 inverse frequencies
+ * (compute_rope_inv_freqs, engine.rs:139-195) into inv_freqs_host; upload
+ * them once per model.  rotary_dim even and >= 2. */
+int lnskv_rope_inv_freqs(int32_t rotary_dim, float theta, int32_t mode, const float* params,
+                         float* inv_freqs_host);
+
+typedef struct lnskv_rope {
+  const float* inv_freqs_dev;  /* device, [rotary_dim / 2] f32 */
+  int32_t rotary_dim;          /* even, 2 .. head_dim */
+} lnskv_rope;
+
+/* lnskv_append with K rotated first: token t's K (every kv head) turns by
+ * position tok_pos_dev[t] before it is converted and stored; V is stored as
+ * given. */
+int lnskv_rope_append(const lnskv_pages* c, const lnskv_rope* rope, const float* k_new_dev,
+                      const float* v_new_dev, const int32_t* tok_seq_dev, const int32_t* tok_pos_dev,
+                      int32_t n_tok, const uint32_t* block_tables_dev, int32_t bt_stride, int32_t n_rows,
+                      lnskv_stream_t stream);
+
+/* lnskv_append_decode with q_dev and k_new_dev before the rotation: both turn
+ * by the new token's position kv_len_dev[s]-1, then the token is stored and
+ * attended to as lnskv_append_decode does. */
+int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const float* q_dev,
+                             const float* k_new_dev, const float* v_new_dev, float* out_dev,
+                             const uint32_t* block_tables_dev, int32_t bt_stride,
+                             const int32_t* kv_len_dev, const int32_t* p_start_dev, int32_t n_seq,
+                             int32_t n_heads, int32_t max_kv_len, float scale, int32_t split_tokens,
+                             void* workspace_dev, size_t ws_bytes, lnskv_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * The reference call itself, one sequence: append the token at `pos` (k_in,
  * v_in [n_kv_heads*head_dim] f32) into its page and attend over [p_start, pos]
  * with scale 1/sqrt(head_dim) (metal:539).  Arguments follow

@@ -267,9 +267,11 @@ struct PieceLoads {
   int tbl;
   float4v qv[8];
   float2v knew, vnew;
+  float4v qinv[4];  // RoPE: inverse frequencies of this lane's q pairs
+  float2v kinv;     // RoPE: inverse frequencies of this lane's new-K pair
 };
 
-template <int REP, bool FUSED>
+template <int REP, bool FUSED, bool ROPE>
 __device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh, int tbl, PieceLoads<REP>& pl) {
   const int lane = threadIdx.x;
   const int g = lane >> 4, n = lane & 15;
@@ -295,6 +297,19 @@ __device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh,
     pl.knew = *reinterpret_cast<const float2v*>(a.k_new + src);
     pl.vnew = *reinterpret_cast<const float2v*>(a.v_new + src);
   }
+  if constexpr (ROPE) {
+    // RoPE tables: this lane's q holds elements 8g + 32j + e, and element
+    // i < half pairs with i + half (j and j+2 when half is 64, j = 0 and 1
+    // when it is 32); its new-K pair is elements 2*(lane % half/2) + {0,1}
+    const int i1 = a.rope_half == 64 ? 8 * g + 32 : 8 * g;
+    const float4v* inv = reinterpret_cast<const float4v*>(a.rope_inv);
+    pl.qinv[0] = inv[2 * g];
+    pl.qinv[1] = inv[2 * g + 1];
+    pl.qinv[2] = inv[i1 / 4];
+    pl.qinv[3] = inv[i1 / 4 + 1];
+    const int kl = a.rope_half == 64 ? (lane & 31) : (lane & 15);
+    pl.kinv = reinterpret_cast<const float2v*>(a.rope_inv)[kl];
+  }
 }
 
 // Where a piece's result goes: the normalised output rows, or partial rows
@@ -314,7 +329,7 @@ struct PieceOut {
 // the page data it reads.  `tbl_ok`: pl.btv holds the table window from
 // pl.tbl; the window is reloaded when that is not so or does not cover the
 // piece's first page.
-template <int REP, bool FUSED, int DEPTH>
+template <int REP, bool FUSED, int DEPTH, bool ROPE>
 __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, lds_u8* newtok, PieceLoads<REP>& pl,
                                           bool tbl_ok, int s, int kvh, int ta, int tb, bool append, int pos,
                                           const PieceOut& po) {
@@ -384,6 +399,52 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
   asm volatile(""
                : "+v"(pl.qv[0]), "+v"(pl.qv[1]), "+v"(pl.qv[2]), "+v"(pl.qv[3]), "+v"(pl.qv[4]), "+v"(pl.qv[5]),
                  "+v"(pl.qv[6]), "+v"(pl.qv[7]), "+v"(pl.knew), "+v"(pl.vnew));
+
+  // Fused RoPE: turn q (every piece) and the new K (the appending piece) by
+  // the new token's position before they are used.
+  if constexpr (FUSED && ROPE) {
+    {
+      const float fpos = (float)max(pos, 0);
+      // q pairs: vectors (v0, v1) hold the first halves, (w0, w1) the
+      // partners: (j, j+2) for half 64, (0, 1) for half 32
+      auto turn4 = [&](float4v& x, float4v& y, const float4v& f) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float sn, cs;
+          sincosf(fpos * f[e], &sn, &cs);
+          const float x0 = x[e], x1 = y[e];
+          x[e] = x0 * cs - x1 * sn;
+          y[e] = x0 * sn + x1 * cs;
+        }
+      };
+      if (a.rope_half == 64) {
+        turn4(pl.qv[0], pl.qv[4], pl.qinv[0]);
+        turn4(pl.qv[1], pl.qv[5], pl.qinv[1]);
+        turn4(pl.qv[2], pl.qv[6], pl.qinv[2]);
+        turn4(pl.qv[3], pl.qv[7], pl.qinv[3]);
+      } else {
+        turn4(pl.qv[0], pl.qv[2], pl.qinv[0]);
+        turn4(pl.qv[1], pl.qv[3], pl.qinv[1]);
+      }
+      if (append) {
+        // new K: lane holds elements 2*lane, 2*lane+1; the partner half sits
+        // half/2 lanes away
+        const int mlane = a.rope_half / 2;
+        const bool first = (lane & mlane) == 0;
+        const float p0 = __shfl_xor(pl.knew.x, mlane, kWave);
+        const float p1 = __shfl_xor(pl.knew.y, mlane, kWave);
+        const bool rotated = a.rope_half == 64 || lane < 32;  // half 32: elements 64.. stay
+        if (rotated) {
+          float sn0, cs0, sn1, cs1;
+          sincosf(fpos * pl.kinv.x, &sn0, &cs0);
+          sincosf(fpos * pl.kinv.y, &sn1, &cs1);
+          // first half: x*cos - partner*sin; second half: partner*sin + x*cos
+          pl.knew.x = first ? pl.knew.x * cs0 - p0 * sn0 : p0 * sn0 + pl.knew.x * cs0;
+          pl.knew.y = first ? pl.knew.y * cs1 - p1 * sn1 : p1 * sn1 + pl.knew.y * cs1;
+        }
+      }
+    }
+  }
 
   // Fused append: convert the new token, store it to its page slot, and
   // stage it in LDS for substitution.
@@ -537,7 +598,7 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
 
 // Split-K schedule: block (kv head, partition, sequence) attends one
 // partition of `split` tokens.  Partial rows: [sequence][head][partition].
-template <int REP, bool FUSED>
+template <int REP, bool FUSED, bool ROPE>
 __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
   __shared__ __attribute__((aligned(16))) uint8_t vring_[2 * kVSlot];
@@ -547,7 +608,7 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
   // sliding window), so that every load of the piece is issued before the
   // sequence's length is known; a wrong guess reloads it.
   PieceLoads<REP> pl;
-  piece_loads<REP, FUSED>(a, s, kvh, part * (a.split / kPage), pl);
+  piece_loads<REP, FUSED, ROPE>(a, s, kvh, part * (a.split / kPage), pl);
   const SeqWindow w = seq_window<FUSED>(a, s);
   if (part >= w.nparts) return;  // wave-uniform
   const int jp = w.jf + part;
@@ -557,7 +618,7 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
   po.final = w.nparts == 1;
   po.pbase = ((size_t)s * a.n_heads + (size_t)kvh * REP) * a.max_parts + part;
   po.pstride = a.max_parts;
-  run_piece<REP, FUSED, 2>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, w.jf == 0, s, kvh, ta, tb,
+  run_piece<REP, FUSED, 2, ROPE>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, w.jf == 0, s, kvh, ta, tb,
                         FUSED && part == w.nparts - 1 && w.L > 0, w.L - 1, po);
 }
 
@@ -656,7 +717,7 @@ __device__ __forceinline__ int sk_chunk(int total, int n_waves) {
   return max(kSkMinPages, (total + n_waves - 1) / n_waves);
 }
 
-template <int REP, bool FUSED, int DEPTH>
+template <int REP, bool FUSED, int DEPTH, bool ROPE>
 __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
   __shared__ __attribute__((aligned(16))) uint8_t vring_[DEPTH * kVSlot];
@@ -706,12 +767,13 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
       desc = make_int4(s, kvh, wa, (wv - wa + 1) * 2 + (seg0 == wa * chunk ? 0 : 1));
     }
     PieceLoads<REP> pl;
-    piece_loads<REP, FUSED>(a, s, kvh, pg0 + i0, pl);
+    piece_loads<REP, FUSED, ROPE>(a, s, kvh, pg0 + i0, pl);
     PieceOut po;
     po.final = i0 == 0 && i1 == np;
     po.pbase = ((size_t)wv * 2 + slot) * REP;
     po.pstride = 1;
-    run_piece<REP, FUSED, DEPTH>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh, max(p0, (pg0 + i0) * kPage),
+    run_piece<REP, FUSED, DEPTH, ROPE>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh,
+                                       max(p0, (pg0 + i0) * kPage),
                           min(L, (pg0 + i1) * kPage), FUSED && i1 == np && L > 0, L - 1, po);
     cur = pend;
     slot = 1;
@@ -747,14 +809,26 @@ __global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_
 
 }  // namespace
 
+namespace {
+// RoPE variants exist for fused calls only (a.rope_half > 0).
+template <int REP, bool FUSED>
+void launch_mfma_rep(const DecodeArgs& a, int n_seq, hipStream_t st) {
+  const dim3 grid((unsigned)a.n_kv, (unsigned)a.max_parts, (unsigned)n_seq);
+  if (FUSED && a.rope_half > 0)
+    decode_mfma_kernel<REP, FUSED, FUSED><<<grid, kWave, 0, st>>>(a);
+  else
+    decode_mfma_kernel<REP, FUSED, false><<<grid, kWave, 0, st>>>(a);
+  launch_combine<REP, kD, FUSED>(a, n_seq, st);
+}
+}  // namespace
+
 template <bool FUSED>
 int launch_decode_mfma_f16_d128(const DecodeArgs& a, int rep, int n_seq, hipStream_t st) {
-  const dim3 grid((unsigned)a.n_kv, (unsigned)a.max_parts, (unsigned)n_seq);
   switch (rep) {
-    case 1: decode_mfma_kernel<1, FUSED><<<grid, kWave, 0, st>>>(a); launch_combine<1, kD, FUSED>(a, n_seq, st); break;
-    case 2: decode_mfma_kernel<2, FUSED><<<grid, kWave, 0, st>>>(a); launch_combine<2, kD, FUSED>(a, n_seq, st); break;
-    case 4: decode_mfma_kernel<4, FUSED><<<grid, kWave, 0, st>>>(a); launch_combine<4, kD, FUSED>(a, n_seq, st); break;
-    case 8: decode_mfma_kernel<8, FUSED><<<grid, kWave, 0, st>>>(a); launch_combine<8, kD, FUSED>(a, n_seq, st); break;
+    case 1: launch_mfma_rep<1, FUSED>(a, n_seq, st); break;
+    case 2: launch_mfma_rep<2, FUSED>(a, n_seq, st); break;
+    case 4: launch_mfma_rep<4, FUSED>(a, n_seq, st); break;
+    case 8: launch_mfma_rep<8, FUSED>(a, n_seq, st); break;
     default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
   }
   return hip_check("decode kernel launch");
@@ -773,18 +847,25 @@ constexpr int kSkWavesPerCu = 4;
 
 template <int REP, bool FUSED>
 int sk_waves_of(int cus, int* waves) {
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, kSkDepth>, kWave, 0) !=
-          hipSuccess ||
-      per_cu <= 0)
+  // the smaller occupancy of the plain and (fused) RoPE variants, so one
+  // wave count serves both
+  int per_cu = 0, per_cu_rope = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, kSkDepth, false>, kWave,
+                                                   0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rope, decode_sk_kernel<REP, FUSED, kSkDepth, FUSED>,
+                                                   kWave, 0) != hipSuccess ||
+      per_cu <= 0 || per_cu_rope <= 0)
     return fail(LNSKV_ERR_HIP, "occupancy query of the stream-K decode kernel failed");
-  *waves = cus * std::min(per_cu, kSkWavesPerCu);
+  *waves = cus * std::min(std::min(per_cu, per_cu_rope), kSkWavesPerCu);
   return LNSKV_OK;
 }
 
 template <int REP, bool FUSED>
 void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, hipStream_t st) {
-  decode_sk_kernel<REP, FUSED, kSkDepth><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+  if (FUSED && a.rope_half > 0)
+    decode_sk_kernel<REP, FUSED, kSkDepth, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+  else
+    decode_sk_kernel<REP, FUSED, kSkDepth, false><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
   combine_sk_kernel<REP, FUSED><<<n_waves, kBlock, 0, st>>>(a, n_seq, n_waves);
 }
 }  // namespace

@@ -123,6 +123,8 @@ struct DecodeArgs {
   float* ws_acc;        // [n_seq][n_heads][max_parts][D] partial numerators
   float* ws_ml;         // [n_seq][n_heads][max_parts][2] partial (max, sum)
   int4* sk_desc;        // stream-K: per wave, the segment its first piece closes
+  const float* rope_inv;  // fused RoPE in the MFMA kernels: inverse frequencies
+  int32_t rope_half;      // fused RoPE: rotary_dim / 2, 32 or 64; 0: none (the kernels without RoPE run)
   int32_t kv_len_scalar;   // used when kv_len == nullptr
   int32_t p_start_scalar;  // used when p_start == nullptr
   int32_t bt_stride;

@@ -12,6 +12,8 @@
 //   clear_kv_cache (tables part)  :2923-2930
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <deque>
@@ -302,6 +304,46 @@ int lnskv_block_tables_upload(const lnskv_block_tables* t, uint32_t* dst_dev, ln
   hipError_t e = hipMemcpyAsync(dst_dev, t->table.data(), bytes, hipMemcpyHostToDevice,
                                 (hipStream_t)stream);
   if (e != hipSuccess) return fail(LNSKV_ERR_HIP, "block table upload: %s", hipGetErrorString(e));
+  return LNSKV_OK;
+}
+
+// RoPE tables (engine.rs:826-833 and 139-195), host only.
+int32_t lnskv_rope_dim(int32_t head_dim, float partial_rotary_factor) {
+  const int32_t rot = (int32_t)std::lround((double)((float)head_dim * partial_rotary_factor));
+  return rot >= 2 && rot < head_dim ? rot : head_dim;
+}
+
+int lnskv_rope_inv_freqs(int32_t rotary_dim, float theta, int32_t mode, const float* params, float* out) {
+  lnskv::clear_error();
+  if (rotary_dim < 2 || rotary_dim % 2 != 0) return fail(LNSKV_ERR_INVALID, "rotary_dim %d must be even and >= 2", rotary_dim);
+  if (!out) return fail(LNSKV_ERR_INVALID, "output is NULL");
+  if (mode < LNSKV_ROPE_DEFAULT || mode > LNSKV_ROPE_YARN) return fail(LNSKV_ERR_INVALID, "rope mode %d", mode);
+  const int n_params = mode == LNSKV_ROPE_DEFAULT || mode == LNSKV_ROPE_LINEAR ? 1 : 4;
+  if (!params) return fail(LNSKV_ERR_INVALID, "rope mode %d needs %d parameters", mode, n_params);
+  const float two_pi = 6.28318530717958647692f;
+  for (int32_t i = 0; i < rotary_dim / 2; ++i) {
+    // f32 throughout, as the reference computes it
+    const float base = std::pow(theta, -(2.0f * (float)i) / (float)rotary_dim);
+    float f = base;
+    if (n_params == 1) {
+      f = base / std::max(params[0], 1.0f);
+    } else {
+      // Llama3 {factor, original_max_pos, low, high}; YaRN {factor, original_max_pos, beta_fast, beta_slow}
+      const float factor = params[0], orig = params[1];
+      const float low = mode == LNSKV_ROPE_LLAMA3 ? params[2] : params[3];
+      const float high = mode == LNSKV_ROPE_LLAMA3 ? params[3] : params[2];
+      const float wavelen = two_pi / base;
+      if (wavelen < orig / high) {
+        f = base;
+      } else if (wavelen > orig / low) {
+        f = base / factor;
+      } else {
+        const float smooth = (orig / wavelen - low) / (high - low);
+        f = base * ((1.0f - smooth) / factor + smooth);
+      }
+    }
+    out[i] = f;
+  }
   return LNSKV_OK;
 }
 

@@ -48,6 +48,9 @@ struct AppendArgs {
   int32_t n_tok;
   int32_t n_kv;
   uint32_t num_pages;
+  const float* rope_inv;  // append_vec_kernel: K turns by tok_pos with these inverse frequencies
+  int32_t rope_half;      // rotary_dim / 2 (a multiple of 8, half/8 a power of two); 0: none
+  int32_t head_dim;
 };
 
 template <int DT, int D>
@@ -113,10 +116,37 @@ __global__ __launch_bounds__(kBlock) void append_vec_kernel(AppendArgs a, int ro
   if (phys >= a.num_pages) return;  // LNSKV_NO_PAGE or outside the pool
   const size_t dst = ((size_t)phys * kPage + (size_t)(pos % kPage)) * row_elems + e;
   const size_t src = (size_t)t * row_elems + e;
-  const float4 k0 = *reinterpret_cast<const float4*>(a.k_new + src);
-  const float4 k1 = *reinterpret_cast<const float4*>(a.k_new + src + 4);
+  float4 k0 = *reinterpret_cast<const float4*>(a.k_new + src);
+  float4 k1 = *reinterpret_cast<const float4*>(a.k_new + src + 4);
   const float4 v0 = *reinterpret_cast<const float4*>(a.v_new + src);
   const float4 v1 = *reinterpret_cast<const float4*>(a.v_new + src + 4);
+  if (a.rope_half > 0) {
+    // RoPE on K: this thread's 8 elements hl..hl+7 of a head lie in one half
+    // of the rotary part (or past it); the partner elements sit half/8
+    // threads away in the same head (heads start at multiples of d/8 >= 2m)
+    const int half = a.rope_half, m = half / 8;
+    const int hl = e % a.head_dim;
+    float x[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    float p[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p[j] = __shfl_xor(x[j], m, kWave);
+    if (hl < 2 * half) {
+      const bool first = hl < half;
+      const int i0 = first ? hl : hl - half;
+      const float4 f0 = *reinterpret_cast<const float4*>(a.rope_inv + i0);
+      const float4 f1 = *reinterpret_cast<const float4*>(a.rope_inv + i0 + 4);
+      const float f[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+      const float fpos = (float)pos;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float sn, cs;
+        sincosf(fpos * f[j], &sn, &cs);
+        x[j] = first ? x[j] * cs - p[j] * sn : p[j] * sn + x[j] * cs;
+      }
+      k0 = make_float4(x[0], x[1], x[2], x[3]);
+      k1 = make_float4(x[4], x[5], x[6], x[7]);
+    }
+  }
   if constexpr (DT == LNSKV_DTYPE_F32) {
     float4* kd = reinterpret_cast<float4*>(reinterpret_cast<float*>(a.k_pages) + dst);
     float4* vd = reinterpret_cast<float4*>(reinterpret_cast<float*>(a.v_pages) + dst);
@@ -206,6 +236,32 @@ __global__ __launch_bounds__(kBlock) void gather_kernel(GatherArgs a) {
       a.ks_out[(size_t)t * a.n_kv + h] = valid ? a.k_scales[slot * a.n_kv + h] : 0.0f;
       a.vs_out[(size_t)t * a.n_kv + h] = valid ? a.v_scales[slot * a.n_kv + h] : 0.0f;
     }
+  }
+}
+
+// RoPE for the shapes the fused kernels do not turn in place:
+// y[r][h][:] = x[r][h][:] with the first 2*half elements of every head turned
+// by row r's position (a decode row: kv_len[r]-1; an append row: tok_pos[r]).
+// Block per row, threads over (head, element).
+__global__ __launch_bounds__(kBlock) void rope_rows_kernel(const float* x, float* y, int heads, int d, int half,
+                                                          const float* inv, const int32_t* kv_len,
+                                                          int32_t kv_len_scalar, const int32_t* tok_pos) {
+  const int r = blockIdx.x;
+  const int pos = tok_pos ? tok_pos[r] : (kv_len ? kv_len[r] : kv_len_scalar) - 1;
+  const float fpos = (float)max(pos, 0);
+  const float* xr = x + (size_t)r * heads * d;
+  float* yr = y + (size_t)r * heads * d;
+  for (int idx = threadIdx.x; idx < heads * d; idx += kBlock) {
+    const int h = idx / d, i = idx % d;
+    float v = xr[idx];
+    if (i < 2 * half) {
+      const int kk = i < half ? i : i - half;
+      float sn, cs;
+      sincosf(fpos * inv[kk], &sn, &cs);
+      const float x0 = xr[h * d + kk], x1 = xr[h * d + kk + half];
+      v = i < half ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
+    }
+    yr[idx] = v;
   }
 }
 
@@ -329,14 +385,14 @@ struct DeviceWorkspace {
   size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::vector<DeviceWorkspace> g_ws;
+std::vector<DeviceWorkspace> g_ws;  // [device * 2 + which]: 0 decode workspace, 1 RoPE rows
 
-int library_workspace(size_t need, void** out) {
+int library_buffer(int which, size_t need, void** out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  if ((int)g_ws.size() <= dev) g_ws.resize((size_t)dev + 1);
-  DeviceWorkspace& w = g_ws[(size_t)dev];
+  if ((int)g_ws.size() <= dev * 2 + which) g_ws.resize((size_t)dev * 2 + 2);
+  DeviceWorkspace& w = g_ws[(size_t)dev * 2 + which];
   if (w.bytes < need) {
     if (w.ptr) {
       // Kernels queued earlier may still use the old buffer.
@@ -355,12 +411,24 @@ int library_workspace(size_t need, void** out) {
   return LNSKV_OK;
 }
 
+int library_workspace(size_t need, void** out) { return library_buffer(0, need, out); }
+
+// Checks a RoPE descriptor against head_dim; half = rotary_dim / 2.
+int check_rope(const lnskv_rope* rope, int d, int* half) {
+  if (!rope || !rope->inv_freqs_dev) return fail(LNSKV_ERR_INVALID, "rope and its inverse frequencies must be non-null");
+  if (rope->rotary_dim < 2 || rope->rotary_dim % 2 != 0 || rope->rotary_dim > d)
+    return fail(LNSKV_ERR_INVALID, "rotary_dim %d must be even and in [2, head_dim %d]", rope->rotary_dim, d);
+  *half = rope->rotary_dim / 2;
+  return LNSKV_OK;
+}
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 template <bool FUSED>
 int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const float* v_new,
                  float* out, const uint32_t* bt, int32_t bt_stride, const int32_t* kv_len,
                  int32_t kv_len_scalar, const int32_t* p_start, int32_t p_start_scalar,
                  int32_t n_seq, int32_t n_heads, int32_t max_kv_len, float scale, int32_t split,
-                 void* ws, size_t ws_bytes, lnskv_stream_t stream) {
+                 void* ws, size_t ws_bytes, lnskv_stream_t stream, const lnskv_rope* rope = nullptr) {
   clear_error();
   if (int rc = check_pages(c)) return rc;
   if (!q || !out || !bt) return fail(LNSKV_ERR_INVALID, "q, out and block tables must be non-null");
@@ -373,6 +441,33 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(LNSKV_ERR_INVALID, "scale must be positive and finite");
   if (split < 0) return fail(LNSKV_ERR_INVALID, "split_tokens %d is negative", split);
   const int rep = n_heads / (int)c->n_kv_heads;
+  const int d = (int)c->head_dim;
+  // RoPE: turned inside the MFMA kernels for rotary widths 64 and 128 of
+  // 128-wide heads; otherwise q and k_new are turned into a library buffer
+  // first and that is what the decode reads
+  int rope_half = 0;
+  if (rope) {
+    if (!FUSED) return fail(LNSKV_ERR_INVALID, "RoPE needs the fused append");
+    if (int rc = check_rope(rope, d, &rope_half)) return rc;
+    const bool in_kernel = mfma_path((int)c->dtype, d, rep) && d == 128 && (rope_half == 32 || rope_half == 64) &&
+                           aligned16(rope->inv_freqs_dev);
+    if (!in_kernel) {
+      const size_t qn = (size_t)n_seq * n_heads * d, kn = (size_t)n_seq * c->n_kv_heads * d;
+      void* buf = nullptr;
+      if (int rc = library_buffer(1, (qn + kn) * sizeof(float), &buf)) return rc;
+      float* qr = static_cast<float*>(buf);
+      float* kr = qr + qn;
+      const hipStream_t st = (hipStream_t)stream;
+      rope_rows_kernel<<<(unsigned)n_seq, kBlock, 0, st>>>(q, qr, n_heads, d, rope_half, rope->inv_freqs_dev, kv_len,
+                                                          kv_len_scalar, nullptr);
+      rope_rows_kernel<<<(unsigned)n_seq, kBlock, 0, st>>>(k_new, kr, (int)c->n_kv_heads, d, rope_half,
+                                                          rope->inv_freqs_dev, kv_len, kv_len_scalar, nullptr);
+      if (int rc = hip_check("rope kernel launch")) return rc;
+      q = qr;
+      k_new = kr;
+      rope_half = 0;
+    }
+  }
   DecodePlan plan;
   if (int rc = plan_decode(c, n_seq, n_heads, max_kv_len, split, FUSED ? 1 : 0, &plan)) return rc;
   const size_t need = plan.ws_bytes;
@@ -411,6 +506,8 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
   a.max_kv_len = max_kv_len;
   a.num_pages = c->num_pages;
   a.scale_log2 = scale * kLog2e;
+  a.rope_half = rope_half;
+  a.rope_inv = rope_half > 0 ? rope->inv_freqs_dev : nullptr;
   if (plan.sk_waves > 0) {
     a.ws_acc = static_cast<float*>(ws);
     a.ws_ml = a.ws_acc + (size_t)plan.sk_waves * 2 * rep * c->head_dim;
@@ -481,9 +578,11 @@ int lnskv_clear(const lnskv_pages* c, lnskv_stream_t stream) {
   return hip_check("clear kernel launch");
 }
 
-int lnskv_append(const lnskv_pages* c, const float* k_new, const float* v_new,
-                 const int32_t* tok_seq, const int32_t* tok_pos, int32_t n_tok,
-                 const uint32_t* bt, int32_t bt_stride, int32_t n_rows, lnskv_stream_t stream) {
+namespace lnskv {
+namespace {
+int append_entry(const lnskv_pages* c, const lnskv_rope* rope, const float* k_new, const float* v_new,
+                 const int32_t* tok_seq, const int32_t* tok_pos, int32_t n_tok, const uint32_t* bt,
+                 int32_t bt_stride, int32_t n_rows, lnskv_stream_t stream) {
   clear_error();
   if (int rc = check_pages(c)) return rc;
   if (n_tok < 0) return fail(LNSKV_ERR_INVALID, "n_tok %d is negative", n_tok);
@@ -509,12 +608,54 @@ int lnskv_append(const lnskv_pages* c, const float* k_new, const float* v_new,
   a.n_tok = n_tok;
   a.n_kv = (int32_t)c->n_kv_heads;
   a.num_pages = c->num_pages;
+  a.head_dim = (int32_t)c->head_dim;
+  const int d = (int)c->head_dim;
   const hipStream_t st = (hipStream_t)stream;
-  switch (c->dtype) {
-    case LNSKV_DTYPE_F32: return launch_append_dt<LNSKV_DTYPE_F32>(a, (int)c->head_dim, st);
-    case LNSKV_DTYPE_F16: return launch_append_dt<LNSKV_DTYPE_F16>(a, (int)c->head_dim, st);
-    default: return launch_append_dt<LNSKV_DTYPE_Q8A>(a, (int)c->head_dim, st);
+  if (rope) {
+    // turned in the vector kernel when its lanes can pair up (half a multiple
+    // of 8 with half/8 a power of two); otherwise K goes through a library
+    // buffer first
+    int half = 0;
+    if (int rc = check_rope(rope, d, &half)) return rc;
+    const int m = half / 8;
+    const bool in_kernel = c->dtype != LNSKV_DTYPE_Q8A && (d == 64 || d == 128 || d == 256) && half % 8 == 0 &&
+                           (m & (m - 1)) == 0 && aligned16(k_new) && aligned16(v_new) &&
+                           aligned16(rope->inv_freqs_dev);
+    if (in_kernel) {
+      a.rope_inv = rope->inv_freqs_dev;
+      a.rope_half = half;
+    } else {
+      void* buf = nullptr;
+      if (int rc = library_buffer(1, (size_t)n_tok * c->n_kv_heads * d * sizeof(float), &buf)) return rc;
+      rope_rows_kernel<<<(unsigned)n_tok, kBlock, 0, st>>>(k_new, static_cast<float*>(buf), (int)c->n_kv_heads, d,
+                                                          half, rope->inv_freqs_dev, nullptr, 0, tok_pos);
+      if (int rc = hip_check("rope kernel launch")) return rc;
+      a.k_new = static_cast<const float*>(buf);
+    }
   }
+  switch (c->dtype) {
+    case LNSKV_DTYPE_F32: return launch_append_dt<LNSKV_DTYPE_F32>(a, d, st);
+    case LNSKV_DTYPE_F16: return launch_append_dt<LNSKV_DTYPE_F16>(a, d, st);
+    default: return launch_append_dt<LNSKV_DTYPE_Q8A>(a, d, st);
+  }
+}
+}  // namespace
+}  // namespace lnskv
+
+int lnskv_append(const lnskv_pages* c, const float* k_new, const float* v_new,
+                 const int32_t* tok_seq, const int32_t* tok_pos, int32_t n_tok,
+                 const uint32_t* bt, int32_t bt_stride, int32_t n_rows, lnskv_stream_t stream) {
+  return append_entry(c, nullptr, k_new, v_new, tok_seq, tok_pos, n_tok, bt, bt_stride, n_rows, stream);
+}
+
+int lnskv_rope_append(const lnskv_pages* c, const lnskv_rope* rope, const float* k_new, const float* v_new,
+                      const int32_t* tok_seq, const int32_t* tok_pos, int32_t n_tok, const uint32_t* bt,
+                      int32_t bt_stride, int32_t n_rows, lnskv_stream_t stream) {
+  if (!rope) {
+    clear_error();
+    return fail(LNSKV_ERR_INVALID, "rope must be non-null");
+  }
+  return append_entry(c, rope, k_new, v_new, tok_seq, tok_pos, n_tok, bt, bt_stride, n_rows, stream);
 }
 
 int lnskv_decode_workspace_size(const lnskv_pages* c, int32_t n_seq, int32_t n_heads,
@@ -548,6 +689,18 @@ int lnskv_append_decode(const lnskv_pages* c, const float* q, const float* k_new
   if (!kv_len) return fail(LNSKV_ERR_INVALID, "kv_len must be non-null");
   return decode_entry<true>(c, q, k_new, v_new, out, bt, bt_stride, kv_len, 0, p_start, 0, n_seq,
                             n_heads, max_kv_len, scale, split_tokens, ws, ws_bytes, stream);
+}
+
+int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const float* q, const float* k_new,
+                             const float* v_new, float* out, const uint32_t* bt, int32_t bt_stride,
+                             const int32_t* kv_len, const int32_t* p_start, int32_t n_seq, int32_t n_heads,
+                             int32_t max_kv_len, float scale, int32_t split_tokens, void* ws, size_t ws_bytes,
+                             lnskv_stream_t stream) {
+  clear_error();
+  if (!kv_len) return fail(LNSKV_ERR_INVALID, "kv_len must be non-null");
+  if (!rope) return fail(LNSKV_ERR_INVALID, "rope must be non-null");
+  return decode_entry<true>(c, q, k_new, v_new, out, bt, bt_stride, kv_len, 0, p_start, 0, n_seq,
+                            n_heads, max_kv_len, scale, split_tokens, ws, ws_bytes, stream, rope);
 }
 
 int lnskv_attention_paged(const float* q, const float* k_in, const float* v_in, const lnskv_pages* c,

@@ -52,7 +52,14 @@ class Pages(C.Structure):
     ]
 
 
+class Rope(C.Structure):
+    """lnskv_rope: device inverse frequencies + rotary width."""
+
+    _fields_ = [("inv_freqs_dev", C.c_void_p), ("rotary_dim", C.c_int32)]
+
+
 _P = C.POINTER(Pages)
+_R = C.POINTER(Rope)
 _vp, _i32, _u32, _sz, _f32 = C.c_void_p, C.c_int32, C.c_uint32, C.c_size_t, C.c_float
 
 # name -> (restype, argtypes); every symbol include/lnskv.h declares.
@@ -96,7 +103,14 @@ SIGNATURES = {
     "lnskv_fork_sequence": (
         C.c_int, [_vp, _vp, _i32, _i32, _i32, C.POINTER(_u32), C.POINTER(_u32), C.POINTER(_i32)]),
     "lnskv_block_tables_upload": (C.c_int, [_vp, _vp, _vp]),
+    "lnskv_rope_dim": (_i32, [_i32, _f32]),
+    "lnskv_rope_inv_freqs": (C.c_int, [_i32, _f32, _i32, _vp, _vp]),
+    "lnskv_rope_append": (C.c_int, [_P, _R, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp]),
+    "lnskv_rope_append_decode": (
+        C.c_int, [_P, _R, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _sz, _vp]),
 }
+
+ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3, ROPE_YARN = 0, 1, 2, 3
 
 _lib = None
 

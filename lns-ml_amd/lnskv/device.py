@@ -11,7 +11,7 @@ import ctypes as C
 
 import torch
 
-from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q8A, PAGE_SIZE, Pages, check, lib)
+from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q8A, PAGE_SIZE, Pages, Rope, check, lib)
 
 TORCH_DTYPE = {DTYPE_F32: torch.float32, DTYPE_F16: torch.float16, DTYPE_Q8A: torch.int8}
 
@@ -135,6 +135,37 @@ class PagedKV:
                                         _stream(self.device)))
         return out
 
+    def rope_append(self, rope: "RopeTable", k_new, v_new, tok_seq, tok_pos, tables) -> None:
+        """lnskv_rope_append: lnskv_append with K turned by tok_pos first."""
+        n_tok = int(tok_seq.numel())
+        _need(k_new, "k_new", torch.float32, n_tok * self.row_elems, self.device)
+        _need(v_new, "v_new", torch.float32, n_tok * self.row_elems, self.device)
+        _need(tok_seq, "tok_seq", torch.int32, n_tok, self.device)
+        _need(tok_pos, "tok_pos", torch.int32, n_tok, self.device)
+        if tables.dim() != 2:
+            raise ValueError("block tables must be 2-D")
+        check(lib().lnskv_rope_append(C.byref(self.desc), C.byref(rope.desc), _ptr(k_new), _ptr(v_new),
+                                      _ptr(tok_seq), _ptr(tok_pos), n_tok, _ptr(tables), int(tables.shape[1]),
+                                      int(tables.shape[0]), _stream(self.device)))
+
+    def rope_append_decode(self, rope: "RopeTable", q, k_new, v_new, tables, kv_len, *, n_heads: int,
+                           max_kv_len: int, scale: float, p_start=None, split: int = 0, workspace=None,
+                           out=None) -> torch.Tensor:
+        """lnskv_rope_append_decode: q and k_new before RoPE; both turn by the
+        new token's position kv_len-1, then append + decode."""
+        n_seq, stride = self._decode_common(q, tables, kv_len, p_start, n_heads)
+        _need(k_new, "k_new", torch.float32, n_seq * self.row_elems, self.device)
+        _need(v_new, "v_new", torch.float32, n_seq * self.row_elems, self.device)
+        if out is None:
+            out = torch.empty((n_seq, n_heads, self.head_dim), dtype=torch.float32, device=self.device)
+        _need(out, "out", torch.float32, n_seq * n_heads * self.head_dim, self.device)
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(lib().lnskv_rope_append_decode(C.byref(self.desc), C.byref(rope.desc), _ptr(q), _ptr(k_new),
+                                             _ptr(v_new), _ptr(out), _ptr(tables), stride, _ptr(kv_len),
+                                             _ptr(p_start), n_seq, n_heads, max_kv_len, scale, split,
+                                             _ptr(workspace), ws_bytes, _stream(self.device)))
+        return out
+
     def attention_paged(self, q, k_in, v_in, block_table, pos: int, n_heads: int, p_start: int = 0,
                         out=None, dispatch: bool = False) -> torch.Tensor:
         """The reference's single-sequence call (encode_attention_paged_q8a,
@@ -175,6 +206,24 @@ class PagedKV:
         check(lib().lnskv_gather(C.byref(self.desc), _ptr(block_table_row), start, n_tok, _ptr(ko), _ptr(vo),
                                  _ptr(kso), _ptr(vso), _stream(self.device)))
         return ko, vo, kso, vso
+
+
+class RopeTable:
+    """The model's RoPE table on the device: inverse frequencies from
+    lnskv_rope_inv_freqs (compute_rope_inv_freqs, engine.rs:139-195)."""
+
+    def __init__(self, rotary_dim: int, theta: float, mode: int = 0, params=(1.0,), device="cuda"):
+        import numpy as np
+
+        p = np.zeros(4, np.float32)
+        p[:len(params)] = params
+        host = np.zeros(rotary_dim // 2, np.float32)
+        check(lib().lnskv_rope_inv_freqs(rotary_dim, theta, mode, p.ctypes.data_as(C.c_void_p),
+                                         host.ctypes.data_as(C.c_void_p)))
+        self.rotary_dim = rotary_dim
+        self.inv_freqs_host = host
+        self.inv_freqs = torch.from_numpy(host).to(device)
+        self.desc = Rope(self.inv_freqs.data_ptr(), rotary_dim)
 
 
 def sync(device=None) -> None:

@@ -69,6 +69,8 @@ def lib() -> C.CDLL:
             "orc_decode_split_f64": (None, [P, vp, vp, vp, i32, vp, vp, i32, i32, C.c_double, i32]),
             "orc_append_decode_refscan": (None, [P, vp, vp, vp, vp, vp, i32, vp, vp, i32, i32, C.c_float, i32]),
             "orc_max_threads": (i32, []),
+            "orc_rope_inv_freqs": (None, [i32, C.c_float, i32, vp, vp]),
+            "orc_rope_apply": (None, [vp, i32, i32, i32, i32, vp, i32, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -274,3 +276,27 @@ class Pool:
     @property
     def num_free(self) -> int:
         return lib().orc_pool_num_free(self.h)
+
+
+ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3, ROPE_YARN = 0, 1, 2, 3
+
+
+def rope_inv_freqs(rotary_dim: int, theta: float, mode: int = ROPE_DEFAULT, params=(1.0,)) -> np.ndarray:
+    """compute_rope_inv_freqs (engine.rs:139-195): float32[rotary_dim // 2]."""
+    p = np.zeros(4, np.float32)
+    p[:len(params)] = params
+    out = np.zeros(rotary_dim // 2, np.float32)
+    lib().orc_rope_inv_freqs(rotary_dim, theta, mode, _p(p), _p(out))
+    return out
+
+
+def rope_apply(x, rotary_dim: int, inv_freqs, pos) -> np.ndarray:
+    """apply_cpu_rope_with_freqs (engine.rs:200-229) on a copy of x
+    [rows][heads][head_dim] (float32); row r rotated by position pos[r]."""
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    rows, heads, d = y.shape
+    inv = np.ascontiguousarray(inv_freqs, np.float32)
+    p = np.ascontiguousarray(pos, np.int32)
+    assert p.shape == (rows,)
+    lib().orc_rope_apply(_p(y), rows, heads, d, rotary_dim, _p(inv), len(inv), _p(p))
+    return y

@@ -521,3 +521,58 @@ int orc_max_threads(void) {
   return 1;
 #endif
 }
+
+/* ---- RoPE ------------------------------------------------------------------
+ * compute_rope_inv_freqs, engine.rs:139-195: base_i = theta^(-2i/rotary_dim),
+ * then the scaling mode's adjustment of each frequency. */
+void orc_rope_inv_freqs(int rotary_dim, float theta, int mode, const float* params, float* out) {
+  const int half = rotary_dim / 2;
+  const float tau = 6.28318530717958647692f;
+  for (int i = 0; i < half; ++i) {
+    const float base = powf(theta, -(2.0f * (float)i) / (float)rotary_dim);
+    float f = base;
+    if (mode == ORC_ROPE_DEFAULT || mode == ORC_ROPE_LINEAR) {
+      f = base / fmaxf(params[0], 1.0f);
+    } else {  /* LLAMA3 {factor, original_max_pos, low, high}; YARN {factor, original_max_pos, beta_fast, beta_slow} */
+      const float factor = params[0], omp = params[1];
+      const float lo = mode == ORC_ROPE_LLAMA3 ? params[2] : params[3];  /* low_freq_factor / beta_slow */
+      const float hi = mode == ORC_ROPE_LLAMA3 ? params[3] : params[2];  /* high_freq_factor / beta_fast */
+      const float wavelen = tau / base;
+      const float low_w = omp / lo, high_w = omp / hi;
+      if (wavelen < high_w) {
+        f = base;
+      } else if (wavelen > low_w) {
+        f = base / factor;
+      } else {
+        const float smooth = (omp / wavelen - lo) / (hi - lo);
+        f = base * ((1.0f - smooth) / factor + smooth);
+      }
+    }
+    out[i] = f;
+  }
+}
+
+/* apply_cpu_rope_with_freqs, engine.rs:200-229 (the same rotation as the
+ * rope_with_freqs kernel, lns_decode.metal:158-191): the first rotary_dim
+ * elements of a head are two halves (x0 = first[i], x1 = second[i]) rotated
+ * by angle pos * inv_freqs[i]; the rest of the head is untouched. */
+void orc_rope_apply(float* x, int n_rows, int heads, int head_dim, int rotary_dim, const float* inv_freqs,
+                    int n_inv, const int32_t* pos) {
+  int rd = rotary_dim < head_dim ? rotary_dim : head_dim;
+  if (rd < 2) rd = 2;
+  rd &= ~1;
+  const int half = rd / 2;
+  const int n = half < n_inv ? half : n_inv;
+  for (int r = 0; r < n_rows; ++r) {
+    for (int h = 0; h < heads; ++h) {
+      float* v = x + ((size_t)r * heads + h) * head_dim;
+      for (int i = 0; i < n; ++i) {
+        const float angle = (float)pos[r] * inv_freqs[i];
+        const float sn = sinf(angle), cs = cosf(angle);
+        const float x0 = v[i], x1 = v[half + i];
+        v[i] = x0 * cs - x1 * sn;
+        v[half + i] = x0 * sn + x1 * cs;
+      }
+    }
+  }
+}

@@ -110,6 +110,18 @@ void orc_append_decode_refscan(const orc_pages* c, const float* q, const float* 
                                int n_seq, int n_heads, float scale, int n_threads);
 int orc_max_threads(void);
 
+/* ---- RoPE (engine.rs:137-229, lns_decode.metal:154-191) ----------------- */
+enum { ORC_ROPE_DEFAULT = 0, ORC_ROPE_LINEAR = 1, ORC_ROPE_LLAMA3 = 2, ORC_ROPE_YARN = 3 };
+/* compute_rope_inv_freqs (engine.rs:139-195): out[rotary_dim / 2].  params:
+ * DEFAULT {scaling_factor}, LINEAR {factor}, LLAMA3 {factor, original_max_pos,
+ * low_freq_factor, high_freq_factor}, YARN {factor, original_max_pos,
+ * beta_fast, beta_slow}.  f32 arithmetic throughout, as the reference. */
+void orc_rope_inv_freqs(int rotary_dim, float theta, int mode, const float* params, float* out);
+/* apply_cpu_rope_with_freqs (engine.rs:200-229) on x[n_rows][heads][head_dim]
+ * in place; row r is at position pos[r]; angle_i = pos * inv_freqs[i]. */
+void orc_rope_apply(float* x, int n_rows, int heads, int head_dim, int rotary_dim, const float* inv_freqs,
+                    int n_inv, const int32_t* pos);
+
 #ifdef __cplusplus
 }
 #endif
