@@ -52,6 +52,8 @@ def parse():
     p.add_argument("--graph", type=int, default=0,
                    help="1: replay each layer's step from a captured HIP graph (no per-step host launch work); "
                         "0: launch eagerly from Python")
+    p.add_argument("--rope", type=int, default=0,
+                   help="1: the step goes through the fused RoPE entry points (Llama-3.1 table, rotary = head_dim)")
     p.add_argument("--copy-only", action="store_true",
                    help="run only the plain copy (the calibration kernel for HBM byte counters)")
     return p.parse_args()
@@ -157,7 +159,12 @@ def main():
     w = make(args.config)
     if args.split >= 0:
         w.split = args.split
-    runner = StepRunner(w, dev, n_layers=args.layers, seed=1)
+    rope = None
+    if args.rope:
+        from lnskv.device import RopeTable
+
+        rope = RopeTable(w.head_dim, 500000.0, 2, (8.0, 8192.0, 1.0, 4.0), device=dev)
+    runner = StepRunner(w, dev, n_layers=args.layers, seed=1, rope=rope)
     torch.cuda.synchronize()
     nb = w.algorithmic_bytes()
     stream = torch.cuda.current_stream(dev)
@@ -222,6 +229,8 @@ def main():
             "split_tokens": int(w.split),
             "layers_cycled": args.layers,
             "launch": "HIP graph replay per step" if args.graph else "eager launches from Python",
+            "rope": ("fused RoPE (lnskv_rope_append_decode), Llama-3.1 inverse frequencies, rotary = head_dim"
+                     if args.rope else None),
             "algorithmic_bytes_per_step": int(nb["total"]),
             "bytes_breakdown": {k: int(v) for k, v in nb.items() if k != "total"},
             "parallelism": "single GPU",

@@ -48,6 +48,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 #include "lnskv_device.h"
 
 namespace lnskv {
@@ -93,12 +94,21 @@ __device__ __forceinline__ float sum_xor16(float x) {
   return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
 }
 
-// out[h] = x of lane h of this lane's 16-lane row, h < N (DPP row_newbcast).
-template <int N, int H = 0>
-__device__ __forceinline__ void row_broadcast(float x, float (&out)[N]) {
-  if constexpr (H < N) {
-    out[H] = dpp_mov<kDppRowNewBcast + H>(x);
-    row_broadcast<N, H + 1>(x, out);
+// x of lane H of this lane's 16-lane row (DPP row_newbcast).  Per-head
+// values are picked with compile-time lane numbers: a select between two
+// elements of a local array, taken inside a loop, becomes one load at a
+// select of indices and leaves the array in scratch.
+template <int H>
+__device__ __forceinline__ float row_value(float x) {
+  return dpp_mov<kDppRowNewBcast + H>(x);
+}
+
+// f(integral_constant<int, I>) for I = 0..N-1, each with a compile-time I.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
   }
 }
 
@@ -124,20 +134,14 @@ struct WaveState {
 // Multiplies the result rows 4g+ii of this lane by their head's alpha: row r
 // belongs to head r % REP, whose alpha sits in lane (r % REP) of every
 // 16-lane row (all rows agree).
-template <int REP>
+template <int REP, int II = 0>
 __device__ __forceinline__ void scale_rows(WaveState<REP>& st, float alpha, int g) {
-  float ab[REP];
-  row_broadcast<REP>(alpha, ab);
+  if constexpr (II < 4) {
+    float f = row_value<II % REP>(alpha);
+    if constexpr (REP == 8) f = (g & 1) ? row_value<4 + II>(alpha) : f;
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii) {
-    float f;
-    if constexpr (REP <= 4) {
-      f = ab[ii % REP];
-    } else {
-      f = (g & 1) ? ab[4 + ii] : ab[ii];
-    }
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) st.acc[nb][ii] *= f;
+    for (int nb = 0; nb < 8; ++nb) st.acc[nb][II] *= f;
+    scale_rows<REP, II + 1>(st, alpha, g);
   }
 }
 
@@ -267,8 +271,6 @@ struct PieceLoads {
   int tbl;
   float4v qv[8];
   float2v knew, vnew;
-  float4v qinv[4];  // RoPE: inverse frequencies of this lane's q pairs
-  float2v kinv;     // RoPE: inverse frequencies of this lane's new-K pair
 };
 
 template <int REP, bool FUSED, bool ROPE>
@@ -297,18 +299,16 @@ __device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh,
     pl.knew = *reinterpret_cast<const float2v*>(a.k_new + src);
     pl.vnew = *reinterpret_cast<const float2v*>(a.v_new + src);
   }
+}
+
+// RoPE: the wave's copy of the inverse frequencies in LDS (64 floats), read
+// where the rotation needs them so that no table values are held in
+// registers while the pages are in flight.
+template <bool ROPE>
+__device__ __forceinline__ void stage_rope_table(const DecodeArgs& a, lds_u8* table) {
   if constexpr (ROPE) {
-    // RoPE tables: this lane's q holds elements 8g + 32j + e, and element
-    // i < half pairs with i + half (j and j+2 when half is 64, j = 0 and 1
-    // when it is 32); its new-K pair is elements 2*(lane % half/2) + {0,1}
-    const int i1 = a.rope_half == 64 ? 8 * g + 32 : 8 * g;
-    const float4v* inv = reinterpret_cast<const float4v*>(a.rope_inv);
-    pl.qinv[0] = inv[2 * g];
-    pl.qinv[1] = inv[2 * g + 1];
-    pl.qinv[2] = inv[i1 / 4];
-    pl.qinv[3] = inv[i1 / 4 + 1];
-    const int kl = a.rope_half == 64 ? (lane & 31) : (lane & 15);
-    pl.kinv = reinterpret_cast<const float2v*>(a.rope_inv)[kl];
+    const int lane = (int)(threadIdx.x & (kWave - 1));
+    ((__attribute__((address_space(3))) float*)table)[lane] = lane < a.rope_half ? a.rope_inv[lane] : 0.0f;
   }
 }
 
@@ -332,7 +332,7 @@ struct PieceOut {
 template <int REP, bool FUSED, int DEPTH, bool ROPE>
 __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, lds_u8* newtok, PieceLoads<REP>& pl,
                                           bool tbl_ok, int s, int kvh, int ta, int tb, bool append, int pos,
-                                          const PieceOut& po) {
+                                          const PieceOut& po, lds_u8* rope_table = nullptr) {
   const int lane = threadIdx.x;
   const int g = lane >> 4, n = lane & 15;
   const bool qcol = n < 2 * REP;
@@ -405,27 +405,46 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
   if constexpr (FUSED && ROPE) {
     {
       const float fpos = (float)max(pos, 0);
+      // this lane's q holds elements 8g + 32j + e, and element i < half pairs
+      // with i + half (j and j+2 when half is 64, j = 0 and 1 when it is 32)
+      typedef __attribute__((address_space(3))) float4v lds_float4v;
+      const lds_float4v* tq = (const lds_float4v*)rope_table;
+      const int i1 = a.rope_half == 64 ? 8 * g + 32 : 8 * g;
+      float4v qinv[4];
+      qinv[0] = tq[2 * g];
+      qinv[1] = tq[2 * g + 1];
+      qinv[2] = tq[i1 / 4];
+      qinv[3] = tq[i1 / 4 + 1];
       // q pairs: vectors (v0, v1) hold the first halves, (w0, w1) the
       // partners: (j, j+2) for half 64, (0, 1) for half 32
       auto turn4 = [&](float4v& x, float4v& y, const float4v& f) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float sn, cs;
-          sincosf(fpos * f[e], &sn, &cs);
+          rope_sincos(fpos * f[e], &sn, &cs);
           const float x0 = x[e], x1 = y[e];
           x[e] = x0 * cs - x1 * sn;
           y[e] = x0 * sn + x1 * cs;
         }
       };
-      if (a.rope_half == 64) {
-        turn4(pl.qv[0], pl.qv[4], pl.qinv[0]);
-        turn4(pl.qv[1], pl.qv[5], pl.qinv[1]);
-        turn4(pl.qv[2], pl.qv[6], pl.qinv[2]);
-        turn4(pl.qv[3], pl.qv[7], pl.qinv[3]);
-      } else {
-        turn4(pl.qv[0], pl.qv[2], pl.qinv[0]);
-        turn4(pl.qv[1], pl.qv[3], pl.qinv[1]);
-      }
+      // Partners are picked by value, not by array index: a branch on the
+      // rotary width that names different elements of pl.qv gets merged into
+      // a dynamically indexed (scratch) array.  Width 32 turns j = 2, 3 as
+      // well and discards the result.
+      const bool h64 = a.rope_half == 64;
+      float4v y0 = h64 ? pl.qv[4] : pl.qv[2];
+      float4v y1 = h64 ? pl.qv[5] : pl.qv[3];
+      float4v x2 = pl.qv[2], x3 = pl.qv[3], y2 = pl.qv[6], y3 = pl.qv[7];
+      turn4(pl.qv[0], y0, qinv[0]);
+      turn4(pl.qv[1], y1, qinv[1]);
+      turn4(x2, y2, qinv[2]);
+      turn4(x3, y3, qinv[3]);
+      pl.qv[2] = h64 ? x2 : y0;
+      pl.qv[3] = h64 ? x3 : y1;
+      pl.qv[4] = h64 ? y0 : pl.qv[4];
+      pl.qv[5] = h64 ? y1 : pl.qv[5];
+      pl.qv[6] = h64 ? y2 : pl.qv[6];
+      pl.qv[7] = h64 ? y3 : pl.qv[7];
       if (append) {
         // new K: lane holds elements 2*lane, 2*lane+1; the partner half sits
         // half/2 lanes away
@@ -435,9 +454,12 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
         const float p1 = __shfl_xor(pl.knew.y, mlane, kWave);
         const bool rotated = a.rope_half == 64 || lane < 32;  // half 32: elements 64.. stay
         if (rotated) {
+          // its new-K pair is elements 2*(lane % (half/2)) + {0, 1}
+          typedef __attribute__((address_space(3))) float2v lds_float2v;
+          const float2v kinv = ((const lds_float2v*)rope_table)[lane & (mlane - 1)];
           float sn0, cs0, sn1, cs1;
-          sincosf(fpos * pl.kinv.x, &sn0, &cs0);
-          sincosf(fpos * pl.kinv.y, &sn1, &cs1);
+          rope_sincos(fpos * kinv.x, &sn0, &cs0);
+          rope_sincos(fpos * kinv.y, &sn1, &cs1);
           // first half: x*cos - partner*sin; second half: partner*sin + x*cos
           pl.knew.x = first ? pl.knew.x * cs0 - p0 * sn0 : p0 * sn0 + pl.knew.x * cs0;
           pl.knew.y = first ? pl.knew.y * cs1 - p1 * sn1 : p1 * sn1 + pl.knew.y * cs1;
@@ -567,16 +589,20 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
       for (int ii = 0; ii < 4; ++ii) o[ii][nb] = sum_xor32(st.acc[nb][ii]);
     }
   }
-  // l and m of the heads this lane writes (REP == 8: lanes g == 1 hold heads 4..7)
-  float lb[REP];
-  row_broadcast<REP>(st.l, lb);
-  float mb[REP];
-  row_broadcast<REP>(st.m, mb);
+  // l and m of the heads this lane writes (REP == 8: lanes g == 1 hold heads
+  // 4..7), broadcast while every lane is active: DPP reads of inactive lanes
+  // return nothing useful.
+  float lsel[NH], msel[NH];
+  static_for<NH>([&](auto c) {
+    constexpr int ii = decltype(c)::value;
+    lsel[ii] = (REP == 8 && g == 1) ? row_value<(4 + ii) % REP>(st.l) : row_value<ii>(st.l);
+    msel[ii] = (REP == 8 && g == 1) ? row_value<(4 + ii) % REP>(st.m) : row_value<ii>(st.m);
+  });
   if (g == 0 || (REP == 8 && g == 1)) {
     const int hb = REP == 8 ? 4 * g : 0;
-#pragma unroll
-    for (int ii = 0; ii < NH; ++ii) {
-      const float lh = (REP == 8 && g == 1) ? lb[(4 + ii) % REP] : lb[ii];
+    static_for<NH>([&](auto c) {
+      constexpr int ii = decltype(c)::value;
+      const float lh = lsel[ii], mh = msel[ii];
       if (po.final) {
         const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + hb + ii;
         const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
@@ -587,12 +613,11 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) a.ws_acc[pidx * kD + 16 * nb + n] = o[ii][nb];
         if (n == 0) {
-          const float mh = (REP == 8 && g == 1) ? mb[(4 + ii) % REP] : mb[ii];
           a.ws_ml[pidx * 2 + 0] = mh;
           a.ws_ml[pidx * 2 + 1] = lh;
         }
       }
-    }
+    });
   }
 }
 
@@ -608,6 +633,8 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
   // sliding window), so that every load of the piece is issued before the
   // sequence's length is known; a wrong guess reloads it.
   PieceLoads<REP> pl;
+  __shared__ __attribute__((aligned(16))) uint8_t rope_table_[ROPE ? 256 : 16];
+  stage_rope_table<ROPE>(a, (lds_u8*)rope_table_);
   piece_loads<REP, FUSED, ROPE>(a, s, kvh, part * (a.split / kPage), pl);
   const SeqWindow w = seq_window<FUSED>(a, s);
   if (part >= w.nparts) return;  // wave-uniform
@@ -619,7 +646,7 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
   po.pbase = ((size_t)s * a.n_heads + (size_t)kvh * REP) * a.max_parts + part;
   po.pstride = a.max_parts;
   run_piece<REP, FUSED, 2, ROPE>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, w.jf == 0, s, kvh, ta, tb,
-                        FUSED && part == w.nparts - 1 && w.L > 0, w.L - 1, po);
+                        FUSED && part == w.nparts - 1 && w.L > 0, w.L - 1, po, (lds_u8*)rope_table_);
 }
 
 // ---------------------------------------------------------------------------
@@ -722,6 +749,8 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
   __shared__ __attribute__((aligned(16))) uint8_t vring_[DEPTH * kVSlot];
   __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
+  __shared__ __attribute__((aligned(16))) uint8_t rope_table_[ROPE ? 256 : 16];
+  stage_rope_table<ROPE>(a, (lds_u8*)rope_table_);
   const int wv = blockIdx.x;
   const int n_groups = (n_seq + kWave - 1) / kWave;
   int total = 0, gb = 0, g = 0;
@@ -774,7 +803,8 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
     po.pstride = 1;
     run_piece<REP, FUSED, DEPTH, ROPE>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh,
                                        max(p0, (pg0 + i0) * kPage),
-                          min(L, (pg0 + i1) * kPage), FUSED && i1 == np && L > 0, L - 1, po);
+                          min(L, (pg0 + i1) * kPage), FUSED && i1 == np && L > 0, L - 1, po,
+                          (lds_u8*)rope_table_);
     cur = pend;
     slot = 1;
   }

@@ -90,6 +90,19 @@ __device__ __forceinline__ float cross_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// sin and cos of a RoPE angle theta (the f32 product pos * inv_freq, as the
+// reference forms it): the angle is reduced to [0, 1) revolutions in f64
+// (theta/2pi exact to ~1e-16 relative, so even angles of ~1e5 rad keep ~1e-11
+// revolutions of precision), then v_sin_f32 / v_cos_f32, which take
+// revolutions.  Absolute error ~1e-6, against ~1e-3 relative for one f16 ulp.
+__device__ __forceinline__ void rope_sincos(float theta, float* s, float* c) {
+  double r = (double)theta * 0.15915494309189533577;  // 1 / (2 pi)
+  r -= floor(r);
+  const float rf = (float)r;
+  *s = __builtin_amdgcn_sinf(rf);
+  *c = __builtin_amdgcn_cosf(rf);
+}
+
 // Converts one f32 to the page dtype's bits; Q8A needs the head's scale.
 // f16: v_cvt_f16_f32 under the default round-to-nearest-even mode.
 // Q8A: IEEE division (HIP's correctly rounded f32 divide), roundf = half away

@@ -140,7 +140,7 @@ __global__ __launch_bounds__(kBlock) void append_vec_kernel(AppendArgs a, int ro
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         float sn, cs;
-        sincosf(fpos * f[j], &sn, &cs);
+        rope_sincos(fpos * f[j], &sn, &cs);
         x[j] = first ? x[j] * cs - p[j] * sn : p[j] * sn + x[j] * cs;
       }
       k0 = make_float4(x[0], x[1], x[2], x[3]);
@@ -257,7 +257,7 @@ __global__ __launch_bounds__(kBlock) void rope_rows_kernel(const float* x, float
     if (i < 2 * half) {
       const int kk = i < half ? i : i - half;
       float sn, cs;
-      sincosf(fpos * inv[kk], &sn, &cs);
+      rope_sincos(fpos * inv[kk], &sn, &cs);
       const float x0 = xr[h * d + kk], x1 = xr[h * d + kk + half];
       v = i < half ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
     }

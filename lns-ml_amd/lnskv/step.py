@@ -32,8 +32,11 @@ def _i32(a: np.ndarray, dev) -> torch.Tensor:
 
 class StepRunner:
     def __init__(self, w: Workload, device="cuda", n_layers: int = 1, seed: int = 0,
-                 fill: bool = True):
+                 fill: bool = True, rope=None):
+        """rope: a RopeTable to run the step through the fused RoPE entry
+        points (q and the new K/chunk K are then taken before the rotation)."""
         self.w = w
+        self.rope = rope
         self.dev = torch.device(device)
         if self.dev.type == "cuda" and self.dev.index is None:
             self.dev = torch.device("cuda", torch.cuda.current_device())
@@ -84,11 +87,19 @@ class StepRunner:
         if len(w.copies):
             pk.page_copy(self.copy_src, self.copy_dst)
         if self.n_chunk_tok:
-            pk.append(self.chunk_k, self.chunk_v, self.chunk_seq, self.chunk_pos, self.tables)
+            if self.rope is not None:
+                pk.rope_append(self.rope, self.chunk_k, self.chunk_v, self.chunk_seq, self.chunk_pos, self.tables)
+            else:
+                pk.append(self.chunk_k, self.chunk_v, self.chunk_seq, self.chunk_pos, self.tables)
         if self.n_dec:
-            pk.append_decode(self.q, self.k_new, self.v_new, self.dec_tables, self.dec_kv_len,
-                             n_heads=w.n_heads, max_kv_len=self.max_kv_len, scale=w.scale, split=w.split,
-                             workspace=self.workspace, out=self.out)
+            if self.rope is not None:
+                pk.rope_append_decode(self.rope, self.q, self.k_new, self.v_new, self.dec_tables, self.dec_kv_len,
+                                      n_heads=w.n_heads, max_kv_len=self.max_kv_len, scale=w.scale,
+                                      split=w.split, workspace=self.workspace, out=self.out)
+            else:
+                pk.append_decode(self.q, self.k_new, self.v_new, self.dec_tables, self.dec_kv_len,
+                                 n_heads=w.n_heads, max_kv_len=self.max_kv_len, scale=w.scale, split=w.split,
+                                 workspace=self.workspace, out=self.out)
         return self.out
 
     def capture(self, layer: int = 0) -> "torch.cuda.CUDAGraph":
