@@ -54,6 +54,8 @@ def parse():
                         "0: launch eagerly from Python")
     p.add_argument("--rope", type=int, default=0,
                    help="1: the step goes through the fused RoPE entry points (Llama-3.1 table, rotary = head_dim)")
+    p.add_argument("--pattern-reps", type=int, default=40,
+                   help="launches of the load probe over the step's decode pages (0 = skip)")
     p.add_argument("--copy-only", action="store_true",
                    help="run only the plain copy (the calibration kernel for HBM byte counters)")
     return p.parse_args()
@@ -78,6 +80,61 @@ def copy_ceiling(dev, mb: int, reps: int = 20) -> dict:
     torch.cuda.synchronize()
     dt = s.elapsed_time(e) / 1e3 / reps
     return {"bytes_per_copy": 2 * n * 4, "gb_per_s": round(2 * n * 4 / dt / 1e9, 1)}
+
+
+def pattern_ceiling(w, runner, dev, reps: int) -> dict | None:
+    """Load ceiling of the step's decode page pattern, timed live with HIP
+    events: lnskv_read_units over the same (page, kv head) units as the
+    decode, in its order ((sequence, kv head, page)) and its stream-K wave
+    split (CUs x 4 waves), cycling the same layers' pools (no cache reuse
+    between launches).  Bytes per launch: units x 2 pools x 16 rows x 256 B.
+    None for shapes the probe does not read (kv-head rows other than 256 B)."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    from lnskv._lib import check, lib
+
+    if reps <= 0 or runner.n_dec == 0 or w.head_dim * {0: 4, 1: 2, 2: 1}[w.dtype] != 256:
+        return None
+    pages, kvhs = [], []
+    for s in runner.dec_rows:
+        npg = (int(w.kv_len[s]) + 15) // 16  # window from position 0, including the appended token
+        row = np.asarray(w.tables[s][:npg], dtype=np.uint32)
+        for k in range(w.n_kv):
+            pages.append(row)
+            kvhs.append(np.full(npg, k, dtype=np.int32))
+    unit_page = np.concatenate(pages)
+    unit_kvh = np.concatenate(kvhs)
+    n_units = len(unit_page)
+    waves = torch.cuda.get_device_properties(dev).multi_processor_count * 4
+    chunk = max(4, -(-n_units // waves))
+    start = np.minimum(np.arange(waves + 1, dtype=np.int64) * chunk, n_units).astype(np.int32)
+    d_page = torch.from_numpy(unit_page.view(np.int32)).to(dev)
+    d_kvh = torch.from_numpy(unit_kvh).to(dev)
+    d_start = torch.from_numpy(start).to(dev)
+    sink = torch.empty(waves * 64, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def launch(i):
+        pk = runner.layers[i % len(runner.layers)]
+        check(lib().lnskv_read_units(C.byref(pk.desc), d_page.data_ptr(), d_kvh.data_ptr(), d_start.data_ptr(),
+                                     waves, sink.data_ptr(), C.c_void_p(stream.cuda_stream)))
+
+    for i in range(2 * len(runner.layers)):
+        launch(i)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for i in range(reps):
+        launch(i)
+    e.record(stream)
+    torch.cuda.synchronize()
+    dt = s.elapsed_time(e) / 1e3 / reps
+    nbytes = n_units * 2 * 16 * 256
+    return {"bytes_per_launch": int(nbytes), "us_per_launch": round(dt * 1e6, 2),
+            "gb_per_s": round(nbytes / dt / 1e9, 1), "waves": int(waves), "units": int(n_units)}
 
 
 def measured_traffic(name: str):
@@ -195,6 +252,7 @@ def main():
     gbs_wall = nb["total"] / wall / 1e9
     gbs_ev = nb["total"] / ev_mean / 1e9
     copy = copy_ceiling(dev, args.copy_mb) if args.copy_mb > 0 else None
+    pattern = pattern_ceiling(w, runner, dev, args.pattern_reps)
     cpu = None
     if args.cpu_seconds > 0:
         threads = args.cpu_threads or len(os.sched_getaffinity(0))
@@ -246,6 +304,8 @@ def main():
                        "of one lnskv_append_decode call), mean HIP-event duration per step"),
             "copy_ceiling_gbs": copy["gb_per_s"] if copy else None,
             "frac_of_copy_ceiling": round(gbs_ev / copy["gb_per_s"], 4) if copy else None,
+            "pattern_ceiling": pattern,
+            "frac_of_pattern_ceiling": round(gbs_ev / pattern["gb_per_s"], 4) if pattern else None,
         },
         "cpu_baseline": cpu,
     }

@@ -67,6 +67,11 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert rc == _lib.ERR_INVALID and "differ" in msg
     rc, _ = _status(lib.lnskv_gather, C.byref(good), 1, 0, 4, 1, 1, 1, 1, None)
     assert rc == _lib.ERR_INVALID  # scale outputs only for Q8A
+    # the load probe reads 256-byte kv-head rows only (f16 x 64 dims: 128 bytes)
+    rc, msg = _status(lib.lnskv_read_units, C.byref(good), 1, 1, 1, 4, 1, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "256" in msg
+    rc, _ = _status(lib.lnskv_read_units, C.byref(good), 1, 1, 1, 0, 1, None)
+    assert rc == _lib.ERR_INVALID
 
 
 def test_workspace_size_formula():

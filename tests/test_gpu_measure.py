@@ -1,0 +1,65 @@
+"""GPU load probe (lnskv_read_units, measurement only): every lane's XOR word
+equals the host XOR of exactly the bytes the header says it loads -- each
+unit once, empty waves zero, odd and even unit counts, page ids and kv heads
+outside the pools reading page 0 / kv head 0."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import fill_pages, say
+from lnskv import DTYPE_F16, DTYPE_F32
+from lnskv._lib import check, lib
+from lnskv.device import PagedKV, _stream, sync
+
+pytestmark = pytest.mark.gpu
+
+
+def _expected(k32, v32, pages, kvhs, start, num_pages, n_kv):
+    """sink[w*64 + 16r + c]: XOR over the wave's units, K and V, rows r + 4j
+    (j < 4), of the four words of 16-byte chunk c of the unit's kv-head row."""
+    n_waves = len(start) - 1
+    out = np.zeros((n_waves, 64), np.uint32)
+    for w in range(n_waves):
+        acc = np.zeros((4, 16), np.uint32)
+        for u in range(start[w], start[w + 1]):
+            p = int(pages[u]) if pages[u] < num_pages else 0
+            h = int(kvhs[u]) if 0 <= kvhs[u] < n_kv else 0
+            for pool in (k32, v32):
+                words = pool[p, :, h, :].reshape(16, 16, 4)              # row, chunk, word
+                chunk = np.bitwise_xor.reduce(words, axis=2)            # row, chunk
+                acc ^= np.bitwise_xor.reduce(chunk.reshape(4, 4, 16), axis=0)  # rows r + 4j -> r
+        out[w] = acc.reshape(64)
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("dtype,d", [(DTYPE_F16, 128), (DTYPE_F32, 64)])
+def test_read_units_checksum(gpu, dtype, d):
+    say("read_units", dtype, d)
+    n_kv, num_pages = 4, 40
+    pk = PagedKV(num_pages, n_kv, d, dtype, gpu)
+    fill_pages(pk, seed=5)
+    rng = np.random.default_rng(d)
+    n_units = 61
+    pages = rng.integers(0, num_pages, n_units).astype(np.uint32)
+    kvhs = rng.integers(0, n_kv, n_units).astype(np.int32)
+    pages[3], pages[10] = num_pages, 0xFFFFFFFF  # outside the pool: page 0
+    kvhs[7], kvhs[20] = n_kv, -1                 # outside: kv head 0
+    # waves with 0, 1, 2, 3, 5, 7 ... units
+    counts = [0, 1, 2, 3, 5, 7, 0, 11, 4, 28]
+    assert sum(counts) == n_units
+    start = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    n_waves = len(counts)
+    sink = torch.full((n_waves * 64,), -1, dtype=torch.int32, device=gpu)
+    d_pages = torch.from_numpy(pages.view(np.int32)).to(gpu)
+    d_kvhs = torch.from_numpy(kvhs).to(gpu)
+    d_start = torch.from_numpy(start).to(gpu)
+    check(lib().lnskv_read_units(C.byref(pk.desc), d_pages.data_ptr(), d_kvhs.data_ptr(), d_start.data_ptr(),
+                                 n_waves, sink.data_ptr(), _stream(gpu)))
+    sync()
+    k32 = pk.k.view(torch.int32).cpu().numpy().view(np.uint32).reshape(num_pages, 16, n_kv, -1)
+    v32 = pk.v.view(torch.int32).cpu().numpy().view(np.uint32).reshape(num_pages, 16, n_kv, -1)
+    exp = _expected(k32, v32, pages, kvhs, start, num_pages, n_kv)
+    got = sink.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, exp)
