@@ -204,6 +204,33 @@ int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const
                              void* workspace_dev, size_t ws_bytes, lnskv_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Gated attention (gated_query_attention models): the q projection holds, per
+ * query head, head_dim q values then head_dim gate logits; the attention
+ * output is multiplied by sigmoid(logits) before o_proj.
+ * ---------------------------------------------------------------------------
+ * lnskv_split_gated_query (split_gated_query_kernel, lns_decode.metal:193-209;
+ * split_gated_query_interleaved, engine.rs:287-307): input_dev is
+ * [n_rows][n_heads][2 * head_dim]; q_out_dev gets the first halves and
+ * gate_out_dev 1 / (1 + exp(-x)) of the second, both [n_rows][n_heads][head_dim]
+ * (the engine then norms and rotates q). */
+int lnskv_split_gated_query(const float* input_dev, float* q_out_dev, float* gate_out_dev,
+                            int32_t n_rows, int32_t n_heads, int32_t head_dim,
+                            lnskv_stream_t stream);
+/* lnskv_append_decode (rope NULL) or lnskv_rope_append_decode (rope non-NULL)
+ * whose output row is multiplied, as it is stored, by gate_dev
+ * ([n_seq][n_heads][head_dim], the gate_out above): the engine's
+ * mul_inplace_enc after the attention (engine.rs:3424-3431,
+ * mul_inplace_kernel lns_decode.metal:211-221) folded into the decode.  The
+ * stored value is exactly out * gate of the ungated call (one f32 multiply);
+ * an empty window still stores a zero row. */
+int lnskv_gated_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const float* gate_dev,
+                              const float* q_dev, const float* k_new_dev, const float* v_new_dev,
+                              float* out_dev, const uint32_t* block_tables_dev, int32_t bt_stride,
+                              const int32_t* kv_len_dev, const int32_t* p_start_dev, int32_t n_seq,
+                              int32_t n_heads, int32_t max_kv_len, float scale, int32_t split_tokens,
+                              void* workspace_dev, size_t ws_bytes, lnskv_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * The reference call itself, one sequence: append the token at `pos` (k_in,
  * v_in [n_kv_heads*head_dim] f32) into its page and attend over [p_start, pos]
  * with scale 1/sqrt(head_dim) (metal:539).  Arguments follow

@@ -607,7 +607,7 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
         const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + hb + ii;
         const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) a.out[hrow * kD + 16 * nb + n] = o[ii][nb] * inv;
+        for (int nb = 0; nb < 8; ++nb) a.out[hrow * kD + 16 * nb + n] = gated(a, hrow * kD + 16 * nb + n, o[ii][nb] * inv);
       } else {
         const size_t pidx = po.pbase + (size_t)(hb + ii) * po.pstride;
 #pragma unroll
@@ -831,9 +831,10 @@ __global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_
     merge_wave<kD, 1, 8>(reinterpret_cast<const float2*>(a.ws_ml), a.ws_acc, 0, nw,
                          [=](int j) { return ((size_t)(wa + j) * 2 + (j == 0 ? first_slot : 0)) * REP + h; },
                          M, Ls, A);
-    float* out = a.out + ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * kD;
+    const size_t row = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * kD;
 #pragma unroll
-    for (int c = 0; c < C; ++c) out[c * kWave + lane] = Ls > 0.0f ? A[c] / Ls : 0.0f;
+    for (int c = 0; c < C; ++c)
+      a.out[row + c * kWave + lane] = gated(a, row + c * kWave + lane, Ls > 0.0f ? A[c] / Ls : 0.0f);
   }
 }
 

@@ -136,6 +136,7 @@ struct DecodeArgs {
   float* ws_acc;        // [n_seq][n_heads][max_parts][D] partial numerators
   float* ws_ml;         // [n_seq][n_heads][max_parts][2] partial (max, sum)
   int4* sk_desc;        // stream-K: per wave, the segment its first piece closes
+  const float* gate;      // gated attention: out *= gate ([n_seq][n_heads][D]); nullptr: none
   const float* rope_inv;  // fused RoPE in the MFMA kernels: inverse frequencies
   int32_t rope_half;      // fused RoPE: rotary_dim / 2, 32 or 64; 0: none (the kernels without RoPE run)
   int32_t kv_len_scalar;   // used when kv_len == nullptr
@@ -149,6 +150,13 @@ struct DecodeArgs {
   uint32_t num_pages;
   float scale_log2;  // softmax scale * log2(e): scores live in the exp2 domain
 };
+
+// The value stored at out[idx]: the attention output, multiplied by the
+// caller's gate when the call is gated (the reference's mul_inplace after the
+// attention, applied as the row is written).
+__device__ __forceinline__ float gated(const DecodeArgs& a, size_t idx, float v) {
+  return a.gate ? v * a.gate[idx] : v;
+}
 
 struct SeqWindow {
   int L;       // kv_len clamped to what the grid and the table can address
@@ -215,7 +223,7 @@ __device__ __forceinline__ void finish_block(const DecodeArgs& a, EpilogueLds<RE
     }
     const size_t hrow = (size_t)s * a.n_heads + h0 + h;
     if (single) {
-      a.out[hrow * D + i] = Ls > 0.0f ? A / Ls : 0.0f;
+      a.out[hrow * D + i] = gated(a, hrow * D + i, Ls > 0.0f ? A / Ls : 0.0f);
     } else {
       const size_t pidx = hrow * a.max_parts + part;
       a.ws_acc[pidx * D + i] = A;
@@ -276,7 +284,7 @@ __device__ __forceinline__ void merge_wave(const float2* ml, const float* acc, i
 
 template <int D, class Row>
 __device__ __forceinline__ void merge_partials(const float2* ml, const float* acc, int np, Row row,
-                                               float* out) {
+                                               float* out, const float* gate) {
   constexpr int C = D / kWave;
   __shared__ float s_acc[kWavesPerBlock][D];
   __shared__ float s_m[kWavesPerBlock], s_l[kWavesPerBlock];
@@ -305,7 +313,8 @@ __device__ __forceinline__ void merge_partials(const float2* ml, const float* ac
     float At = 0.0f;
 #pragma unroll
     for (int q = 0; q < kWavesPerBlock; ++q) At = fmaf(wq[q], s_acc[q][c * kWave + lane], At);
-    out[c * kWave + lane] = Lt > 0.0f ? At / Lt : 0.0f;
+    const float v = Lt > 0.0f ? At / Lt : 0.0f;
+    out[c * kWave + lane] = gate ? v * gate[c * kWave + lane] : v;
   }
 }
 
@@ -318,7 +327,8 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(DecodeArgs a) {
   const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + h;
   const size_t base = hrow * a.max_parts;
   merge_partials<D>(reinterpret_cast<const float2*>(a.ws_ml), a.ws_acc, np,
-                    [base](int j) { return base + (size_t)j; }, a.out + hrow * D);
+                    [base](int j) { return base + (size_t)j; }, a.out + hrow * D,
+                    a.gate ? a.gate + hrow * D : nullptr);
 }
 
 template <int REP, int D, bool FUSED>

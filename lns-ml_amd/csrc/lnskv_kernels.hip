@@ -340,6 +340,38 @@ bool mfma_path(int dtype, int d, int rep) {
   return dtype == LNSKV_DTYPE_F16 && d == 128 && (rep == 1 || rep == 2 || rep == 4 || rep == 8) && !force_valu();
 }
 
+// Gated query split (split_gated_query_kernel, lns_decode.metal:193-209): the
+// q projection holds, per (row, head), head_dim q values then head_dim gate
+// logits.  Element gid of q_out / gate_out is lane gid % head_dim of global
+// head gid / head_dim; gate_out = 1 / (1 + exp(-logit)).
+__global__ __launch_bounds__(kBlock) void split_gated_query_kernel(const float* in, float* q_out, float* gate_out,
+                                                                   int64_t n, int head_dim) {
+  for (int64_t gid = (int64_t)blockIdx.x * kBlock + threadIdx.x; gid < n; gid += (int64_t)gridDim.x * kBlock) {
+    const int64_t base = (gid / head_dim) * 2 * head_dim + gid % head_dim;
+    q_out[gid] = in[base];
+    gate_out[gid] = 1.0f / (1.0f + expf(-in[base + head_dim]));
+  }
+}
+
+// The same, four elements per thread (head_dim a multiple of 4, 16-byte
+// aligned buffers): 16-byte loads and stores.
+__global__ __launch_bounds__(kBlock) void split_gated_query_vec_kernel(const float* in, float* q_out,
+                                                                       float* gate_out, int64_t n4, int head_dim) {
+  for (int64_t g4 = (int64_t)blockIdx.x * kBlock + threadIdx.x; g4 < n4; g4 += (int64_t)gridDim.x * kBlock) {
+    const int64_t gid = 4 * g4;
+    const int64_t base = (gid / head_dim) * 2 * head_dim + gid % head_dim;
+    const float4 q = *reinterpret_cast<const float4*>(in + base);
+    const float4 z = *reinterpret_cast<const float4*>(in + base + head_dim);
+    float4 g;
+    g.x = 1.0f / (1.0f + expf(-z.x));
+    g.y = 1.0f / (1.0f + expf(-z.y));
+    g.z = 1.0f / (1.0f + expf(-z.z));
+    g.w = 1.0f / (1.0f + expf(-z.w));
+    *reinterpret_cast<float4*>(q_out + gid) = q;
+    *reinterpret_cast<float4*>(gate_out + gid) = g;
+  }
+}
+
 // How one decode call runs.  Stream-K (one wave per resident slot, each
 // taking an equal share of all pages) when the caller leaves the split to
 // the library, the MFMA kernel serves the pages and there are at most
@@ -428,7 +460,8 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
                  float* out, const uint32_t* bt, int32_t bt_stride, const int32_t* kv_len,
                  int32_t kv_len_scalar, const int32_t* p_start, int32_t p_start_scalar,
                  int32_t n_seq, int32_t n_heads, int32_t max_kv_len, float scale, int32_t split,
-                 void* ws, size_t ws_bytes, lnskv_stream_t stream, const lnskv_rope* rope = nullptr) {
+                 void* ws, size_t ws_bytes, lnskv_stream_t stream, const lnskv_rope* rope = nullptr,
+                 const float* gate = nullptr) {
   clear_error();
   if (int rc = check_pages(c)) return rc;
   if (!q || !out || !bt) return fail(LNSKV_ERR_INVALID, "q, out and block tables must be non-null");
@@ -508,6 +541,7 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
   a.scale_log2 = scale * kLog2e;
   a.rope_half = rope_half;
   a.rope_inv = rope_half > 0 ? rope->inv_freqs_dev : nullptr;
+  a.gate = gate;
   if (plan.sk_waves > 0) {
     a.ws_acc = static_cast<float*>(ws);
     a.ws_ml = a.ws_acc + (size_t)plan.sk_waves * 2 * rep * c->head_dim;
@@ -701,6 +735,38 @@ int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const
   if (!rope) return fail(LNSKV_ERR_INVALID, "rope must be non-null");
   return decode_entry<true>(c, q, k_new, v_new, out, bt, bt_stride, kv_len, 0, p_start, 0, n_seq,
                             n_heads, max_kv_len, scale, split_tokens, ws, ws_bytes, stream, rope);
+}
+
+int lnskv_gated_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const float* gate, const float* q,
+                              const float* k_new, const float* v_new, float* out, const uint32_t* bt,
+                              int32_t bt_stride, const int32_t* kv_len, const int32_t* p_start, int32_t n_seq,
+                              int32_t n_heads, int32_t max_kv_len, float scale, int32_t split_tokens, void* ws,
+                              size_t ws_bytes, lnskv_stream_t stream) {
+  clear_error();
+  if (!kv_len) return fail(LNSKV_ERR_INVALID, "kv_len must be non-null");
+  if (!gate) return fail(LNSKV_ERR_INVALID, "gate must be non-null");
+  return decode_entry<true>(c, q, k_new, v_new, out, bt, bt_stride, kv_len, 0, p_start, 0, n_seq,
+                            n_heads, max_kv_len, scale, split_tokens, ws, ws_bytes, stream, rope, gate);
+}
+
+int lnskv_split_gated_query(const float* input, float* q_out, float* gate_out, int32_t n_rows, int32_t n_heads,
+                            int32_t head_dim, lnskv_stream_t stream) {
+  clear_error();
+  if (!input || !q_out || !gate_out) return fail(LNSKV_ERR_INVALID, "input, q_out and gate_out must be non-null");
+  if (n_rows <= 0 || n_heads <= 0 || head_dim <= 0)
+    return fail(LNSKV_ERR_INVALID, "n_rows %d, n_heads %d and head_dim %d must be positive", n_rows, n_heads,
+                head_dim);
+  const int64_t n = (int64_t)n_rows * n_heads * head_dim;
+  const hipStream_t st = (hipStream_t)stream;
+  if (head_dim % 4 == 0 && aligned16(input) && aligned16(q_out) && aligned16(gate_out)) {
+    const int64_t n4 = n / 4;
+    const unsigned blocks = (unsigned)std::min<int64_t>((n4 + kBlock - 1) / kBlock, 65535);
+    split_gated_query_vec_kernel<<<blocks, kBlock, 0, st>>>(input, q_out, gate_out, n4, head_dim);
+  } else {
+    const unsigned blocks = (unsigned)std::min<int64_t>((n + kBlock - 1) / kBlock, 65535);
+    split_gated_query_kernel<<<blocks, kBlock, 0, st>>>(input, q_out, gate_out, n, head_dim);
+  }
+  return hip_check("split_gated_query kernel launch");
 }
 
 int lnskv_attention_paged(const float* q, const float* k_in, const float* v_in, const lnskv_pages* c,

@@ -37,6 +37,21 @@ def _need(t: torch.Tensor, name: str, dtype, numel: int, device) -> None:
         raise ValueError(f"{name} must have {numel} elements, got {t.numel()}")
 
 
+def split_gated_query(qg: torch.Tensor, n_heads: int, head_dim: int, q_out=None, gate_out=None):
+    """lnskv_split_gated_query: qg [n_rows][n_heads][2*head_dim] -> (q, sigmoid(gate))."""
+    n_rows = qg.numel() // (2 * n_heads * head_dim)
+    _need(qg, "qg", torch.float32, n_rows * n_heads * 2 * head_dim, qg.device)
+    if q_out is None:
+        q_out = torch.empty((n_rows, n_heads, head_dim), dtype=torch.float32, device=qg.device)
+    if gate_out is None:
+        gate_out = torch.empty((n_rows, n_heads, head_dim), dtype=torch.float32, device=qg.device)
+    _need(q_out, "q_out", torch.float32, n_rows * n_heads * head_dim, qg.device)
+    _need(gate_out, "gate_out", torch.float32, n_rows * n_heads * head_dim, qg.device)
+    check(lib().lnskv_split_gated_query(_ptr(qg), _ptr(q_out), _ptr(gate_out), n_rows, n_heads, head_dim,
+                                        _stream(qg.device)))
+    return q_out, gate_out
+
+
 class PagedKV:
     """One layer's paged K/V pools in the reference layout
     [num_pages][16][n_kv_heads][head_dim] (+ Q8A scales [num_pages*16][n_kv]),
@@ -164,6 +179,26 @@ class PagedKV:
                                              _ptr(v_new), _ptr(out), _ptr(tables), stride, _ptr(kv_len),
                                              _ptr(p_start), n_seq, n_heads, max_kv_len, scale, split,
                                              _ptr(workspace), ws_bytes, _stream(self.device)))
+        return out
+
+    def gated_append_decode(self, gate, q, k_new, v_new, tables, kv_len, *, n_heads: int, max_kv_len: int,
+                            scale: float, rope: "RopeTable | None" = None, p_start=None, split: int = 0,
+                            workspace=None, out=None) -> torch.Tensor:
+        """lnskv_gated_append_decode: append + decode (RoPE first when `rope`
+        is given) with the output multiplied by `gate` [n_seq][n_heads][d]."""
+        n_seq, stride = self._decode_common(q, tables, kv_len, p_start, n_heads)
+        _need(gate, "gate", torch.float32, n_seq * n_heads * self.head_dim, self.device)
+        _need(k_new, "k_new", torch.float32, n_seq * self.row_elems, self.device)
+        _need(v_new, "v_new", torch.float32, n_seq * self.row_elems, self.device)
+        if out is None:
+            out = torch.empty((n_seq, n_heads, self.head_dim), dtype=torch.float32, device=self.device)
+        _need(out, "out", torch.float32, n_seq * n_heads * self.head_dim, self.device)
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(lib().lnskv_gated_append_decode(C.byref(self.desc), C.byref(rope.desc) if rope is not None else None,
+                                              _ptr(gate), _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(out),
+                                              _ptr(tables), stride, _ptr(kv_len), _ptr(p_start), n_seq, n_heads,
+                                              max_kv_len, scale, split, _ptr(workspace), ws_bytes,
+                                              _stream(self.device)))
         return out
 
     def attention_paged(self, q, k_in, v_in, block_table, pos: int, n_heads: int, p_start: int = 0,

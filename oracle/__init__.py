@@ -71,6 +71,7 @@ def lib() -> C.CDLL:
             "orc_max_threads": (i32, []),
             "orc_rope_inv_freqs": (None, [i32, C.c_float, i32, vp, vp]),
             "orc_rope_apply": (None, [vp, i32, i32, i32, i32, vp, i32, vp]),
+            "orc_split_gated_query": (None, [vp, vp, vp, i32, i32, i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -300,3 +301,14 @@ def rope_apply(x, rotary_dim: int, inv_freqs, pos) -> np.ndarray:
     assert p.shape == (rows,)
     lib().orc_rope_apply(_p(y), rows, heads, d, rotary_dim, _p(inv), len(inv), _p(p))
     return y
+
+
+def split_gated_query(x, heads: int, head_dim: int):
+    """split_gated_query_interleaved (engine.rs:287-307): x [rows][heads][2*head_dim]
+    float32 -> (q, gate) [rows][heads][head_dim], gate = 1/(1+exp(-logit)) in f32."""
+    a = np.ascontiguousarray(x, np.float32).reshape(-1, heads, 2 * head_dim)
+    rows = a.shape[0]
+    q = np.empty((rows, heads, head_dim), np.float32)
+    g = np.empty((rows, heads, head_dim), np.float32)
+    lib().orc_split_gated_query(_p(a), _p(q), _p(g), rows, heads, head_dim)
+    return q, g

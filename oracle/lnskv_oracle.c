@@ -576,3 +576,17 @@ void orc_rope_apply(float* x, int n_rows, int heads, int head_dim, int rotary_di
     }
   }
 }
+
+/* split_gated_query_interleaved, engine.rs:287-307 (the kernel form is
+ * split_gated_query_kernel, lns_decode.metal:193-209): head h of row r starts
+ * at (r * heads + h) * 2 * head_dim; its first head_dim values are q, the
+ * next head_dim are gate logits, squashed by the f32 logistic function. */
+void orc_split_gated_query(const float* in, float* q_out, float* gate_out, int n_rows, int heads, int head_dim) {
+  for (size_t hh = 0; hh < (size_t)n_rows * heads; ++hh) {
+    const float* src = in + hh * 2 * head_dim;
+    for (int i = 0; i < head_dim; ++i) {
+      q_out[hh * head_dim + i] = src[i];
+      gate_out[hh * head_dim + i] = 1.0f / (1.0f + expf(-src[head_dim + i]));
+    }
+  }
+}

@@ -122,6 +122,12 @@ void orc_rope_inv_freqs(int rotary_dim, float theta, int mode, const float* para
 void orc_rope_apply(float* x, int n_rows, int heads, int head_dim, int rotary_dim, const float* inv_freqs,
                     int n_inv, const int32_t* pos);
 
+/* ---- gated query (engine.rs:287-307, lns_decode.metal:193-221) ---------- */
+/* split_gated_query_interleaved (engine.rs:287-307): in[n_rows][heads][2*head_dim]
+ * -> q_out[n_rows][heads][head_dim] (first halves) and gate_out (same shape)
+ * = 1 / (1 + exp(-x)) of the second halves, in f32 as the reference. */
+void orc_split_gated_query(const float* in, float* q_out, float* gate_out, int n_rows, int heads, int head_dim);
+
 #ifdef __cplusplus
 }
 #endif

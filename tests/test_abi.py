@@ -72,6 +72,11 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert rc == _lib.ERR_UNSUPPORTED and "256" in msg
     rc, _ = _status(lib.lnskv_read_units, C.byref(good), 1, 1, 1, 0, 1, None)
     assert rc == _lib.ERR_INVALID
+    rc, msg = _status(lib.lnskv_gated_append_decode, C.byref(good), None, None, 1, 1, 1, 1, 1, 4, 1, None, 1,
+                      32, 16, 0.1, 0, None, 0, None)
+    assert rc == _lib.ERR_INVALID and "gate" in msg
+    rc, _ = _status(lib.lnskv_split_gated_query, 1, 1, 1, 0, 4, 64, None)
+    assert rc == _lib.ERR_INVALID
 
 
 def test_workspace_size_formula():
