@@ -56,6 +56,8 @@ def parse():
                    help="1: the step goes through the fused RoPE entry points (Llama-3.1 table, rotary = head_dim)")
     p.add_argument("--pattern-reps", type=int, default=40,
                    help="launches of the load probe over the step's decode pages (0 = skip)")
+    p.add_argument("--oproj-reps", type=int, default=100,
+                   help="launches of the o_proj Q4L GEMV-accumulate at the config's shape (0 = skip)")
     p.add_argument("--copy-only", action="store_true",
                    help="run only the plain copy (the calibration kernel for HBM byte counters)")
     return p.parse_args()
@@ -135,6 +137,49 @@ def pattern_ceiling(w, runner, dev, reps: int) -> dict | None:
     nbytes = n_units * 2 * 16 * 256
     return {"bytes_per_launch": int(nbytes), "us_per_launch": round(dt * 1e6, 2),
             "gb_per_s": round(nbytes / dt / 1e9, 1), "waves": int(waves), "units": int(n_units)}
+
+
+def oproj_measure(w, runner, dev, reps: int) -> dict | None:
+    """The step after the path: o_proj, y += W_o attn_out over Q4_L weights
+    (lnskv_q4l_gemv_accumulate), at the config's shape: W_o is
+    (n_heads*head_dim) x (n_heads*head_dim) (Llama-3-8B: 4096 x 4096), one
+    vector per decoding sequence.  Random Q4L blocks; 32 weight copies are
+    cycled (300 MB for c2, more than the 256 MB MALL).  HIP events around
+    `reps` launches; bytes per launch: the weight blocks + x + y read and
+    written."""
+    import numpy as np
+    import torch
+
+    from lnskv.device import Q4LMatrix
+
+    dim = w.n_heads * w.head_dim
+    if reps <= 0 or runner.n_dec == 0 or dim % 256 != 0:
+        return None
+    rng = np.random.default_rng(5)
+    nb = dim * dim // 256
+    disk = rng.integers(0, 256, (nb, 134), dtype=np.uint8)
+    g = np.exp2(rng.uniform(-12, -2, nb)).astype(np.float16)
+    disk[:, 0:2] = g.view(np.uint8).reshape(nb, 2)
+    mats = [Q4LMatrix(disk.reshape(-1), dim, dim, dev) for _ in range(32)]
+    n_vec = runner.n_dec
+    x = torch.randn(n_vec, dim, device=dev)
+    y = torch.zeros(n_vec, dim, device=dev)
+    ws = torch.empty(max(mats[0].workspace_size(n_vec), 16), dtype=torch.uint8, device=dev)
+    for i in range(len(mats)):
+        mats[i].gemv_accumulate(x, y, ws)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(reps):
+        mats[i % len(mats)].gemv_accumulate(x, y, ws)
+    e.record()
+    torch.cuda.synchronize()
+    dt = s.elapsed_time(e) / 1e3 / reps
+    nbytes = nb * 144 + n_vec * dim * 4 * 3
+    del mats
+    return {"shape": f"{dim} x {dim} Q4L, {n_vec} vectors", "us_per_launch": round(dt * 1e6, 2),
+            "bytes_per_launch": int(nbytes), "gb_per_s": round(nbytes / dt / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def measured_traffic(name: str):
@@ -253,6 +298,7 @@ def main():
     gbs_ev = nb["total"] / ev_mean / 1e9
     copy = copy_ceiling(dev, args.copy_mb) if args.copy_mb > 0 else None
     pattern = pattern_ceiling(w, runner, dev, args.pattern_reps)
+    oproj = oproj_measure(w, runner, dev, args.oproj_reps)
     cpu = None
     if args.cpu_seconds > 0:
         threads = args.cpu_threads or len(os.sched_getaffinity(0))
@@ -308,6 +354,7 @@ def main():
             "frac_of_pattern_ceiling": round(gbs_ev / pattern["gb_per_s"], 4) if pattern else None,
         },
         "cpu_baseline": cpu,
+        "after_the_path": {"o_proj_q4l_gemv_accumulate": oproj},
     }
     print(json.dumps(line), flush=True)
 

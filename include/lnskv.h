@@ -231,6 +231,41 @@ int lnskv_gated_append_decode(const lnskv_pages* c, const lnskv_rope* rope, cons
                               void* workspace_dev, size_t ws_bytes, lnskv_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * o_proj after the attention: x += W_o . attn_out over Q4_L weights
+ * ---------------------------------------------------------------------------
+ * Disk super-block (Q4LSuperBlock, lns-core/src/quant/q4l.rs:136-158), 134
+ * bytes per 256 weights: scale_global (f16 bits), 8 local-scale nibbles (4
+ * bytes), 128 weight bytes (weight i in nibble i, low nibble first; bit 3
+ * sign, bits 0-2 magnitude m: 0 is zero, else 2^(m - 5)).  Device block
+ * (block_q4_l, lns_decode.metal:12-15), 144 bytes: 8 f16 effective scales
+ * f16(scale_global * 2^(scale_local - 7)), then the 128 weight bytes.  A
+ * rows x cols matrix is rows x ceil(cols / 256) blocks, row-major. */
+#define LNSKV_Q4L_DISK_BYTES 134
+#define LNSKV_Q4L_DEVICE_BYTES 144
+/* MetalContext::prepare_tensor, Q4L branch (lns-metal/src/lib.rs:1255-1320):
+ * host repack of rows x ceil(cols/256) disk blocks into device blocks
+ * (out_blocks: rows * ceil(cols/256) * 144 bytes of host memory); effective
+ * scales rounded to nearest even, as F16::from_f32. */
+int lnskv_q4l_prepare(const void* disk_blocks, size_t disk_bytes, int32_t rows, int32_t cols,
+                      void* out_blocks);
+/* q4l_gemv_accumulate_multirow (lns_decode.metal:1174-1225; the engine's
+ * gemv_accumulate_multirow_enc for o_proj, engine.rs:3433-3446), batched:
+ * y[v][r] += sum_c W[r][c] * x[v][c] for v < n_vec, x [n_vec][x_stride] and
+ * y [n_vec][y_stride] f32 on the device, W the device blocks (16-byte
+ * aligned).  cols a multiple of 256 (as the reference kernel's ncols >> 8),
+ * |x| < 65504.  Products of f16 weight codes and f16 parts of x on the matrix
+ * cores, f32 sums in a fixed order: the same bits on every call.
+ * workspace_dev/ws_bytes: 16-byte aligned device scratch of at least
+ * lnskv_q4l_workspace_size(cols, n_vec) bytes (x split into the matrix-core
+ * operands), or NULL/0 to use a buffer the library keeps per device (calls
+ * that use it must not overlap in time). */
+int lnskv_q4l_workspace_size(int32_t cols, int32_t n_vec, size_t* bytes);
+int lnskv_q4l_gemv_accumulate(const void* blocks_dev, const float* x_dev, float* y_dev,
+                              int32_t rows, int32_t cols, int32_t n_vec, int32_t x_stride,
+                              int32_t y_stride, void* workspace_dev, size_t ws_bytes,
+                              lnskv_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * The reference call itself, one sequence: append the token at `pos` (k_in,
  * v_in [n_kv_heads*head_dim] f32) into its page and attend over [p_start, pos]
  * with scale 1/sqrt(head_dim) (metal:539).  Arguments follow

@@ -350,5 +350,10 @@ int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, 
 int mfma_sk_waves(int rep, bool fused, int* waves);
 
 int hip_check(const char* what);
+// A device buffer the library keeps per device and grows on demand (hipMalloc;
+// growing synchronizes the device first): 0 the decode workspace, 1 RoPE'd
+// q/k rows, 2 the Q4L GEMV's x operands.  Calls that share one must not
+// overlap in time.
+int library_buffer(int which, size_t need, void** out);
 
 }  // namespace lnskv

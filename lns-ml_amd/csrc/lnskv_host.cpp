@@ -17,6 +17,7 @@
 #include <cstdio>
 #include <cstring>
 #include <deque>
+#include <limits>
 #include <new>
 #include <vector>
 
@@ -59,6 +60,49 @@ int check_pages(const lnskv_pages* c) {
   if (c->dtype == LNSKV_DTYPE_Q8A && (!c->k_scales || !c->v_scales))
     return fail(LNSKV_ERR_INVALID, "Q8A pools need k_scales and v_scales");
   return LNSKV_OK;
+}
+
+// f32 -> f16 bits, round to nearest even (overflow to infinity, NaN kept
+// quiet), and back; host side of the Q4L repack.
+uint16_t f32_to_f16_bits(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7FFFFFFFu;
+  if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u);
+  if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);  // 65520 and up round to infinity
+  if (ax < 0x38800000u) {                                    // below 2^-14: f16 subnormal or zero
+    // units of 2^-24: shift the 24-bit significand right, rounding to even
+    if (ax < 0x33000000u) return (uint16_t)sign;  // below 2^-25: rounds to zero (2^-25 itself ties to 0)
+    const uint32_t e = ax >> 23;
+    const uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+    const uint32_t shift = 126u - e;  // value = m * 2^(e - 150) = m >> shift units of 2^-24
+    uint32_t h = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (h & 1u))) h += 1u;
+    return (uint16_t)(sign | h);
+  }
+  uint32_t h = ((((ax >> 23) & 0xFFu) - 112u) << 10) | ((ax >> 13) & 0x3FFu);
+  const uint32_t rem = ax & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;
+  return (uint16_t)(sign | h);
+}
+
+float f16_bits_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+  float v;
+  if (e == 0)
+    v = std::ldexp((float)m, -24);
+  else if (e == 31)
+    v = m ? std::numeric_limits<float>::quiet_NaN() : std::numeric_limits<float>::infinity();
+  else
+    v = std::ldexp((float)(m | 0x400u), (int)e - 25);
+  uint32_t bits;
+  std::memcpy(&bits, &v, 4);
+  bits |= sign;
+  std::memcpy(&v, &bits, 4);
+  return v;
 }
 
 }  // namespace lnskv
@@ -343,6 +387,32 @@ int lnskv_rope_inv_freqs(int32_t rotary_dim, float theta, int32_t mode, const fl
       }
     }
     out[i] = f;
+  }
+  return LNSKV_OK;
+}
+
+// prepare_tensor's Q4L branch (lns-metal/src/lib.rs:1296-1315): per
+// super-block, the 8 effective scales f16(scale_global * 2^(sl - 7)) (round
+// to nearest even), then the 128 weight bytes unchanged.
+int lnskv_q4l_prepare(const void* disk_blocks, size_t disk_bytes, int32_t rows, int32_t cols, void* out_blocks) {
+  lnskv::clear_error();
+  if (!disk_blocks || !out_blocks) return fail(LNSKV_ERR_INVALID, "disk and output blocks must be non-null");
+  if (rows <= 0 || cols <= 0) return fail(LNSKV_ERR_INVALID, "rows %d and cols %d must be positive", rows, cols);
+  const size_t n_blocks = (size_t)rows * (size_t)((cols + 255) / 256);
+  if (disk_bytes < n_blocks * LNSKV_Q4L_DISK_BYTES)
+    return fail(LNSKV_ERR_INVALID, "%zu bytes of Q4L blocks, %zu needed for %d x %d", disk_bytes,
+                n_blocks * LNSKV_Q4L_DISK_BYTES, rows, cols);
+  const uint8_t* src = static_cast<const uint8_t*>(disk_blocks);
+  uint8_t* dst = static_cast<uint8_t*>(out_blocks);
+  for (size_t b = 0; b < n_blocks; ++b, src += LNSKV_Q4L_DISK_BYTES, dst += LNSKV_Q4L_DEVICE_BYTES) {
+    const float g = lnskv::f16_bits_to_f32((uint16_t)(src[0] | (src[1] << 8)));
+    for (int i = 0; i < 8; ++i) {
+      const int sl = (src[2 + i / 2] >> ((i % 2) * 4)) & 0xF;
+      const uint16_t e = lnskv::f32_to_f16_bits(g * std::ldexp(1.0f, sl - 7));
+      dst[2 * i] = (uint8_t)(e & 0xFF);
+      dst[2 * i + 1] = (uint8_t)(e >> 8);
+    }
+    std::memcpy(dst + 16, src + 6, 128);
   }
   return LNSKV_OK;
 }

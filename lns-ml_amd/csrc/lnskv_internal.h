@@ -21,5 +21,7 @@ inline size_t dtype_bytes(int32_t dtype) {
 int check_geometry(const lnskv_pages* c);
 // Checks geometry and that the pools (and Q8A scales) are non-null.
 int check_pages(const lnskv_pages* c);
+uint16_t f32_to_f16_bits(float f);
+float f16_bits_to_f32(uint16_t h);
 
 }  // namespace lnskv

@@ -411,20 +411,28 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
   return LNSKV_OK;
 }
 
-// Library-kept workspace per device, grown on demand.
+}  // namespace
+
+// Library-kept buffers per device, grown on demand: 0 decode workspace,
+// 1 RoPE rows, 2 Q4L x operands.
+namespace {
+constexpr int kLibraryBuffers = 3;
 struct DeviceWorkspace {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::vector<DeviceWorkspace> g_ws;  // [device * 2 + which]: 0 decode workspace, 1 RoPE rows
+std::vector<DeviceWorkspace> g_ws;  // [device * kLibraryBuffers + which]
+}  // namespace
 
 int library_buffer(int which, size_t need, void** out) {
+  if (which < 0 || which >= kLibraryBuffers) return fail(LNSKV_ERR_INVALID, "library buffer %d", which);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  if ((int)g_ws.size() <= dev * 2 + which) g_ws.resize((size_t)dev * 2 + 2);
-  DeviceWorkspace& w = g_ws[(size_t)dev * 2 + which];
+  const size_t slot = (size_t)dev * kLibraryBuffers + (size_t)which;
+  if (g_ws.size() <= slot) g_ws.resize((size_t)(dev + 1) * kLibraryBuffers);
+  DeviceWorkspace& w = g_ws[slot];
   if (w.bytes < need) {
     if (w.ptr) {
       // Kernels queued earlier may still use the old buffer.
@@ -443,6 +451,7 @@ int library_buffer(int which, size_t need, void** out) {
   return LNSKV_OK;
 }
 
+namespace {
 int library_workspace(size_t need, void** out) { return library_buffer(0, need, out); }
 
 // Checks a RoPE descriptor against head_dim; half = rotary_dim / 2.

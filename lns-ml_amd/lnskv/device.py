@@ -261,6 +261,45 @@ class RopeTable:
         self.desc = Rope(self.inv_freqs.data_ptr(), rotary_dim)
 
 
+class Q4LMatrix:
+    """A rows x cols Q4_L weight matrix on the device: the disk super-blocks
+    (134 bytes per 256 weights, row-major) repacked by lnskv_q4l_prepare
+    (MetalContext::prepare_tensor, lns-metal/src/lib.rs:1255-1320)."""
+
+    def __init__(self, disk_blocks, rows: int, cols: int, device="cuda"):
+        import numpy as np
+
+        disk = np.ascontiguousarray(disk_blocks, np.uint8).reshape(-1)
+        n = rows * ((cols + 255) // 256)
+        host = np.zeros(n * 144, np.uint8)
+        check(lib().lnskv_q4l_prepare(disk.ctypes.data_as(C.c_void_p), disk.nbytes, rows, cols,
+                                      host.ctypes.data_as(C.c_void_p)))
+        self.rows, self.cols = rows, cols
+        self.device = torch.device(device)
+        self.blocks = torch.from_numpy(host).to(self.device)
+
+    def workspace_size(self, n_vec: int) -> int:
+        out = C.c_size_t()
+        check(lib().lnskv_q4l_workspace_size(self.cols, n_vec, C.byref(out)))
+        return out.value
+
+    def gemv_accumulate(self, x: torch.Tensor, y: torch.Tensor, workspace=None) -> torch.Tensor:
+        """lnskv_q4l_gemv_accumulate: y[v] += W x[v] for every row v of x
+        [n_vec][>= cols] into y [n_vec][>= rows] (rows of both unit-stride);
+        workspace None: the library's buffer."""
+        if x.dim() != 2 or y.dim() != 2 or x.shape[0] != y.shape[0]:
+            raise ValueError("x and y must be [n_vec][...] with the same n_vec")
+        if x.dtype != torch.float32 or y.dtype != torch.float32 or x.stride(1) != 1 or y.stride(1) != 1:
+            raise ValueError("x and y must be float32 with unit-stride rows")
+        if x.shape[1] < self.cols or y.shape[1] < self.rows:
+            raise ValueError("x rows need >= cols entries and y rows >= rows entries")
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(lib().lnskv_q4l_gemv_accumulate(self.blocks.data_ptr(), x.data_ptr(), y.data_ptr(), self.rows,
+                                              self.cols, int(x.shape[0]), int(x.stride(0)), int(y.stride(0)),
+                                              _ptr(workspace), ws_bytes, _stream(self.device)))
+        return y
+
+
 def sync(device=None) -> None:
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
     check(lib().lnskv_sync(_stream(dev)))

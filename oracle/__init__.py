@@ -72,6 +72,10 @@ def lib() -> C.CDLL:
             "orc_rope_inv_freqs": (None, [i32, C.c_float, i32, vp, vp]),
             "orc_rope_apply": (None, [vp, i32, i32, i32, i32, vp, i32, vp]),
             "orc_split_gated_query": (None, [vp, vp, vp, i32, i32, i32]),
+            "orc_q4l_prepare": (None, [vp, i32, vp]),
+            "orc_q4l_decode_block": (None, [vp, vp]),
+            "orc_q4l_gemv_f64": (None, [vp, vp, i32, vp, i32, vp, i32, i32, i32]),
+            "orc_q4l_decode_matrix": (None, [vp, i32, i32, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -312,3 +316,46 @@ def split_gated_query(x, heads: int, head_dim: int):
     g = np.empty((rows, heads, head_dim), np.float32)
     lib().orc_split_gated_query(_p(a), _p(q), _p(g), rows, heads, head_dim)
     return q, g
+
+
+Q4L_DISK_BYTES, Q4L_DEV_BYTES = 134, 144
+
+
+def q4l_prepare(disk) -> np.ndarray:
+    """prepare_tensor's Q4L repack (lns-metal/src/lib.rs:1296-1315): disk
+    super-blocks (134 bytes each) -> device blocks (144 bytes each)."""
+    d = np.ascontiguousarray(disk, np.uint8).reshape(-1)
+    n = d.size // Q4L_DISK_BYTES
+    out = np.zeros(n * Q4L_DEV_BYTES, np.uint8)
+    lib().orc_q4l_prepare(_p(d), n, _p(out))
+    return out
+
+
+def q4l_decode_block(dev_block) -> np.ndarray:
+    """The kernel's weights of one device block (lns_decode_byte, lns_decode.metal:38-48)."""
+    b = np.ascontiguousarray(dev_block, np.uint8).reshape(-1)
+    assert b.size == Q4L_DEV_BYTES
+    w = np.zeros(256, np.float32)
+    lib().orc_q4l_decode_block(_p(b), _p(w))
+    return w
+
+
+def q4l_gemv_f64(dev_blocks, x, y_in, rows: int, cols: int) -> np.ndarray:
+    """y_in + W x in float64 for every vector of x [n_vec][cols] (W: rows x cols device blocks)."""
+    blk = np.ascontiguousarray(dev_blocks, np.uint8).reshape(-1)
+    xv = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+    yv = np.ascontiguousarray(y_in, np.float32).reshape(-1, rows)
+    n_vec = xv.shape[0]
+    assert yv.shape[0] == n_vec and blk.size == rows * (cols // 256) * Q4L_DEV_BYTES
+    out = np.zeros((n_vec, rows), np.float64)
+    lib().orc_q4l_gemv_f64(_p(blk), _p(xv), cols, _p(yv), rows, _p(out), rows, cols, n_vec)
+    return out
+
+
+def q4l_decode_matrix(dev_blocks, rows: int, cols: int) -> np.ndarray:
+    """The kernel's weights of a rows x cols device matrix (float32)."""
+    blk = np.ascontiguousarray(dev_blocks, np.uint8).reshape(-1)
+    assert blk.size == rows * (cols // 256) * Q4L_DEV_BYTES
+    w = np.zeros((rows, cols), np.float32)
+    lib().orc_q4l_decode_matrix(_p(blk), rows, cols, _p(w))
+    return w

@@ -590,3 +590,57 @@ void orc_split_gated_query(const float* in, float* q_out, float* gate_out, int n
     }
   }
 }
+
+/* prepare_tensor's Q4L branch, lns-metal/src/lib.rs:1296-1315. */
+void orc_q4l_prepare(const uint8_t* disk, int n_blocks, uint8_t* dev) {
+  for (int b = 0; b < n_blocks; ++b) {
+    const uint8_t* src = disk + (size_t)b * 134;
+    uint8_t* dst = dev + (size_t)b * 144;
+    const uint16_t g_bits = (uint16_t)(src[0] | (src[1] << 8));
+    const float g = orc_f16_to_f32(g_bits);
+    for (int i = 0; i < 8; ++i) {
+      const int sl = (src[2 + i / 2] >> ((i % 2) * 4)) & 0xF;
+      const float ef = g * (float)ldexp(1.0, sl - 7); /* exact power-of-two product in f32 */
+      const uint16_t eb = orc_f32_to_f16(ef); /* round to nearest even, as F16::from_f32 */
+      dst[2 * i] = (uint8_t)(eb & 0xFF);
+      dst[2 * i + 1] = (uint8_t)(eb >> 8);
+    }
+    memcpy(dst + 16, src + 6, 128);
+  }
+}
+
+/* lns_decode_byte, lns_decode.metal:38-48, over one block. */
+void orc_q4l_decode_block(const uint8_t* blk, float* w) {
+  static const float lut[8] = {0.0f, 0.0625f, 0.125f, 0.25f, 0.5f, 1.0f, 2.0f, 4.0f};
+  for (int i = 0; i < 256; ++i) {
+    const float scale = orc_f16_to_f32((uint16_t)(blk[2 * (i / 32)] | (blk[2 * (i / 32) + 1] << 8)));
+    const int nib = (blk[16 + i / 2] >> ((i % 2) * 4)) & 0xF;
+    const float sgn = 1.0f - 2.0f * (float)((nib >> 3) & 1);
+    w[i] = sgn * scale * lut[nib & 7];
+  }
+}
+
+void orc_q4l_gemv_f64(const uint8_t* blocks, const float* x, int x_stride, const float* y_in, int y_stride,
+                      double* y_out, int rows, int cols, int n_vec) {
+  const int bpr = cols / 256;
+  float w[256];
+  for (int r = 0; r < rows; ++r) {
+    for (int v = 0; v < n_vec; ++v) y_out[(size_t)v * y_stride + r] = (double)y_in[(size_t)v * y_stride + r];
+    for (int b = 0; b < bpr; ++b) {
+      orc_q4l_decode_block(blocks + ((size_t)r * bpr + b) * 144, w);
+      for (int v = 0; v < n_vec; ++v) {
+        double acc = 0.0;
+        const float* xv = x + (size_t)v * x_stride + (size_t)b * 256;
+        for (int i = 0; i < 256; ++i) acc += (double)w[i] * (double)xv[i];
+        y_out[(size_t)v * y_stride + r] += acc;
+      }
+    }
+  }
+}
+
+void orc_q4l_decode_matrix(const uint8_t* blocks, int rows, int cols, float* w) {
+  const int bpr = cols / 256;
+  for (int r = 0; r < rows; ++r)
+    for (int b = 0; b < bpr; ++b)
+      orc_q4l_decode_block(blocks + ((size_t)r * bpr + b) * 144, w + (size_t)r * cols + (size_t)b * 256);
+}

@@ -128,6 +128,27 @@ void orc_rope_apply(float* x, int n_rows, int heads, int head_dim, int rotary_di
  * = 1 / (1 + exp(-x)) of the second halves, in f32 as the reference. */
 void orc_split_gated_query(const float* in, float* q_out, float* gate_out, int n_rows, int heads, int head_dim);
 
+/* ---- o_proj over Q4_L weights (lns-core/src/quant/q4l.rs, lns-metal) ----- */
+/* Disk super-block (Q4LSuperBlock, q4l.rs:136-158): 134 bytes = scale_global
+ * (f16 bits, LE), 4 bytes of local-scale nibbles (sub-block i in nibble i,
+ * low nibble first), 128 weight bytes (weight i in nibble i, low nibble
+ * first; bit 3 sign, bits 0-2 magnitude m).  Device block (prepare_tensor,
+ * lns-metal/src/lib.rs:1255-1320; block_q4_l, lns_decode.metal:12-15): 144
+ * bytes = 8 f16 effective scales f16(f32(scale_global) * 2^(sl - 7)) (round to
+ * nearest even), then the 128 weight bytes.  n_blocks super-blocks. */
+void orc_q4l_prepare(const uint8_t* disk, int n_blocks, uint8_t* dev);
+/* Weights of one device block as the kernel forms them (lns_decode_byte,
+ * lns_decode.metal:38-48): w[i] = (1 - 2 s) * f32(scale[i / 32]) * LUT[m],
+ * LUT = {0, 2^-4, ..., 2^2}. */
+void orc_q4l_decode_block(const uint8_t* dev_block, float* w256);
+/* q4l_gemv_accumulate_multirow (lns_decode.metal:1174-1225) for n_vec
+ * vectors, in float64: y[b][r] = y_in[b][r] + sum_c W[r][c] x[b][c], W the
+ * rows x cols device blocks (cols / 256 per row, cols a multiple of 256). */
+void orc_q4l_gemv_f64(const uint8_t* dev_blocks, const float* x, int x_stride, const float* y_in,
+                      int y_stride, double* y_out, int rows, int cols, int n_vec);
+/* The kernel's weights of a rows x cols device matrix, w[rows][cols]. */
+void orc_q4l_decode_matrix(const uint8_t* dev_blocks, int rows, int cols, float* w);
+
 #ifdef __cplusplus
 }
 #endif
