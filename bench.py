@@ -58,6 +58,8 @@ def parse():
                    help="launches of the load probe over the step's decode pages (0 = skip)")
     p.add_argument("--oproj-reps", type=int, default=100,
                    help="launches of the o_proj Q4L GEMV-accumulate at the config's shape (0 = skip)")
+    p.add_argument("--prefill-reps", type=int, default=20,
+                   help="launches of chunked-prefill attention over the config's pages (0 = skip)")
     p.add_argument("--copy-only", action="store_true",
                    help="run only the plain copy (the calibration kernel for HBM byte counters)")
     return p.parse_args()
@@ -182,6 +184,51 @@ def oproj_measure(w, runner, dev, reps: int) -> dict | None:
             "frac_of_hbm_peak": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def prefill_measure(w, runner, dev, reps: int, chunk: int = 256) -> dict | None:
+    """Chunked-prefill attention (lnskv_prefill_attention) over the config's
+    pages: the last `chunk` tokens of every decoding sequence are taken as
+    its prompt chunk (their K/V are in the pages), each query attending
+    [0, its position].  Algorithmic work: 4 * head_dim flops per (query,
+    head, attended token) (q.k and p.v); the kernel runs q and p as f16 hi
+    and lo parts, twice that on the matrix cores.  Layers cycled, HIP events
+    around `reps` launches."""
+    import torch
+
+    if reps <= 0 or runner.n_dec == 0 or w.dtype != 1 or w.head_dim != 128:
+        return None
+    desc, tok = [], 0
+    for s in runner.dec_rows:
+        L = int(w.kv_len[s])
+        ln = min(chunk, L)
+        desc.append((int(s), L - ln, ln, tok))
+        tok += ln
+    chunks = torch.tensor(desc, dtype=torch.int32, device=dev)
+    q = torch.randn(tok, w.n_heads, w.head_dim, device=dev)
+    out = torch.empty_like(q)
+    flops = sum(4 * w.head_dim * w.n_heads * (p0 + i + 1) for (_, p0, ln, _) in desc for i in range(ln))
+
+    def launch(i):
+        runner.layers[i % len(runner.layers)].prefill_attention(q, chunks, runner.tables, n_heads=w.n_heads,
+                                                               scale=w.scale, out=out)
+
+    for i in range(2 * len(runner.layers)):
+        launch(i)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(reps):
+        launch(i)
+    e.record()
+    torch.cuda.synchronize()
+    dt = s.elapsed_time(e) / 1e3 / reps
+    return {"shape": f"last {chunk} tokens of each of {len(desc)} sequences ({tok} queries), "
+                     f"Hq{w.n_heads}/Hkv{w.n_kv}/d{w.head_dim} f16 pages",
+            "us_per_launch": round(dt * 1e6, 1), "gflop": round(flops / 1e9, 2),
+            "tflop_per_s": round(flops / dt / 1e12, 1),
+            "frac_of_f16_mfma_peak": round(flops / dt / 1e12 / 2500.0, 4),
+            "mfma_tflop_per_s_with_hi_lo": round(2 * flops / dt / 1e12, 1)}
+
+
 def measured_traffic(name: str):
     """HBM bytes per step from the committed counter summary, or None."""
     path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
@@ -299,6 +346,7 @@ def main():
     copy = copy_ceiling(dev, args.copy_mb) if args.copy_mb > 0 else None
     pattern = pattern_ceiling(w, runner, dev, args.pattern_reps)
     oproj = oproj_measure(w, runner, dev, args.oproj_reps)
+    prefill = prefill_measure(w, runner, dev, args.prefill_reps)
     cpu = None
     if args.cpu_seconds > 0:
         threads = args.cpu_threads or len(os.sched_getaffinity(0))
@@ -355,6 +403,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "after_the_path": {"o_proj_q4l_gemv_accumulate": oproj},
+        "prefill": {"chunked_prefill_attention": prefill},
     }
     print(json.dumps(line), flush=True)
 

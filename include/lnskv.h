@@ -204,6 +204,28 @@ int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const
                              void* workspace_dev, size_t ws_bytes, lnskv_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Chunked-prefill attention over pages.  The reference has none: it runs the
+ * whole forward once per prompt token (engine.rs:2835-2855), each token
+ * appended, then attending [p_start, pos] through the paged kernel.  This
+ * computes, for a chunk of consecutive prompt tokens whose K/V are already in
+ * the pages (lnskv_append first), every token's attention at once: query row
+ * t attends positions [p_start, pos(t)] of its sequence -- what lnskv_decode
+ * with kv_len = pos(t) + 1 gives that token alone.
+ *   chunks_dev: n_chunks x {table row, first position, length, first token}
+ *   (int32 x 4, 16-byte aligned): chunk i's tokens are q/out rows
+ *   [first token, first token + length), at positions first position + 0,
+ *   1, ...; chunks outside [0, n_rows) x [0, n_tok) are skipped.
+ *   q_dev / out_dev: [n_tok][n_heads][head_dim] f32; p_start_dev: per table
+ *   row (NULL = 0).  f16 pages with head_dim 128 only (LNSKV_ERR_UNSUPPORTED
+ *   otherwise).
+ * ------------------------------------------------------------------------- */
+int lnskv_prefill_attention(const lnskv_pages* c, const float* q_dev, float* out_dev,
+                            const int32_t* chunks_dev, int32_t n_chunks, int32_t n_tok,
+                            const uint32_t* block_tables_dev, int32_t bt_stride, int32_t n_rows,
+                            const int32_t* p_start_dev, int32_t n_heads, float scale,
+                            lnskv_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Gated attention (gated_query_attention models): the q projection holds, per
  * query head, head_dim q values then head_dim gate logits; the attention
  * output is multiplied by sigmoid(logits) before o_proj.

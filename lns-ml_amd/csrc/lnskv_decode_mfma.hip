@@ -946,4 +946,294 @@ int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, 
 template int launch_decode_mfma_sk<false>(const DecodeArgs&, int, int, int, hipStream_t);
 template int launch_decode_mfma_sk<true>(const DecodeArgs&, int, int, int, hipStream_t);
 
+
+// ---------------------------------------------------------------------------
+// Chunked prefill over pages.  The chunk's K/V are already in the pages; a
+// query at position P attends the window [p_start, P] of its sequence, as the
+// decode would with kv_len = P + 1 -- for 16 queries of one chunk at a time.
+// Block (tile slot, kv head) has REP waves; wave w serves query head
+// kvh * REP + w for the tile's queries, streaming the tile's pages exactly as
+// the decode does (K into registers, V by LDS DMA into a two-slot ring), so
+// the REP waves of a block read the same pages through one CU's caches.
+//
+// Per page (16 tokens) and head:
+//  Q.K^T  S^T[16 tok][16 query] = K . Q^T as 4 x 2 v_mfma_f32_16x16x32_f16:
+//         q enters as f16 hi and lo parts (per query scaled by 2^-E), both
+//         accumulated into the same registers.  Lane (g, n) receives
+//         S^T[token 4g+ii][query n].
+//  softmax  per query column, running max raised only past a slack of 8
+//         (log2 units); tokens after the query's position are masked.
+//  P.V    O[16 query][128] = P . V: lane (g, n) already holds P[query n]
+//         [tokens 4g..4g+3], the A layout; f16 hi and lo of p as two
+//         v_mfma_f32_16x16x16_f16 per 16 dims, V from the transposed LDS
+//         reads.  Lane (g, n) accumulates O[query 4g+ii][16 nb + n].
+// ---------------------------------------------------------------------------
+namespace {
+
+template <bool FULL>
+__device__ __forceinline__ void consume_prefill(float4v (&acc)[8], float& m, float& l, const half8 (&qh)[4],
+                                                const half8 (&ql)[4], float qexp, const Stream& sm,
+                                                const half8 (&k)[4], int slot, int tok0, bool valid, int ta, int tb,
+                                                int qpos, bool qok, int g, int n) {
+  lds_u8* vslot = sm.vring + slot * kVSlot;
+  if constexpr (!FULL) {
+    // rows of tokens no query attends (and of a missing page) must not carry
+    // NaN bits into the matrix product: zero them in the slot
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = tok0 + 4 * g + j;
+      if (!(valid && t >= ta && t < tb))
+        *(lds_u32x4*)(vslot + (4 * j + g) * kRowBytes + 16 * n) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  float4v sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[j], qh[j], sacc, 0, 0, 0);
+    sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[j], ql[j], sacc, 0, 0, 0);
+  }
+  float s[4];
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) s[ii] = sacc[ii] * qexp;
+  if constexpr (!FULL) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int t = tok0 + 4 * g + ii;
+      if (!(qok && valid && t >= ta && t < tb && t <= qpos)) s[ii] = -INFINITY;
+    }
+  }
+  float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  mx = max_xor16(max_xor32(mx));  // over the 16 tokens of query n
+  const bool need = mx > m + kRescaleSlack;
+  if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform
+    const float m_new = need ? mx : m;
+    const float alpha = fast_exp2(m - m_new);
+    m = m_new;
+    l *= alpha;
+    // result row 4g+ii is query 4g+ii, whose alpha sits in lane 16g + 4g + ii
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const float aq = __shfl(alpha, 20 * g + ii, kWave);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) acc[nb][ii] *= aq;
+    }
+  }
+  float pr[4];
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) pr[ii] = fast_exp2(s[ii] - m);
+  l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+  half4 ph, pl;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    const _Float16 hi = (_Float16)pr[ii];
+    ph[ii] = hi;
+    pl[ii] = (_Float16)(pr[ii] - (float)hi);
+  }
+  // transposed V reads as in consume_page (inline asm: the DMA into this
+  // slot is complete -- the caller's vmcnt wait -- and the lgkmcnt wait tied
+  // to the results completes the reads before any use)
+  const uint32_t vbase = (uint32_t)(size_t)(vslot + sm.vr_off + sm.vr_half);
+  short4v bv[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    const uint32_t chunk = ((uint32_t)(2 * nb) + sm.vr_sub) ^ sm.vr_swz;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[nb]) : "v"(vbase + 16u * chunk) : "memory");
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]), "+v"(bv[4]), "+v"(bv[5]), "+v"(bv[6]),
+                 "+v"(bv[7])
+               :
+               : "memory");
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    const half4 b = __builtin_bit_cast(half4, bv[nb]);
+    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, b, acc[nb], 0, 0, 0);
+    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, b, acc[nb], 0, 0, 0);
+  }
+}
+
+template <int REP>
+__global__ __launch_bounds__(kWave * REP) void prefill_mfma_kernel(PrefillArgs a) {
+  constexpr int DEPTH = 2;
+  __shared__ __attribute__((aligned(16))) uint8_t vring_[REP][DEPTH * kVSlot];
+  const int lane = (int)(threadIdx.x & (kWave - 1)), w = (int)(threadIdx.x / kWave);
+  const int g = lane >> 4, n = lane & 15;
+  const int kvh = (int)blockIdx.y, h = kvh * REP + w;
+
+  // The tile of this block: chunk c's tiles are 16 consecutive queries; the
+  // tiles of all chunks are numbered in chunk order (64 chunks per scan).
+  int slot = (int)blockIdx.x, c = -1, tile = 0;
+  for (int c0 = 0; c0 < a.n_chunks; c0 += kWave) {  // wave-uniform
+    const int ci = c0 + lane;
+    const int len = ci < a.n_chunks ? a.chunks[ci].z : 0;
+    const int nt = len > 0 ? (len + 15) / 16 : 0;
+    const int incl = wave_incl_scan(nt);
+    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+    if (slot < total) {
+      const int idx = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(incl <= slot));
+      c = c0 + idx;
+      tile = slot - (__builtin_amdgcn_readlane(incl, idx) - __builtin_amdgcn_readlane(nt, idx));
+      break;
+    }
+    slot -= total;
+  }
+  if (c < 0) return;  // beyond the last tile
+  const int4 ch = a.chunks[c];
+  const int s = ch.x;
+  if (s < 0 || s >= a.n_rows || ch.w < 0 || ch.w + ch.z > a.n_tok || ch.y < 0) return;  // a chunk outside the inputs
+  const int pos0 = ch.y + 16 * tile;
+  const int qn = min(16, ch.z - 16 * tile);  // queries in this tile
+  const int t0 = ch.w + 16 * tile;
+  const int p_last = pos0 + qn - 1;
+  int p0 = a.p_start ? a.p_start[s] : 0;
+  p0 = min(max(p0, 0), p_last);
+  const int ta = p0, tb = min(p_last + 1, a.bt_stride * kPage);
+  const bool qok = n < qn;
+  const int qpos = pos0 + n;
+
+  // q of query n, head h: dims 32j + 8g .. +7 (loaded before the pages)
+  float4v qraw[8];
+  {
+    const float4v* qsrc =
+        reinterpret_cast<const float4v*>(a.q + ((size_t)(t0 + (qok ? n : 0)) * a.n_heads + h) * kD + 8 * g);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qraw[2 * j] = qsrc[8 * j];
+      qraw[2 * j + 1] = qsrc[8 * j + 1];
+    }
+  }
+
+  Stream sm;
+  sm.k_pages = a.k_pages;
+  sm.v_pages = a.v_pages;
+  sm.vring = (lds_u8*)vring_[w];
+  sm.num_pages = a.num_pages;
+  sm.kvh_off = (uint32_t)kvh * kRowBytes;
+  const uint32_t rs = (uint32_t)a.n_kv * kRowBytes;
+  sm.page_bytes = kPage * rs;
+  sm.koff = (uint32_t)n * rs + 16u * g;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sm.voff[j] = (uint32_t)(4 * g + j) * rs + 16u * ((uint32_t)n ^ v_swz(4 * j + g));
+  {
+    const int R = 4 * (n >> 2) + g;
+    sm.vr_off = (uint32_t)R * kRowBytes;
+    sm.vr_swz = v_swz(R);
+    sm.vr_half = 8u * (n & 1);
+    sm.vr_sub = (uint32_t)((n & 3) >> 1);
+  }
+
+  // table window of 64 entries (lane j: entry base + j), as in run_piece
+  const uint32_t* bt_row = a.bt + (size_t)s * a.bt_stride;
+  const int pg_first = ta / kPage;
+  const int npg = ta < tb ? (tb - 1) / kPage - pg_first + 1 : 0;
+  int base = pg_first;
+  uint32_t btv = 0;
+  auto load_window = [&]() {
+    const int e = base + lane;
+    btv = e < a.bt_stride ? bt_row[e] : 0u;
+    wait_vmcnt<0>();
+  };
+  load_window();
+  auto phys_of = [&](int i) -> uint32_t {
+    int idx = pg_first + i - base;
+    if (idx >= 64) {
+      base += 64;
+      idx -= 64;
+      load_window();
+    }
+    return __builtin_amdgcn_readlane(btv, idx);
+  };
+
+  half8 kbuf[DEPTH][4];
+  bool vld[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) vld[d] = issue_page(sm, phys_of(d), d, kbuf[d]) && npg > d;
+
+  // q -> B operands: per query, scale by 2^-E (E from max |q * scale|) so
+  // that hi and lo stay in f16 range; scores are scaled back by 2^E
+  half8 qh[4], ql[4];
+  float qexp;
+  {
+    float amax = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(qraw[r][e] * a.scale_log2));
+    amax = max_xor16(max_xor32(amax));  // over the 4 lanes of query n
+    int E = 0;
+    if (amax > 0.0f && amax < INFINITY) (void)frexpf(amax, &E);
+    const float inv = ldexpf(1.0f, -E);
+    qexp = ldexpf(1.0f, E);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = qok ? qraw[2 * j + (e >> 2)][e & 3] * a.scale_log2 * inv : 0.0f;
+        const _Float16 hi = (_Float16)y;
+        qh[j][e] = hi;
+        ql[j][e] = (_Float16)(y - (float)hi);
+      }
+  }
+  float4v acc[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = kMInit, l = 0.0f;
+
+  // page i: wait for its loads (the page issued after it stays in flight),
+  // consume, refill the slot with page i + DEPTH
+  auto step = [&](int i, half8(&k)[4], bool& valid, int sl, bool steady) {
+    const int ahead = steady ? DEPTH - 1 : min(npg - 1 - i, DEPTH - 1);
+    if (ahead >= 1)
+      wait_vmcnt<8>();
+    else
+      wait_vmcnt<0>();
+    const int tok0 = (pg_first + i) * kPage;
+    if (steady && valid && tok0 >= ta && tok0 + kPage <= tb && tok0 + kPage - 1 <= pos0)
+      consume_prefill<true>(acc, m, l, qh, ql, qexp, sm, k, sl, tok0, valid, ta, tb, qpos, qok, g, n);
+    else
+      consume_prefill<false>(acc, m, l, qh, ql, qexp, sm, k, sl, tok0, valid, ta, tb, qpos, qok, g, n);
+    if (steady || i + DEPTH < npg) valid = issue_page(sm, phys_of(i + DEPTH), sl, k);
+  };
+  int i = 0;
+  for (; i + 2 * DEPTH - 1 < npg; i += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) step(i + d, kbuf[d], vld[d], d, true);
+  }
+#pragma unroll
+  for (int d = 0; d < 2 * DEPTH - 1; ++d)
+    if (i + d < npg) step(i + d, kbuf[d % DEPTH], vld[d % DEPTH], d % DEPTH, false);
+  wait_vmcnt<0>();  // stand-in pages of a tile with fewer than DEPTH pages
+
+  // l over the 16 tokens of each page: sum the four lanes of query n
+  const float lt = sum_xor16(sum_xor32(l));
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    const float L = __shfl(lt, 20 * g + ii, kWave);  // query 4g + ii
+    const int qq = 4 * g + ii;
+    if (qq < qn) {
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      float* orow = a.out + ((size_t)(t0 + qq) * a.n_heads + h) * kD;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) orow[16 * nb + n] = acc[nb][ii] * inv;
+    }
+  }
+}
+
+template <int REP>
+void launch_prefill_rep(const PrefillArgs& a, int n_tile_slots, hipStream_t st) {
+  prefill_mfma_kernel<REP><<<dim3((unsigned)n_tile_slots, (unsigned)a.n_kv), kWave * REP, 0, st>>>(a);
+}
+}  // namespace
+
+int launch_prefill_mfma(const PrefillArgs& a, int rep, int n_tile_slots, hipStream_t st) {
+  switch (rep) {
+    case 1: launch_prefill_rep<1>(a, n_tile_slots, st); break;
+    case 2: launch_prefill_rep<2>(a, n_tile_slots, st); break;
+    case 4: launch_prefill_rep<4>(a, n_tile_slots, st); break;
+    case 8: launch_prefill_rep<8>(a, n_tile_slots, st); break;
+    default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
+  }
+  return hip_check("prefill kernel launch");
+}
+
 }  // namespace lnskv

@@ -349,6 +349,26 @@ int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, 
 // Waves of the stream-K kernel resident at once on the current device.
 int mfma_sk_waves(int rep, bool fused, int* waves);
 
+// Chunked prefill over f16 pages with head_dim 128 (lnskv_prefill_attention).
+struct PrefillArgs {
+  const uint8_t* k_pages;
+  const uint8_t* v_pages;
+  const float* q;          // [n_tok][n_heads][128]
+  float* out;              // [n_tok][n_heads][128]
+  const int4* chunks;      // [n_chunks]: {table row, first position, length, first token}
+  const uint32_t* bt;      // [n_rows][bt_stride]
+  const int32_t* p_start;  // [n_rows] window starts, or nullptr (0)
+  int32_t n_chunks;
+  int32_t n_tok;
+  int32_t n_rows;
+  int32_t bt_stride;
+  int32_t n_kv;
+  int32_t n_heads;
+  uint32_t num_pages;
+  float scale_log2;
+};
+int launch_prefill_mfma(const PrefillArgs& a, int rep, int n_tile_slots, hipStream_t st);
+
 int hip_check(const char* what);
 // A device buffer the library keeps per device and grows on demand (hipMalloc;
 // growing synchronizes the device first): 0 the decode workspace, 1 RoPE'd

@@ -758,6 +758,44 @@ int lnskv_gated_append_decode(const lnskv_pages* c, const lnskv_rope* rope, cons
                             n_heads, max_kv_len, scale, split_tokens, ws, ws_bytes, stream, rope, gate);
 }
 
+int lnskv_prefill_attention(const lnskv_pages* c, const float* q, float* out, const int32_t* chunks,
+                            int32_t n_chunks, int32_t n_tok, const uint32_t* bt, int32_t bt_stride, int32_t n_rows,
+                            const int32_t* p_start, int32_t n_heads, float scale, lnskv_stream_t stream) {
+  clear_error();
+  if (int rc = check_pages(c)) return rc;
+  if (!q || !out || !chunks || !bt) return fail(LNSKV_ERR_INVALID, "q, out, chunks and block tables must be non-null");
+  if (n_chunks <= 0 || n_chunks > 65535) return fail(LNSKV_ERR_INVALID, "n_chunks %d out of range [1, 65535]", n_chunks);
+  if (n_tok <= 0) return fail(LNSKV_ERR_INVALID, "n_tok %d must be positive", n_tok);
+  if (n_rows <= 0 || bt_stride <= 0)
+    return fail(LNSKV_ERR_INVALID, "n_rows %d and bt_stride %d must be positive", n_rows, bt_stride);
+  if (n_heads <= 0 || n_heads % (int)c->n_kv_heads != 0)
+    return fail(LNSKV_ERR_INVALID, "n_heads %d is not a multiple of n_kv_heads %u", n_heads, c->n_kv_heads);
+  if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(LNSKV_ERR_INVALID, "scale must be positive and finite");
+  if (c->dtype != LNSKV_DTYPE_F16 || c->head_dim != 128)
+    return fail(LNSKV_ERR_UNSUPPORTED, "prefill attention is built for f16 pages with head_dim 128");
+  if (!aligned16(chunks) || !aligned16(q)) return fail(LNSKV_ERR_INVALID, "chunks and q must be 16-byte aligned");
+  PrefillArgs a{};
+  a.k_pages = static_cast<const uint8_t*>(c->k_pages);
+  a.v_pages = static_cast<const uint8_t*>(c->v_pages);
+  a.q = q;
+  a.out = out;
+  a.chunks = reinterpret_cast<const int4*>(chunks);
+  a.bt = bt;
+  a.p_start = p_start;
+  a.n_chunks = n_chunks;
+  a.n_tok = n_tok;
+  a.n_rows = n_rows;
+  a.bt_stride = bt_stride;
+  a.n_kv = (int32_t)c->n_kv_heads;
+  a.n_heads = n_heads;
+  a.num_pages = c->num_pages;
+  a.scale_log2 = scale * kLog2e;
+  // at most one partly filled tile per chunk beyond n_tok / 16 full ones
+  const int64_t slots = ((int64_t)n_tok + 15) / 16 + n_chunks;
+  if (slots > INT32_MAX) return fail(LNSKV_ERR_INVALID, "too many query tiles");
+  return launch_prefill_mfma(a, n_heads / (int)c->n_kv_heads, (int)slots, (hipStream_t)stream);
+}
+
 int lnskv_split_gated_query(const float* input, float* q_out, float* gate_out, int32_t n_rows, int32_t n_heads,
                             int32_t head_dim, lnskv_stream_t stream) {
   clear_error();

@@ -108,6 +108,7 @@ SIGNATURES = {
     "lnskv_rope_append": (C.c_int, [_P, _R, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp]),
     "lnskv_rope_append_decode": (
         C.c_int, [_P, _R, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _sz, _vp]),
+    "lnskv_prefill_attention": (C.c_int, [_P, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _i32, _f32, _vp]),
     "lnskv_split_gated_query": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "lnskv_gated_append_decode": (
         C.c_int, [_P, _R, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _sz,

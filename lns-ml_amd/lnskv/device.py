@@ -201,6 +201,25 @@ class PagedKV:
                                               _stream(self.device)))
         return out
 
+    def prefill_attention(self, q, chunks, tables, *, n_heads: int, scale: float, p_start=None,
+                          out=None) -> torch.Tensor:
+        """lnskv_prefill_attention: q [n_tok][n_heads][d]; chunks int32
+        [n_chunks][4] = (table row, first position, length, first token)."""
+        n_tok = q.numel() // (n_heads * self.head_dim)
+        _need(q, "q", torch.float32, n_tok * n_heads * self.head_dim, self.device)
+        if chunks.dtype != torch.int32 or chunks.dim() != 2 or chunks.shape[1] != 4 or not chunks.is_contiguous():
+            raise ValueError("chunks must be a contiguous int32 [n_chunks][4] tensor")
+        if tables.dim() != 2:
+            raise ValueError("tables must be [n_rows][stride]")
+        if out is None:
+            out = torch.empty((n_tok, n_heads, self.head_dim), dtype=torch.float32, device=self.device)
+        _need(out, "out", torch.float32, n_tok * n_heads * self.head_dim, self.device)
+        check(lib().lnskv_prefill_attention(C.byref(self.desc), _ptr(q), _ptr(out), _ptr(chunks),
+                                            int(chunks.shape[0]), n_tok, _ptr(tables), int(tables.shape[1]),
+                                            int(tables.shape[0]), _ptr(p_start), n_heads, scale,
+                                            _stream(self.device)))
+        return out
+
     def attention_paged(self, q, k_in, v_in, block_table, pos: int, n_heads: int, p_start: int = 0,
                         out=None, dispatch: bool = False) -> torch.Tensor:
         """The reference's single-sequence call (encode_attention_paged_q8a,
