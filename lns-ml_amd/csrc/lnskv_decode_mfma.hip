@@ -950,182 +950,260 @@ template int launch_decode_mfma_sk<true>(const DecodeArgs&, int, int, int, hipSt
 // ---------------------------------------------------------------------------
 // Chunked prefill over pages.  The chunk's K/V are already in the pages; a
 // query at position P attends the window [p_start, P] of its sequence, as the
-// decode would with kv_len = P + 1 -- for 16 queries of one chunk at a time.
-// Block (tile slot, kv head) has REP waves; wave w serves query head
-// kvh * REP + w for the tile's queries, streaming the tile's pages exactly as
-// the decode does (K into registers, V by LDS DMA into a two-slot ring), so
-// the REP waves of a block read the same pages through one CU's caches.
+// decode would with kv_len = P + 1.
 //
-// Per page (16 tokens) and head:
-//  Q.K^T  S^T[16 tok][16 query] = K . Q^T as 4 x 2 v_mfma_f32_16x16x32_f16:
-//         q enters as f16 hi and lo parts (per query scaled by 2^-E), both
-//         accumulated into the same registers.  Lane (g, n) receives
-//         S^T[token 4g+ii][query n].
-//  softmax  per query column, running max raised only past a slack of 8
-//         (log2 units); tokens after the query's position are masked.
-//  P.V    O[16 query][128] = P . V: lane (g, n) already holds P[query n]
-//         [tokens 4g..4g+3], the A layout; f16 hi and lo of p as two
-//         v_mfma_f32_16x16x16_f16 per 16 dims, V from the transposed LDS
-//         reads.  Lane (g, n) accumulates O[query 4g+ii][16 nb + n].
+// Workgroup = (tile of QT queries of one chunk, kv head), four waves.  The
+// workgroup streams the tile's window two pages (32 tokens) at a time through
+// a three-slot LDS ring: each wave DMAs one quarter of every page's K and V
+// rows, a barrier publishes the pair, and all four waves read it from LDS, so
+// a page is fetched once per tile.  Wave w serves the 16 queries of query
+// group w / WPQ and HW = min(REP, 4) query heads (head set w % WPQ); the K and
+// V operands it reads from LDS serve all HW heads.
+//
+// Per pair and head, lane (g, n) = (lane / 16, lane % 16):
+//  Q.K^T  per page, S^T[16 tok][16 query] = K . Q^T as 4 x 2
+//         v_mfma_f32_16x16x32_f16 (q as f16 hi and lo parts, each query and
+//         head scaled by 2^-E); lane (g, n) receives S^T[token 4g+ii][query n].
+//  softmax  per query over the pair's 32 tokens; the running max is raised
+//         only past a slack of 8 (log2 units); tokens after the query's
+//         position, outside the window or on a missing page are masked.
+//  P.V    O[16 query][128] += P[16 query][32 tok] . V[32 tok][128] as 8 x 2
+//         v_mfma_f32_16x16x32_f16 (p as f16 hi and lo).  The contraction
+//         index k = 8g + e is page 0's token 4g+e for e < 4 and page 1's token
+//         4g+e-4 otherwise, so the A operand is the lane's own eight weights
+//         and the B operand is two transposed LDS reads, one per page.  Lane
+//         (g, n) accumulates O[query 4g+ii][16 nb + n].
+//
+// LDS slot = K page 0 | K page 1 | V page 0 | V page 1, 4 KiB each.  K row r
+// holds token r with its 16-byte chunk c at chunk c ^ r, so the A-operand
+// reads (16 lanes: 16 tokens, one logical chunk) hit 16 distinct bank groups.
+// V rows use the decode's swizzled layout for ds_read_b64_tr_b16.
+//
+// Blocks are numbered (tile, kv head) with the kv head fastest.  Consecutive
+// blocks go to the 8 XCDs in turn, so with 8 kv heads every tile of one
+// (chunk, kv head) runs on the same XCD and re-reads its pages from that
+// XCD's L2, and every XCD gets an equal share of each chunk.
 // ---------------------------------------------------------------------------
 namespace {
 
-template <bool FULL>
-__device__ __forceinline__ void consume_prefill(float4v (&acc)[8], float& m, float& l, const half8 (&qh)[4],
-                                                const half8 (&ql)[4], float qexp, const Stream& sm,
-                                                const half8 (&k)[4], int slot, int tok0, bool valid, int ta, int tb,
-                                                int qpos, bool qok, int g, int n) {
-  lds_u8* vslot = sm.vring + slot * kVSlot;
-  if constexpr (!FULL) {
-    // rows of tokens no query attends (and of a missing page) must not carry
-    // NaN bits into the matrix product: zero them in the slot
+constexpr int kPfWaves = 4;
+constexpr int kPfSlot = 4 * kVSlot;  // K and V of two pages
+constexpr int kPfDepth = 3;          // ring slots: one pair consumed, two in flight
+
+template <int REP>
+struct PfShape {
+  static constexpr int HW = REP < 4 ? REP : 4;        // query heads per wave
+  static constexpr int WPQ = REP / HW;                 // waves per 16 queries
+  static constexpr int QT = 16 * (kPfWaves / WPQ);     // queries per tile
+};
+
+// Workgroup barrier after this wave's LDS accesses have completed.  No
+// release fence: that would also wait for the DMAs still in flight.  The
+// memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void pf_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Per-lane constants of the pair DMA and the LDS operand reads.
+struct PfLanes {
+  uint32_t koff;    // K DMA: token 4w+g, chunk n ^ (4w+g)
+  uint32_t voff;    // V DMA: token 4g+w, chunk n ^ sw(4w+g)
+  uint32_t lds_q;   // 1024 w: this wave's quarter of a page region
+  uint32_t krow;    // K reads: row n
+  uint32_t kchunk[4];  // 16 * ((4j + g) ^ n)
+  uint32_t vr_off, vr_swz, vr_half, vr_sub;  // transposed V reads, as Stream
+};
+
+// DMA of this wave's quarter of pages ph0 and ph1 (K and V) into `slot`:
+// exactly 4 vector-memory instructions.  A missing page reads page 0 (in
+// bounds); its tokens are masked and its V rows zeroed before use.
+__device__ __forceinline__ void pf_issue(const PrefillArgs& a, const PfLanes& pl, uint32_t page_bytes,
+                                         uint32_t kvh_off, lds_u8* slot, uint32_t ph0, uint32_t ph1) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = tok0 + 4 * g + j;
-      if (!(valid && t >= ta && t < tb))
-        *(lds_u32x4*)(vslot + (4 * j + g) * kRowBytes + 16 * n) = u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-  float4v sacc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[j], qh[j], sacc, 0, 0, 0);
-    sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[j], ql[j], sacc, 0, 0, 0);
-  }
-  float s[4];
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii) s[ii] = sacc[ii] * qexp;
-  if constexpr (!FULL) {
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-      const int t = tok0 + 4 * g + ii;
-      if (!(qok && valid && t >= ta && t < tb && t <= qpos)) s[ii] = -INFINITY;
-    }
-  }
-  float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-  mx = max_xor16(max_xor32(mx));  // over the 16 tokens of query n
-  const bool need = mx > m + kRescaleSlack;
-  if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform
-    const float m_new = need ? mx : m;
-    const float alpha = fast_exp2(m - m_new);
-    m = m_new;
-    l *= alpha;
-    // result row 4g+ii is query 4g+ii, whose alpha sits in lane 16g + 4g + ii
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-      const float aq = __shfl(alpha, 20 * g + ii, kWave);
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) acc[nb][ii] *= aq;
-    }
-  }
-  float pr[4];
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii) pr[ii] = fast_exp2(s[ii] - m);
-  l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-  half4 ph, pl;
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii) {
-    const _Float16 hi = (_Float16)pr[ii];
-    ph[ii] = hi;
-    pl[ii] = (_Float16)(pr[ii] - (float)hi);
-  }
-  // transposed V reads as in consume_page (inline asm: the DMA into this
-  // slot is complete -- the caller's vmcnt wait -- and the lgkmcnt wait tied
-  // to the results completes the reads before any use)
-  const uint32_t vbase = (uint32_t)(size_t)(vslot + sm.vr_off + sm.vr_half);
-  short4v bv[8];
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) {
-    const uint32_t chunk = ((uint32_t)(2 * nb) + sm.vr_sub) ^ sm.vr_swz;
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[nb]) : "v"(vbase + 16u * chunk) : "memory");
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]), "+v"(bv[4]), "+v"(bv[5]), "+v"(bv[6]),
-                 "+v"(bv[7])
-               :
-               : "memory");
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) {
-    const half4 b = __builtin_bit_cast(half4, bv[nb]);
-    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, b, acc[nb], 0, 0, 0);
-    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, b, acc[nb], 0, 0, 0);
+  for (int p = 0; p < 2; ++p) {
+    const uint32_t ph = p ? ph1 : ph0;
+    const size_t base = (size_t)(ph < a.num_pages ? ph : 0u) * page_bytes + kvh_off;
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.k_pages + base), (short)0, (int)page_bytes, kBufferFormat);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(slot + p * kVSlot + pl.lds_q),
+                                             16, (int)pl.koff, 0, 0, 0);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.v_pages + base), (short)0, (int)page_bytes, kBufferFormat);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rv, (__attribute__((address_space(3))) void*)(slot + (2 + p) * kVSlot + pl.lds_q), 16, (int)pl.voff, 0, 0, 0);
   }
 }
 
+// MODE 0: every token of the pair is attended by every query of the wave;
+// 1: causal masks only; 2: some tokens are outside the window or on a missing
+// page: mask them and zero their V rows (stale LDS or page bytes may hold NaN
+// patterns, and 0 * NaN would reach the accumulators).
+template <int HW, int MODE>
+__device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW], float (&l)[HW],
+                                           const half8 (&qh)[HW][4], const half8 (&ql)[HW][4],
+                                           const float (&qexp)[HW], const PfLanes& pl, lds_u8* slot, int tok0,
+                                           bool v0, bool v1, int ta, int tb, int qpos, bool qok, int g, int n) {
+  if constexpr (MODE == 2) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = tok0 + 16 * p + 4 * g + j;
+        if (!((p ? v1 : v0) && t >= ta && t < tb))
+          *(lds_u32x4*)(slot + (2 + p) * kVSlot + (4 * j + g) * kRowBytes + 16 * n) = u32x4{0u, 0u, 0u, 0u};
+      }
+  }
+  // K operands of both pages, then the V operands of both pages; the reads
+  // are inline asm because the compiler cannot tell which slot a DMA writes
+  // and would wait for every DMA in flight before a plain LDS read.  This
+  // slot's DMAs have completed (vmcnt wait and barrier before the call).
+  const uint32_t kb = (uint32_t)(size_t)slot + pl.krow;
+  half8 k[2][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    asm volatile("ds_read_b128 %0, %1" : "=v"(k[0][j]) : "v"(kb + pl.kchunk[j]) : "memory");
+    asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(k[1][j]) : "v"(kb + pl.kchunk[j]) : "memory");
+  }
+  const uint32_t vb = (uint32_t)(size_t)slot + 2 * kVSlot + pl.vr_off + pl.vr_half;
+  short4v bv[2][8];
+  auto read_v = [&](int nb) {
+    const uint32_t a0 = vb + 16u * ((((uint32_t)(2 * nb)) + pl.vr_sub) ^ pl.vr_swz);
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[0][nb]) : "v"(a0) : "memory");
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(bv[1][nb]) : "v"(a0) : "memory");
+  };
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) read_v(nb);
+  // LDS reads complete in order: the 8 V reads just issued may be outstanding
+  asm volatile("s_waitcnt lgkmcnt(8)"
+               : "+v"(k[0][0]), "+v"(k[0][1]), "+v"(k[0][2]), "+v"(k[0][3]), "+v"(k[1][0]), "+v"(k[1][1]),
+                 "+v"(k[1][2]), "+v"(k[1][3])
+               :
+               : "memory");
+#pragma unroll
+  for (int nb = 4; nb < 8; ++nb) read_v(nb);
+  float4v sacc[HW][2];
+#pragma unroll
+  for (int hh = 0; hh < HW; ++hh)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[p][j], qh[hh][j], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[p][j], ql[hh][j], s, 0, 0, 0);
+      }
+      sacc[hh][p] = s;
+    }
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(bv[0][0]), "+v"(bv[0][1]), "+v"(bv[0][2]), "+v"(bv[0][3]), "+v"(bv[0][4]), "+v"(bv[0][5]),
+                 "+v"(bv[0][6]), "+v"(bv[0][7]), "+v"(bv[1][0]), "+v"(bv[1][1]), "+v"(bv[1][2]), "+v"(bv[1][3]),
+                 "+v"(bv[1][4]), "+v"(bv[1][5]), "+v"(bv[1][6]), "+v"(bv[1][7])
+               :
+               : "memory");
+#pragma unroll
+  for (int hh = 0; hh < HW; ++hh) {
+    float s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = sacc[hh][e >> 2][e & 3] * qexp[hh];
+    if constexpr (MODE != 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = tok0 + 16 * (e >> 2) + 4 * g + (e & 3);
+        if (!(qok && ((e >> 2) ? v1 : v0) && t >= ta && t < tb && t <= qpos)) s[e] = -INFINITY;
+      }
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    mx = max_xor16(max_xor32(mx));  // over the 32 tokens of query n
+    const bool need = mx > m[hh] + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform
+      const float m_new = need ? mx : m[hh];
+      const float alpha = fast_exp2(m[hh] - m_new);
+      m[hh] = m_new;
+      l[hh] *= alpha;
+      // result row 4g+ii is query 4g+ii, whose alpha sits in lane 16g + 4g + ii
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const float aq = __shfl(alpha, 20 * g + ii, kWave);
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[hh][nb][ii] *= aq;
+      }
+    }
+    half8 ph, plo;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = fast_exp2(s[e] - m[hh]);
+      lsum += p;
+      const _Float16 hi = (_Float16)p;
+      ph[e] = hi;
+      plo[e] = (_Float16)(p - (float)hi);
+    }
+    l[hh] += lsum;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const half8 b = __builtin_bit_cast(half8, __builtin_shufflevector(bv[0][nb], bv[1][nb], 0, 1, 2, 3, 4, 5, 6, 7));
+      acc[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b, acc[hh][nb], 0, 0, 0);
+      acc[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo, b, acc[hh][nb], 0, 0, 0);
+    }
+  }
+}
+
+// Chunk i's tile count, 0 for a chunk outside the inputs (skipped).
+template <int QT>
+__device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int i) {
+  if (i >= a.n_chunks) return 0;
+  const int4 ch = a.chunks[i];
+  const bool ok = ch.x >= 0 && ch.x < a.n_rows && ch.y >= 0 && ch.z > 0 && ch.w >= 0 && ch.z <= a.n_tok - ch.w;
+  return ok ? (ch.z + QT - 1) / QT : 0;
+}
+
 template <int REP>
-__global__ __launch_bounds__(kWave * REP) void prefill_mfma_kernel(PrefillArgs a) {
-  constexpr int DEPTH = 2;
-  __shared__ __attribute__((aligned(16))) uint8_t vring_[REP][DEPTH * kVSlot];
+__global__ __launch_bounds__(kWave* kPfWaves) void prefill_mfma_kernel(PrefillArgs a) {
+  constexpr int HW = PfShape<REP>::HW, WPQ = PfShape<REP>::WPQ, QT = PfShape<REP>::QT;
+  __shared__ __attribute__((aligned(16))) uint8_t ring_[kPfDepth * kPfSlot];
   const int lane = (int)(threadIdx.x & (kWave - 1)), w = (int)(threadIdx.x / kWave);
   const int g = lane >> 4, n = lane & 15;
-  const int kvh = (int)blockIdx.y, h = kvh * REP + w;
 
-  // The tile of this block: chunk c's tiles are 16 consecutive queries; the
-  // tiles of all chunks are numbered in chunk order (64 chunks per scan).
-  int slot = (int)blockIdx.x, c = -1, tile = 0;
-  for (int c0 = 0; c0 < a.n_chunks; c0 += kWave) {  // wave-uniform
-    const int ci = c0 + lane;
-    const int len = ci < a.n_chunks ? a.chunks[ci].z : 0;
-    const int nt = len > 0 ? (len + 15) / 16 : 0;
+  // block -> (chunk, tile, kv head); the kv head varies fastest
+  const int kvh = (int)(blockIdx.x % (unsigned)a.n_kv);
+  int slot = (int)(blockIdx.x / (unsigned)a.n_kv), c = -1, tile = 0, nt_c = 0;
+  for (int c0 = 0; c0 < a.n_chunks; c0 += kWave) {  // wave-uniform; identical in the four waves
+    const int nt = pf_tiles<QT>(a, c0 + lane);
     const int incl = wave_incl_scan(nt);
     const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
     if (slot < total) {
       const int idx = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(incl <= slot));
       c = c0 + idx;
-      tile = slot - (__builtin_amdgcn_readlane(incl, idx) - __builtin_amdgcn_readlane(nt, idx));
+      nt_c = __builtin_amdgcn_readlane(nt, idx);
+      tile = slot - (__builtin_amdgcn_readlane(incl, idx) - nt_c);
       break;
     }
     slot -= total;
   }
-  if (c < 0) return;  // beyond the last tile
+  if (c < 0) return;  // beyond the last tile: the whole block leaves
+  tile = nt_c - 1 - tile;  // a chunk's later (longer) tiles first
   const int4 ch = a.chunks[c];
   const int s = ch.x;
-  if (s < 0 || s >= a.n_rows || ch.w < 0 || ch.w + ch.z > a.n_tok || ch.y < 0) return;  // a chunk outside the inputs
-  const int pos0 = ch.y + 16 * tile;
-  const int qn = min(16, ch.z - 16 * tile);  // queries in this tile
-  const int t0 = ch.w + 16 * tile;
+  const int pos0 = ch.y + QT * tile;
+  const int qn = min(QT, ch.z - QT * tile);  // queries in this tile
   const int p_last = pos0 + qn - 1;
   int p0 = a.p_start ? a.p_start[s] : 0;
   p0 = min(max(p0, 0), p_last);
   const int ta = p0, tb = min(p_last + 1, a.bt_stride * kPage);
-  const bool qok = n < qn;
-  const int qpos = pos0 + n;
 
-  // q of query n, head h: dims 32j + 8g .. +7 (loaded before the pages)
-  float4v qraw[8];
-  {
-    const float4v* qsrc =
-        reinterpret_cast<const float4v*>(a.q + ((size_t)(t0 + (qok ? n : 0)) * a.n_heads + h) * kD + 8 * g);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      qraw[2 * j] = qsrc[8 * j];
-      qraw[2 * j + 1] = qsrc[8 * j + 1];
-    }
-  }
+  // this wave: queries [wq, wq + qn_w) of the tile, heads h0 .. h0 + HW - 1
+  const int qg = w / WPQ;
+  const int qn_w = min(16, qn - 16 * qg);
+  const bool active = qn_w > 0;
+  const int wq = pos0 + 16 * qg;
+  const int tq = ch.w + QT * tile + 16 * qg;  // q/out row of query wq
+  const int h0 = kvh * REP + (w % WPQ) * HW;
+  const bool qok = n < qn_w;
+  const int qpos = wq + n;
 
-  Stream sm;
-  sm.k_pages = a.k_pages;
-  sm.v_pages = a.v_pages;
-  sm.vring = (lds_u8*)vring_[w];
-  sm.num_pages = a.num_pages;
-  sm.kvh_off = (uint32_t)kvh * kRowBytes;
-  const uint32_t rs = (uint32_t)a.n_kv * kRowBytes;
-  sm.page_bytes = kPage * rs;
-  sm.koff = (uint32_t)n * rs + 16u * g;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) sm.voff[j] = (uint32_t)(4 * g + j) * rs + 16u * ((uint32_t)n ^ v_swz(4 * j + g));
-  {
-    const int R = 4 * (n >> 2) + g;
-    sm.vr_off = (uint32_t)R * kRowBytes;
-    sm.vr_swz = v_swz(R);
-    sm.vr_half = 8u * (n & 1);
-    sm.vr_sub = (uint32_t)((n & 3) >> 1);
-  }
-
-  // table window of 64 entries (lane j: entry base + j), as in run_piece
+  // table window of 64 entries (lane j: entry base + j)
   const uint32_t* bt_row = a.bt + (size_t)s * a.bt_stride;
   const int pg_first = ta / kPage;
   const int npg = ta < tb ? (tb - 1) / kPage - pg_first + 1 : 0;
+  const int npairs = (npg + 1) / 2;
   int base = pg_first;
   uint32_t btv = 0;
   auto load_window = [&]() {
@@ -1134,7 +1212,7 @@ __global__ __launch_bounds__(kWave * REP) void prefill_mfma_kernel(PrefillArgs a
     wait_vmcnt<0>();
   };
   load_window();
-  auto phys_of = [&](int i) -> uint32_t {
+  auto phys_of = [&](int i) -> uint32_t {  // i increases from call to call
     int idx = pg_first + i - base;
     if (idx >= 64) {
       base += 64;
@@ -1144,93 +1222,146 @@ __global__ __launch_bounds__(kWave * REP) void prefill_mfma_kernel(PrefillArgs a
     return __builtin_amdgcn_readlane(btv, idx);
   };
 
-  half8 kbuf[DEPTH][4];
-  bool vld[DEPTH];
-#pragma unroll
-  for (int d = 0; d < DEPTH; ++d) vld[d] = issue_page(sm, phys_of(d), d, kbuf[d]) && npg > d;
-
-  // q -> B operands: per query, scale by 2^-E (E from max |q * scale|) so
-  // that hi and lo stay in f16 range; scores are scaled back by 2^E
-  half8 qh[4], ql[4];
-  float qexp;
+  // q of query n, head h0 + hh: dims 32j + 8g .. +7, loaded before the pages
+  float4v qraw[HW][8];
   {
+    const int trow = qok ? tq + n : ch.w;
+#pragma unroll
+    for (int hh = 0; hh < HW; ++hh) {
+      const float4v* qsrc = reinterpret_cast<const float4v*>(a.q + ((size_t)trow * a.n_heads + h0 + hh) * kD + 8 * g);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        qraw[hh][2 * j] = qsrc[8 * j];
+        qraw[hh][2 * j + 1] = qsrc[8 * j + 1];
+      }
+    }
+  }
+
+  PfLanes pl;
+  const uint32_t rs = (uint32_t)a.n_kv * kRowBytes;
+  const uint32_t page_bytes = kPage * rs;
+  const uint32_t kvh_off = (uint32_t)kvh * kRowBytes;
+  {
+    const uint32_t R = 4u * (uint32_t)w + (uint32_t)g;
+    pl.koff = R * rs + 16u * ((uint32_t)n ^ R);
+    pl.voff = (uint32_t)(4 * g + w) * rs + 16u * ((uint32_t)n ^ v_swz((int)R));
+    pl.lds_q = 1024u * (uint32_t)w;
+    pl.krow = (uint32_t)n * kRowBytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pl.kchunk[j] = 16u * ((uint32_t)(4 * j + g) ^ (uint32_t)n);
+    const int Rv = 4 * (n >> 2) + g;
+    pl.vr_off = (uint32_t)Rv * kRowBytes;
+    pl.vr_swz = v_swz(Rv);
+    pl.vr_half = 8u * (n & 1);
+    pl.vr_sub = (uint32_t)((n & 3) >> 1);
+  }
+  lds_u8* ring = (lds_u8*)ring_;
+
+  // pair i -> ring slot i % 3; validity bits of the slot's two pages
+  uint32_t vbits = 0;
+  auto issue = [&](int i) {
+    const int sl = i % kPfDepth;
+    const uint32_t ph0 = phys_of(2 * i);
+    const uint32_t ph1 = 2 * i + 1 < npg ? phys_of(2 * i + 1) : 0xFFFFFFFFu;
+    const uint32_t bits = (ph0 < a.num_pages ? 1u : 0u) | (ph1 < a.num_pages ? 2u : 0u);
+    vbits = (vbits & ~(3u << (2 * sl))) | (bits << (2 * sl));
+    pf_issue(a, pl, page_bytes, kvh_off, ring + sl * kPfSlot, ph0, ph1);
+  };
+  if (npairs > 0) issue(0);
+  if (npairs > 1) issue(1);
+
+  // q -> B operands: per query and head, scale by 2^-E (E from max |q *
+  // scale|) so that hi and lo stay in f16 range; scores are scaled back by 2^E
+  half8 qh[HW][4], ql[HW][4];
+  float qexp[HW];
+#pragma unroll
+  for (int hh = 0; hh < HW; ++hh) {
     float amax = 0.0f;
 #pragma unroll
     for (int r = 0; r < 8; ++r)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(qraw[r][e] * a.scale_log2));
+      for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(qraw[hh][r][e] * a.scale_log2));
     amax = max_xor16(max_xor32(amax));  // over the 4 lanes of query n
     int E = 0;
     if (amax > 0.0f && amax < INFINITY) (void)frexpf(amax, &E);
     const float inv = ldexpf(1.0f, -E);
-    qexp = ldexpf(1.0f, E);
+    qexp[hh] = ldexpf(1.0f, E);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float y = qok ? qraw[2 * j + (e >> 2)][e & 3] * a.scale_log2 * inv : 0.0f;
+        const float y = qok ? qraw[hh][2 * j + (e >> 2)][e & 3] * a.scale_log2 * inv : 0.0f;
         const _Float16 hi = (_Float16)y;
-        qh[j][e] = hi;
-        ql[j][e] = (_Float16)(y - (float)hi);
+        qh[hh][j][e] = hi;
+        ql[hh][j][e] = (_Float16)(y - (float)hi);
       }
   }
-  float4v acc[8];
+  float4v acc[HW][8];
+  float m[HW], l[HW];
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-  float m = kMInit, l = 0.0f;
+  for (int hh = 0; hh < HW; ++hh) {
+    m[hh] = kMInit;
+    l[hh] = 0.0f;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc[hh][nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  }
 
-  // page i: wait for its loads (the page issued after it stays in flight),
-  // consume, refill the slot with page i + DEPTH
-  auto step = [&](int i, half8(&k)[4], bool& valid, int sl, bool steady) {
-    const int ahead = steady ? DEPTH - 1 : min(npg - 1 - i, DEPTH - 1);
-    if (ahead >= 1)
-      wait_vmcnt<8>();
+  for (int i = 0; i < npairs; ++i) {
+    if (i + 1 < npairs)
+      wait_vmcnt<4>();  // pair i landed; pair i + 1 stays in flight
     else
       wait_vmcnt<0>();
-    const int tok0 = (pg_first + i) * kPage;
-    if (steady && valid && tok0 >= ta && tok0 + kPage <= tb && tok0 + kPage - 1 <= pos0)
-      consume_prefill<true>(acc, m, l, qh, ql, qexp, sm, k, sl, tok0, valid, ta, tb, qpos, qok, g, n);
-    else
-      consume_prefill<false>(acc, m, l, qh, ql, qexp, sm, k, sl, tok0, valid, ta, tb, qpos, qok, g, n);
-    if (steady || i + DEPTH < npg) valid = issue_page(sm, phys_of(i + DEPTH), sl, k);
-  };
-  int i = 0;
-  for (; i + 2 * DEPTH - 1 < npg; i += DEPTH) {
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) step(i + d, kbuf[d], vld[d], d, true);
+    pf_barrier();  // every wave's quarter of pair i landed; pair i - 1 is consumed
+    if (i + 2 < npairs) issue(i + 2);  // into pair i - 1's slot
+    if (active) {
+      const int sl = i % kPfDepth;
+      lds_u8* sp = ring + sl * kPfSlot;
+      const bool v0 = (vbits >> (2 * sl)) & 1u, v1 = (vbits >> (2 * sl + 1)) & 1u;
+      const int tok0 = (pg_first + 2 * i) * kPage;
+      const bool whole = v0 && v1 && tok0 >= ta && tok0 + 2 * kPage <= tb;
+      if (whole && tok0 + 2 * kPage - 1 <= wq)
+        pf_consume<HW, 0>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qok, g, n);
+      else if (whole)
+        pf_consume<HW, 1>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qok, g, n);
+      else
+        pf_consume<HW, 2>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qok, g, n);
+    }
   }
-#pragma unroll
-  for (int d = 0; d < 2 * DEPTH - 1; ++d)
-    if (i + d < npg) step(i + d, kbuf[d % DEPTH], vld[d % DEPTH], d % DEPTH, false);
-  wait_vmcnt<0>();  // stand-in pages of a tile with fewer than DEPTH pages
+  if (!active) return;
 
-  // l over the 16 tokens of each page: sum the four lanes of query n
-  const float lt = sum_xor16(sum_xor32(l));
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii) {
-    const float L = __shfl(lt, 20 * g + ii, kWave);  // query 4g + ii
-    const int qq = 4 * g + ii;
-    if (qq < qn) {
-      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      float* orow = a.out + ((size_t)(t0 + qq) * a.n_heads + h) * kD;
+  for (int hh = 0; hh < HW; ++hh) {
+    // l over the 32 tokens of each pair: sum the four lanes of query n
+    const float lt = sum_xor16(sum_xor32(l[hh]));
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) orow[16 * nb + n] = acc[nb][ii] * inv;
+    for (int ii = 0; ii < 4; ++ii) {
+      const float L = __shfl(lt, 20 * g + ii, kWave);  // query 4g + ii
+      const int qq = 4 * g + ii;
+      if (qq < qn_w) {
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        float* orow = a.out + ((size_t)(tq + qq) * a.n_heads + h0 + hh) * kD;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) orow[16 * nb + n] = acc[hh][nb][ii] * inv;
+      }
     }
   }
 }
 
 template <int REP>
-void launch_prefill_rep(const PrefillArgs& a, int n_tile_slots, hipStream_t st) {
-  prefill_mfma_kernel<REP><<<dim3((unsigned)n_tile_slots, (unsigned)a.n_kv), kWave * REP, 0, st>>>(a);
+void launch_prefill_rep(const PrefillArgs& a, int n_tiles, hipStream_t st) {
+  const unsigned blocks = (unsigned)n_tiles * (unsigned)a.n_kv;
+  prefill_mfma_kernel<REP><<<blocks, kWave * kPfWaves, 0, st>>>(a);
 }
 }  // namespace
 
-int launch_prefill_mfma(const PrefillArgs& a, int rep, int n_tile_slots, hipStream_t st) {
+int prefill_queries_per_tile(int rep) { return rep == 8 ? PfShape<8>::QT : PfShape<4>::QT; }
+
+int launch_prefill_mfma(const PrefillArgs& a, int rep, int n_tiles, hipStream_t st) {
   switch (rep) {
-    case 1: launch_prefill_rep<1>(a, n_tile_slots, st); break;
-    case 2: launch_prefill_rep<2>(a, n_tile_slots, st); break;
-    case 4: launch_prefill_rep<4>(a, n_tile_slots, st); break;
-    case 8: launch_prefill_rep<8>(a, n_tile_slots, st); break;
+    case 1: launch_prefill_rep<1>(a, n_tiles, st); break;
+    case 2: launch_prefill_rep<2>(a, n_tiles, st); break;
+    case 4: launch_prefill_rep<4>(a, n_tiles, st); break;
+    case 8: launch_prefill_rep<8>(a, n_tiles, st); break;
     default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
   }
   return hip_check("prefill kernel launch");

@@ -367,7 +367,9 @@ struct PrefillArgs {
   uint32_t num_pages;
   float scale_log2;
 };
-int launch_prefill_mfma(const PrefillArgs& a, int rep, int n_tile_slots, hipStream_t st);
+// Queries per tile of the prefill kernel (a workgroup per tile and kv head).
+int prefill_queries_per_tile(int rep);
+int launch_prefill_mfma(const PrefillArgs& a, int rep, int n_tiles, hipStream_t st);
 
 int hip_check(const char* what);
 // A device buffer the library keeps per device and grows on demand (hipMalloc;

@@ -790,10 +790,13 @@ int lnskv_prefill_attention(const lnskv_pages* c, const float* q, float* out, co
   a.n_heads = n_heads;
   a.num_pages = c->num_pages;
   a.scale_log2 = scale * kLog2e;
-  // at most one partly filled tile per chunk beyond n_tok / 16 full ones
-  const int64_t slots = ((int64_t)n_tok + 15) / 16 + n_chunks;
-  if (slots > INT32_MAX) return fail(LNSKV_ERR_INVALID, "too many query tiles");
-  return launch_prefill_mfma(a, n_heads / (int)c->n_kv_heads, (int)slots, (hipStream_t)stream);
+  // at most one partly filled tile per chunk beyond n_tok / qt full ones;
+  // blocks past the chunks' real tile count leave at once
+  const int rep = n_heads / (int)c->n_kv_heads;
+  const int64_t qt = prefill_queries_per_tile(rep);
+  const int64_t tiles = ((int64_t)n_tok + qt - 1) / qt + n_chunks;
+  if (tiles * c->n_kv_heads > INT32_MAX) return fail(LNSKV_ERR_INVALID, "too many query tiles");
+  return launch_prefill_mfma(a, rep, (int)tiles, (hipStream_t)stream);
 }
 
 int lnskv_split_gated_query(const float* input, float* q_out, float* gate_out, int32_t n_rows, int32_t n_heads,
