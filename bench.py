@@ -186,22 +186,42 @@ def oproj_measure(w, runner, dev, reps: int) -> dict | None:
 
 def prefill_measure(w, runner, dev, reps: int, chunk: int = 256) -> dict | None:
     """Chunked-prefill attention (lnskv_prefill_attention) over the config's
-    pages: the last `chunk` tokens of every decoding sequence are taken as
-    its prompt chunk (their K/V are in the pages), each query attending
-    [0, its position].  Algorithmic work: 4 * head_dim flops per (query,
-    head, attended token) (q.k and p.v); the kernel runs q and p as f16 hi
-    and lo parts, twice that on the matrix cores.  Layers cycled, HIP events
-    around `reps` launches."""
+    pages.  Configs with prompt chunks (c4) use those chunks (every step
+    appends their K/V); the others take the last `chunk` tokens of every
+    decoding sequence as its prompt chunk (their K/V are in the pages).  Each
+    query attends [0, its position].  Algorithmic work: 4 * head_dim flops
+    per (query, head, attended token) (q.k and p.v); the kernel runs q and p
+    as f16 hi and lo parts, twice that on the matrix cores.  Layers cycled,
+    HIP events around `reps` launches.  For config chunks the same queries
+    also go through lnskv_decode as one row each (kv_len = position + 1: the
+    reference's token-at-a-time order of work, batched into one launch), and
+    the two results are compared."""
+    import numpy as np
     import torch
 
-    if reps <= 0 or runner.n_dec == 0 or w.dtype != 1 or w.head_dim != 128:
+    if reps <= 0 or w.dtype != 1 or w.head_dim != 128:
         return None
+    cs, cp = w.chunk_tokens()
     desc, tok = [], 0
-    for s in runner.dec_rows:
-        L = int(w.kv_len[s])
-        ln = min(chunk, L)
-        desc.append((int(s), L - ln, ln, tok))
-        tok += ln
+    if len(cs):
+        i = 0
+        while i < len(cs):
+            j = i
+            while j + 1 < len(cs) and cs[j + 1] == cs[i] and cp[j + 1] == cp[j] + 1:
+                j += 1
+            desc.append((int(cs[i]), int(cp[i]), j - i + 1, i))
+            i = j + 1
+        tok = len(cs)
+        what = f"the config's {len(desc)} prompt chunks ({tok} queries)"
+    else:
+        if runner.n_dec == 0:
+            return None
+        for s in runner.dec_rows:
+            L = int(w.kv_len[s])
+            ln = min(chunk, L)
+            desc.append((int(s), L - ln, ln, tok))
+            tok += ln
+        what = f"last {chunk} tokens of each of {len(desc)} sequences ({tok} queries)"
     chunks = torch.tensor(desc, dtype=torch.int32, device=dev)
     q = torch.randn(tok, w.n_heads, w.head_dim, device=dev)
     out = torch.empty_like(q)
@@ -211,22 +231,47 @@ def prefill_measure(w, runner, dev, reps: int, chunk: int = 256) -> dict | None:
         runner.layers[i % len(runner.layers)].prefill_attention(q, chunks, runner.tables, n_heads=w.n_heads,
                                                                scale=w.scale, out=out)
 
-    for i in range(2 * len(runner.layers)):
-        launch(i)
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for i in range(reps):
-        launch(i)
-    e.record()
-    torch.cuda.synchronize()
-    dt = s.elapsed_time(e) / 1e3 / reps
-    return {"shape": f"last {chunk} tokens of each of {len(desc)} sequences ({tok} queries), "
-                     f"Hq{w.n_heads}/Hkv{w.n_kv}/d{w.head_dim} f16 pages",
-            "us_per_launch": round(dt * 1e6, 1), "gflop": round(flops / 1e9, 2),
-            "tflop_per_s": round(flops / dt / 1e12, 1),
-            "frac_of_f16_mfma_peak": round(flops / dt / 1e12 / 2500.0, 4),
-            "mfma_tflop_per_s_with_hi_lo": round(2 * flops / dt / 1e12, 1)}
+    def timed(fn):
+        for i in range(2 * len(runner.layers)):
+            fn(i)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(reps):
+            fn(i)
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / 1e3 / reps
+
+    dt = timed(launch)
+    res = {"shape": f"{what}, Hq{w.n_heads}/Hkv{w.n_kv}/d{w.head_dim} f16 pages",
+           "us_per_launch": round(dt * 1e6, 1), "gflop": round(flops / 1e9, 2),
+           "tflop_per_s": round(flops / dt / 1e12, 1),
+           "frac_of_f16_mfma_peak": round(flops / dt / 1e12 / 2500.0, 4),
+           "mfma_tflop_per_s_with_hi_lo": round(2 * flops / dt / 1e12, 1)}
+    if len(cs) and tok <= 4096:
+        # the same queries as single-token decode rows of one lnskv_decode call
+        tables = runner.tables[torch.from_numpy(cs.astype(np.int64)).to(dev)].contiguous()
+        kv_len = torch.from_numpy((cp + 1).astype(np.int32)).to(dev)
+        pk0 = runner.layers[0]
+        ws = torch.zeros(max(pk0.workspace_size(tok, w.n_heads, int(cp.max()) + 1, 0), 4), dtype=torch.uint8,
+                         device=dev)
+        out_d = torch.empty_like(q)
+
+        def launch_d(i):
+            runner.layers[i % len(runner.layers)].decode(q, tables, kv_len, n_heads=w.n_heads,
+                                                         max_kv_len=int(cp.max()) + 1, scale=w.scale,
+                                                         workspace=ws, out=out_d)
+
+        dt_d = timed(launch_d)
+        launch(0)
+        launch_d(0)
+        torch.cuda.synchronize()
+        diff = float((out - out_d).abs().max() / out_d.abs().max())
+        res.update({"decode_rows_us_per_launch": round(dt_d * 1e6, 1),
+                    "prefill_speedup_vs_decode_rows": round(dt_d / dt, 2),
+                    "max_abs_diff_vs_decode_rows_rel": diff})
+    return res
 
 
 def measured_traffic(name: str):

@@ -952,13 +952,14 @@ template int launch_decode_mfma_sk<true>(const DecodeArgs&, int, int, int, hipSt
 // query at position P attends the window [p_start, P] of its sequence, as the
 // decode would with kv_len = P + 1.
 //
-// Workgroup = (tile of QT queries of one chunk, kv head), four waves.  The
+// Workgroup = (tile of QT queries of one chunk, kv head), eight waves.  The
 // workgroup streams the tile's window two pages (32 tokens) at a time through
-// a three-slot LDS ring: each wave DMAs one quarter of every page's K and V
-// rows, a barrier publishes the pair, and all four waves read it from LDS, so
-// a page is fetched once per tile.  Wave w serves the 16 queries of query
-// group w / WPQ and HW = min(REP, 4) query heads (head set w % WPQ); the K and
-// V operands it reads from LDS serve all HW heads.
+// a three-slot LDS ring: each wave DMAs a quarter of two of the pair's four
+// page regions (K and V of each page), a barrier publishes the pair, and all
+// waves read it from LDS, so a page is fetched once per tile.  Wave w serves
+// the 16 queries of query group w / WPQ and HW = min(REP, 2) query heads
+// (head set w % WPQ); the K and V operands it reads from LDS serve all HW
+// heads.  QT = 64 queries for REP <= 4, 32 for REP = 8.
 //
 // Per pair and head, lane (g, n) = (lane / 16, lane % 16):
 //  Q.K^T  per page, S^T[16 tok][16 query] = K . Q^T as 4 x 2
@@ -986,15 +987,21 @@ template int launch_decode_mfma_sk<true>(const DecodeArgs&, int, int, int, hipSt
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int kPfWaves = 4;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 constexpr int kPfSlot = 4 * kVSlot;  // K and V of two pages
 constexpr int kPfDepth = 3;          // ring slots: one pair consumed, two in flight
 
+// Two query heads per wave and eight waves per workgroup (two per SIMD, 256
+// VGPRs each): measured against four heads with four waves (one per SIMD,
+// 20% slower), one head with eight waves (16% slower) and two heads with
+// four waves, two workgroups per CU (35% slower) on c2's pages.
 template <int REP>
 struct PfShape {
-  static constexpr int HW = REP < 4 ? REP : 4;        // query heads per wave
-  static constexpr int WPQ = REP / HW;                 // waves per 16 queries
-  static constexpr int QT = 16 * (kPfWaves / WPQ);     // queries per tile
+  static constexpr int HW = REP < 2 ? REP : 2;  // query heads per wave
+  static constexpr int WPQ = REP / HW;           // waves per 16 queries
+  static constexpr int NW = 8;                   // waves per workgroup
+  static constexpr int QT = 16 * (NW / WPQ);     // queries per tile
+  static constexpr int RPW = 16 / NW;                          // page regions a wave DMAs per pair
 };
 
 // Workgroup barrier after this wave's LDS accesses have completed.  No
@@ -1009,26 +1016,27 @@ struct PfLanes {
   uint32_t lds_q;   // 1024 w: this wave's quarter of a page region
   uint32_t krow;    // K reads: row n
   uint32_t kchunk[4];  // 16 * ((4j + g) ^ n)
-  uint32_t vr_off, vr_swz, vr_half, vr_sub;  // transposed V reads, as Stream
+  uint32_t vrd[8];   // transposed V reads of dims 16 nb ..: row, half and swizzled chunk, as Stream
 };
 
-// DMA of this wave's quarter of pages ph0 and ph1 (K and V) into `slot`:
-// exactly 4 vector-memory instructions.  A missing page reads page 0 (in
-// bounds); its tokens are masked and its V rows zeroed before use.
+// DMA of this wave's share of pages ph0 and ph1 into `slot`: quarter w % 4
+// of page regions (w / 4) * RPW .. + RPW - 1 (region r: K of page r for r < 2,
+// V of page r - 2 otherwise), RPW vector-memory instructions.  A missing page
+// reads page 0 (in bounds); its tokens are masked and its V rows zeroed
+// before use.
+template <int RPW>
 __device__ __forceinline__ void pf_issue(const PrefillArgs& a, const PfLanes& pl, uint32_t page_bytes,
-                                         uint32_t kvh_off, lds_u8* slot, uint32_t ph0, uint32_t ph1) {
+                                         uint32_t kvh_off, lds_u8* slot, uint32_t ph0, uint32_t ph1, int w) {
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const uint32_t ph = p ? ph1 : ph0;
+  for (int t = 0; t < RPW; ++t) {
+    const int r = (w >> 2) * RPW + t;  // wave-uniform
+    const uint32_t ph = (r & 1) ? ph1 : ph0;
     const size_t base = (size_t)(ph < a.num_pages ? ph : 0u) * page_bytes + kvh_off;
-    const __amdgpu_buffer_rsrc_t rk =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(a.k_pages + base), (short)0, (int)page_bytes, kBufferFormat);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(slot + p * kVSlot + pl.lds_q),
-                                             16, (int)pl.koff, 0, 0, 0);
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(a.v_pages + base), (short)0, (int)page_bytes, kBufferFormat);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rv, (__attribute__((address_space(3))) void*)(slot + (2 + p) * kVSlot + pl.lds_q), 16, (int)pl.voff, 0, 0, 0);
+    const uint8_t* src = (r >> 1) ? a.v_pages : a.k_pages;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(src + base), (short)0, (int)page_bytes, kBufferFormat);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(slot + r * kVSlot + pl.lds_q),
+                                             16, (int)((r >> 1) ? pl.voff : pl.koff), 0, 0, 0);
   }
 }
 
@@ -1062,10 +1070,10 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
     asm volatile("ds_read_b128 %0, %1" : "=v"(k[0][j]) : "v"(kb + pl.kchunk[j]) : "memory");
     asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(k[1][j]) : "v"(kb + pl.kchunk[j]) : "memory");
   }
-  const uint32_t vb = (uint32_t)(size_t)slot + 2 * kVSlot + pl.vr_off + pl.vr_half;
+  const uint32_t vb = (uint32_t)(size_t)slot + 2 * kVSlot;
   short4v bv[2][8];
   auto read_v = [&](int nb) {
-    const uint32_t a0 = vb + 16u * ((((uint32_t)(2 * nb)) + pl.vr_sub) ^ pl.vr_swz);
+    const uint32_t a0 = vb + pl.vrd[nb];
     asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[0][nb]) : "v"(a0) : "memory");
     asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(bv[1][nb]) : "v"(a0) : "memory");
   };
@@ -1100,9 +1108,10 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
                : "memory");
 #pragma unroll
   for (int hh = 0; hh < HW; ++hh) {
+    // raw scores (still scaled by 2^-E); masked tokens -inf
     float s[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s[e] = sacc[hh][e >> 2][e & 3] * qexp[hh];
+    for (int e = 0; e < 8; ++e) s[e] = sacc[hh][e >> 2][e & 3];
     if constexpr (MODE != 0) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -1111,7 +1120,7 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
       }
     }
     float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-    mx = max_xor16(max_xor32(mx));  // over the 32 tokens of query n
+    mx = max_xor16(max_xor32(mx)) * qexp[hh];  // over the 32 tokens of query n; 2^E scaling is exact
     const bool need = mx > m[hh] + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform
       const float m_new = need ? mx : m[hh];
@@ -1126,15 +1135,22 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
         for (int nb = 0; nb < 8; ++nb) acc[hh][nb][ii] *= aq;
       }
     }
+    // p = 2^(s 2^E - m) (the product is exact, so one rounding as s - m);
+    // hi = f16(p) to nearest even, lo = f16(p - hi), converted in pairs
+    const float nm = -m[hh];
     half8 ph, plo;
     float lsum = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float p = fast_exp2(s[e] - m[hh]);
-      lsum += p;
-      const _Float16 hi = (_Float16)p;
-      ph[e] = hi;
-      plo[e] = (_Float16)(p - (float)hi);
+    for (int e = 0; e < 8; e += 2) {
+      const float2v pp = {fast_exp2(fmaf(s[e], qexp[hh], nm)), fast_exp2(fmaf(s[e + 1], qexp[hh], nm))};
+      lsum += pp[0] + pp[1];
+      const half2v h = __builtin_convertvector(pp, half2v);
+      const float2v hf = __builtin_convertvector(h, float2v);
+      const half2v lo = __builtin_convertvector(float2v{pp[0] - hf[0], pp[1] - hf[1]}, half2v);
+      ph[e] = h[0];
+      ph[e + 1] = h[1];
+      plo[e] = lo[0];
+      plo[e + 1] = lo[1];
     }
     l[hh] += lsum;
 #pragma unroll
@@ -1156,8 +1172,8 @@ __device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int i) {
 }
 
 template <int REP>
-__global__ __launch_bounds__(kWave* kPfWaves) void prefill_mfma_kernel(PrefillArgs a) {
-  constexpr int HW = PfShape<REP>::HW, WPQ = PfShape<REP>::WPQ, QT = PfShape<REP>::QT;
+__global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(PrefillArgs a) {
+  constexpr int HW = PfShape<REP>::HW, WPQ = PfShape<REP>::WPQ, QT = PfShape<REP>::QT, RPW = PfShape<REP>::RPW;
   __shared__ __attribute__((aligned(16))) uint8_t ring_[kPfDepth * kPfSlot];
   const int lane = (int)(threadIdx.x & (kWave - 1)), w = (int)(threadIdx.x / kWave);
   const int g = lane >> 4, n = lane & 15;
@@ -1165,7 +1181,7 @@ __global__ __launch_bounds__(kWave* kPfWaves) void prefill_mfma_kernel(PrefillAr
   // block -> (chunk, tile, kv head); the kv head varies fastest
   const int kvh = (int)(blockIdx.x % (unsigned)a.n_kv);
   int slot = (int)(blockIdx.x / (unsigned)a.n_kv), c = -1, tile = 0, nt_c = 0;
-  for (int c0 = 0; c0 < a.n_chunks; c0 += kWave) {  // wave-uniform; identical in the four waves
+  for (int c0 = 0; c0 < a.n_chunks; c0 += kWave) {  // wave-uniform; identical in every wave
     const int nt = pf_tiles<QT>(a, c0 + lane);
     const int incl = wave_incl_scan(nt);
     const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
@@ -1242,18 +1258,18 @@ __global__ __launch_bounds__(kWave* kPfWaves) void prefill_mfma_kernel(PrefillAr
   const uint32_t page_bytes = kPage * rs;
   const uint32_t kvh_off = (uint32_t)kvh * kRowBytes;
   {
-    const uint32_t R = 4u * (uint32_t)w + (uint32_t)g;
+    const int j = w & 3;  // this wave's quarter of a page region
+    const uint32_t R = 4u * (uint32_t)j + (uint32_t)g;
     pl.koff = R * rs + 16u * ((uint32_t)n ^ R);
-    pl.voff = (uint32_t)(4 * g + w) * rs + 16u * ((uint32_t)n ^ v_swz((int)R));
-    pl.lds_q = 1024u * (uint32_t)w;
+    pl.voff = (uint32_t)(4 * g + j) * rs + 16u * ((uint32_t)n ^ v_swz((int)R));
+    pl.lds_q = 1024u * (uint32_t)j;
     pl.krow = (uint32_t)n * kRowBytes;
 #pragma unroll
     for (int j = 0; j < 4; ++j) pl.kchunk[j] = 16u * ((uint32_t)(4 * j + g) ^ (uint32_t)n);
     const int Rv = 4 * (n >> 2) + g;
-    pl.vr_off = (uint32_t)Rv * kRowBytes;
-    pl.vr_swz = v_swz(Rv);
-    pl.vr_half = 8u * (n & 1);
-    pl.vr_sub = (uint32_t)((n & 3) >> 1);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+      pl.vrd[nb] = (uint32_t)Rv * kRowBytes + 8u * (n & 1) + 16u * (((uint32_t)(2 * nb) + ((n & 3) >> 1)) ^ v_swz(Rv));
   }
   lds_u8* ring = (lds_u8*)ring_;
 
@@ -1265,7 +1281,7 @@ __global__ __launch_bounds__(kWave* kPfWaves) void prefill_mfma_kernel(PrefillAr
     const uint32_t ph1 = 2 * i + 1 < npg ? phys_of(2 * i + 1) : 0xFFFFFFFFu;
     const uint32_t bits = (ph0 < a.num_pages ? 1u : 0u) | (ph1 < a.num_pages ? 2u : 0u);
     vbits = (vbits & ~(3u << (2 * sl))) | (bits << (2 * sl));
-    pf_issue(a, pl, page_bytes, kvh_off, ring + sl * kPfSlot, ph0, ph1);
+    pf_issue<RPW>(a, pl, page_bytes, kvh_off, ring + sl * kPfSlot, ph0, ph1, w);
   };
   if (npairs > 0) issue(0);
   if (npairs > 1) issue(1);
@@ -1308,7 +1324,7 @@ __global__ __launch_bounds__(kWave* kPfWaves) void prefill_mfma_kernel(PrefillAr
 
   for (int i = 0; i < npairs; ++i) {
     if (i + 1 < npairs)
-      wait_vmcnt<4>();  // pair i landed; pair i + 1 stays in flight
+      wait_vmcnt<RPW>();  // pair i landed; pair i + 1 stays in flight
     else
       wait_vmcnt<0>();
     pf_barrier();  // every wave's quarter of pair i landed; pair i - 1 is consumed
@@ -1350,11 +1366,18 @@ __global__ __launch_bounds__(kWave* kPfWaves) void prefill_mfma_kernel(PrefillAr
 template <int REP>
 void launch_prefill_rep(const PrefillArgs& a, int n_tiles, hipStream_t st) {
   const unsigned blocks = (unsigned)n_tiles * (unsigned)a.n_kv;
-  prefill_mfma_kernel<REP><<<blocks, kWave * kPfWaves, 0, st>>>(a);
+  prefill_mfma_kernel<REP><<<blocks, kWave * PfShape<REP>::NW, 0, st>>>(a);
 }
 }  // namespace
 
-int prefill_queries_per_tile(int rep) { return rep == 8 ? PfShape<8>::QT : PfShape<4>::QT; }
+int prefill_queries_per_tile(int rep) {
+  switch (rep) {
+    case 1: return PfShape<1>::QT;
+    case 2: return PfShape<2>::QT;
+    case 4: return PfShape<4>::QT;
+    default: return PfShape<8>::QT;
+  }
+}
 
 int launch_prefill_mfma(const PrefillArgs& a, int rep, int n_tiles, hipStream_t st) {
   switch (rep) {
