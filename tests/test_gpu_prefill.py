@@ -84,3 +84,21 @@ def test_prefill_small_cases(gpu, rep):
 def test_prefill_long_chunks(gpu):
     chunks = [(0, 1400, 128), (1, 1600, 128)]
     _run(gpu, 4, chunks, [(1400 + 128 + 15) // 16, (1600 + 128 + 15) // 16], n_kv=8, seed=11)
+
+
+def test_prefill_many_chunks(gpu):
+    """70 chunks (past one 64-chunk scan group), lengths 1..40, some sharing a
+    table row at different offsets, one outside the tables (skipped)."""
+    rng = np.random.default_rng(5)
+    n_rows = 24
+    ctx_pages = [int(x) for x in rng.integers(2, 12, n_rows)]
+    chunks = []
+    for i in range(70):
+        row = i % n_rows
+        cap = ctx_pages[row] * 16
+        ln = int(rng.integers(1, 41))
+        pos0 = int(rng.integers(0, cap - ln + 1))
+        chunks.append((row, pos0, ln))
+    chunks[33] = (n_rows + 3, 0, 8)
+    for rep in (4, 8):
+        _run(gpu, rep, chunks, ctx_pages, seed=20 + rep)
