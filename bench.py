@@ -45,6 +45,9 @@ def parse():
     p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     p.add_argument("--layers", type=int, default=4, help="pools cycled across steps (defeats the LLC)")
     p.add_argument("--split", type=int, default=-1, help="split-K tokens (-1 = the config's choice)")
+    p.add_argument("--kv-dtype", default="config", choices=["config", "f32", "f16", "q8a"],
+                   help="page type of c2 (config: f16 as the config states; q8a is the reference's own paged "
+                        "type, f32 the wide one)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample budget (0 = skip)")
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = all cores the process may use")
     p.add_argument("--copy-mb", type=int, default=1024,
@@ -350,7 +353,13 @@ def main():
     if args.copy_only:
         print(json.dumps({"copy_ceiling": copy_ceiling(dev, args.copy_mb or 1024)}), flush=True)
         return
-    w = make(args.config)
+    if args.kv_dtype != "config":
+        if args.config != "c2":
+            print("--kv-dtype applies to c2 only", file=sys.stderr)
+            sys.exit(2)
+        w = make(args.config, dtype={"f32": 0, "f16": 1, "q8a": 2}[args.kv_dtype])
+    else:
+        w = make(args.config)
     if args.split >= 0:
         w.split = args.split
     rope = None
@@ -415,8 +424,8 @@ def main():
         "data": "synthetic (seeded N(0,1)*scale pages, seeded SplitMix64 lengths and page order)",
         "config": {
             "workload": {"c1": "c1 single sequence Hq32/Hkv4/d64 f32 ctx 512",
-                         "c2": "c2 Llama-3-8B layer Hq32/Hkv8/d128 f16 pages, B=32, ctx U[512,4096], "
-                               "1-token append + decode",
+                         "c2": f"c2 Llama-3-8B layer Hq32/Hkv8/d128 {('f32', 'f16', 'q8a')[w.dtype]} pages, B=32, "
+                               "ctx U[512,4096], 1-token append + decode",
                          "c3": "c3 Hq32/Hkv8/d128 f16, B=4 x 32768, split-K 512",
                          "c4": "c4 16 x 256-token chunk appends + 48 decodes at U[1024,8192]",
                          "c5": "c5 B=128 churn: 32 freed/reallocated, 8 CoW forks, 136 decodes"}[w.name],

@@ -59,6 +59,7 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
+typedef unsigned int uint2v __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) short4v lds_short4v;
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -186,9 +187,14 @@ __device__ __forceinline__ bool issue_page(const Stream& sm, uint32_t ph, int sl
   return valid;
 }
 
-template <int REP, bool FULL>
+// SC (Q8A pages): k and the V slot hold the int8 codes as f16; the scores of
+// tokens 4g+ii are multiplied by their K scale ksc[ii] and the weights that
+// multiply V by the V scale vsc[ii] (the sums l stay unscaled).
+template <int REP, bool FULL, bool SC = false>
 __device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& sm, const half8 (&k)[4], int slot,
-                                             int tok0, bool valid, int ta, int tb, int g, int n) {
+                                             int tok0, bool valid, int ta, int tb, int g, int n,
+                                             float4v ksc = float4v{1.0f, 1.0f, 1.0f, 1.0f},
+                                             float4v vsc = float4v{1.0f, 1.0f, 1.0f, 1.0f}) {
   lds_u8* vslot = sm.vring + slot * kVSlot;
   if constexpr (!FULL) {
     // rows of masked tokens (and of a missing page) must not carry NaN bits
@@ -207,6 +213,10 @@ __device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& s
   float s[4];
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) s[ii] = (sacc[ii] + dpp_mov<kDppRowShl + REP>(sacc[ii])) * st.qexp;
+  if constexpr (SC) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) s[ii] *= ksc[ii];
+  }
   if constexpr (!FULL) {
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
@@ -231,6 +241,25 @@ __device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& s
 
   // A operand of P.V: row n < REP: f16(p) of head n; REP <= n < 2REP: the
   // remainder of head n-REP; other rows zero.
+  // SC: the weights carry vs / vmax (vmax the page's largest V scale) so
+  // that their f16 lo parts stay normal numbers, and the page's products are
+  // multiplied by vmax in f32.  Masked tokens' scales (stale bytes) are left
+  // out of the max.
+  float vmax = 1.0f;
+  if constexpr (SC) {
+    if constexpr (!FULL) {
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int t = tok0 + 4 * g + ii;
+        if (!(valid && t >= ta && t < tb)) vsc[ii] = 0.0f;
+      }
+    }
+    vmax = fmaxf(fmaxf(vsc[0], vsc[1]), fmaxf(vsc[2], vsc[3]));
+    vmax = max_xor16(max_xor32(vmax));  // over the page's 16 tokens
+    const float inv = vmax > 0.0f ? 1.0f / vmax : 0.0f;
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) pr[ii] *= vsc[ii] * inv;
+  }
   half4 pa;
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) {
@@ -259,7 +288,14 @@ __device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& s
                : "memory");
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb)
-    st.acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]), st.acc[nb], 0, 0, 0);
+    if constexpr (SC) {
+      const float4v t = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]),
+                                                             float4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st.acc[nb][e] = fmaf(vmax, t[e], st.acc[nb][e]);
+    } else {
+      st.acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]), st.acc[nb], 0, 0, 0);
+    }
 }
 
 // Loads of one piece that do not depend on the sequence's length, issued
@@ -320,6 +356,104 @@ struct PieceOut {
   size_t pbase;
   int pstride;
 };
+
+// q -> B operand: column n < REP is hi of head n, REP <= n < 2REP lo of head
+// n-REP, others zero.  Each head is first scaled by 2^-E (E from its max
+// |q*scale|) so hi/lo stay in f16 range; the scores are scaled back by 2^E.
+template <int REP>
+__device__ __forceinline__ void init_wave_state(const DecodeArgs& a, const PieceLoads<REP>& pl, WaveState<REP>& st,
+                                                int n) {
+  const bool qcol = n < 2 * REP;
+  {
+    float x[4][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float qe = pl.qv[2 * j + (e >> 2)][e & 3];
+        x[j][e] = qcol ? qe * a.scale_log2 : 0.0f;
+        amax = fmaxf(amax, fabsf(x[j][e]));
+      }
+    amax = max_xor16(max_xor32(amax));
+    int E = 0;
+    if (amax > 0.0f && amax < INFINITY) (void)frexpf(amax, &E);
+    const float inv = ldexpf(1.0f, -E);
+    st.qexp = ldexpf(1.0f, E);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = x[j][e] * inv;
+        const _Float16 hi = (_Float16)y;
+        const _Float16 lo = (_Float16)(y - (float)hi);
+        st.qb[j][e] = n < REP ? hi : (qcol ? lo : (_Float16)0.0f);
+      }
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) st.acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    st.m = kMInit;
+    st.l = 0.0f;
+  }
+}
+
+// The end of a piece: sums over the lanes, then the normalised output rows
+// or the partial rows the piece leaves for a merge.
+template <int REP>
+__device__ __forceinline__ void finish_piece(const DecodeArgs& a, WaveState<REP>& st, int s, int kvh,
+                                             const PieceOut& po, int g, int n) {
+  // Denominators: sum this head's lanes over the four 16-lane rows.
+  st.l = sum_xor16(sum_xor32(st.l));
+  // Numerators: result row r (hi) and r + REP (lo) belong to head r.  After
+  // the sums, lanes g == 0 hold heads 0..min(REP,4)-1 and, for REP == 8,
+  // lanes g == 1 hold heads 4..7, at dims 16*nb + n.
+  constexpr int NH = REP < 4 ? REP : 4;
+  float o[NH][8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    if constexpr (REP == 1) {
+      o[0][nb] = st.acc[nb][0] + st.acc[nb][1];
+    } else if constexpr (REP == 2) {
+      o[0][nb] = st.acc[nb][0] + st.acc[nb][2];
+      o[1][nb] = st.acc[nb][1] + st.acc[nb][3];
+    } else if constexpr (REP == 4) {  // hi rows in lanes g=0, lo rows in g=1
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) o[ii][nb] = sum_xor16(st.acc[nb][ii]);
+    } else {  // REP == 8: hi rows in g=0,1, lo rows in g=2,3
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) o[ii][nb] = sum_xor32(st.acc[nb][ii]);
+    }
+  }
+  // l and m of the heads this lane writes (REP == 8: lanes g == 1 hold heads
+  // 4..7), broadcast while every lane is active: DPP reads of inactive lanes
+  // return nothing useful.
+  float lsel[NH], msel[NH];
+  static_for<NH>([&](auto c) {
+    constexpr int ii = decltype(c)::value;
+    lsel[ii] = (REP == 8 && g == 1) ? row_value<(4 + ii) % REP>(st.l) : row_value<ii>(st.l);
+    msel[ii] = (REP == 8 && g == 1) ? row_value<(4 + ii) % REP>(st.m) : row_value<ii>(st.m);
+  });
+  if (g == 0 || (REP == 8 && g == 1)) {
+    const int hb = REP == 8 ? 4 * g : 0;
+    static_for<NH>([&](auto c) {
+      constexpr int ii = decltype(c)::value;
+      const float lh = lsel[ii], mh = msel[ii];
+      if (po.final) {
+        const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + hb + ii;
+        const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) a.out[hrow * kD + 16 * nb + n] = gated(a, hrow * kD + 16 * nb + n, o[ii][nb] * inv);
+      } else {
+        const size_t pidx = po.pbase + (size_t)(hb + ii) * po.pstride;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) a.ws_acc[pidx * kD + 16 * nb + n] = o[ii][nb];
+        if (n == 0) {
+          a.ws_ml[pidx * 2 + 0] = mh;
+          a.ws_ml[pidx * 2 + 1] = lh;
+        }
+      }
+    });
+  }
+}
 
 // Attends tokens [ta, tb) of sequence s for the REP query heads of kv head
 // kvh, streaming the pages with DEPTH of them in flight (K in registers, V
@@ -488,40 +622,8 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
   }
   const bool attend_new = append && pos >= ta;
 
-  // q -> B operand: column n < REP is hi of head n, REP <= n < 2REP lo of head
-  // n-REP, others zero.  Each head is first scaled by 2^-E (E from its max
-  // |q*scale|) so hi/lo stay in f16 range; the scores are scaled back by 2^E.
   WaveState<REP> st;
-  {
-    float x[4][8];
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float qe = pl.qv[2 * j + (e >> 2)][e & 3];
-        x[j][e] = qcol ? qe * a.scale_log2 : 0.0f;
-        amax = fmaxf(amax, fabsf(x[j][e]));
-      }
-    amax = max_xor16(max_xor32(amax));
-    int E = 0;
-    if (amax > 0.0f && amax < INFINITY) (void)frexpf(amax, &E);
-    const float inv = ldexpf(1.0f, -E);
-    st.qexp = ldexpf(1.0f, E);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float y = x[j][e] * inv;
-        const _Float16 hi = (_Float16)y;
-        const _Float16 lo = (_Float16)(y - (float)hi);
-        st.qb[j][e] = n < REP ? hi : (qcol ? lo : (_Float16)0.0f);
-      }
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) st.acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-    st.m = kMInit;
-    st.l = 0.0f;
-  }
+  init_wave_state<REP>(a, pl, st, n);
 
   // Page i: wait for its loads (those of the pages issued after it may stay
   // in flight), patch in the new token if it lives there, consume, refill the
@@ -567,58 +669,167 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
   // the slots and the staged token are reused by the next piece
   __builtin_amdgcn_wave_barrier();
 
-  // Denominators: sum this head's lanes over the four 16-lane rows.
-  st.l = sum_xor16(sum_xor32(st.l));
-  // Numerators: result row r (hi) and r + REP (lo) belong to head r.  After
-  // the sums, lanes g == 0 hold heads 0..min(REP,4)-1 and, for REP == 8,
-  // lanes g == 1 hold heads 4..7, at dims 16*nb + n.
-  constexpr int NH = REP < 4 ? REP : 4;
-  float o[NH][8];
+  finish_piece<REP>(a, st, s, kvh, po, g, n);
+}
+
+// ---------------------------------------------------------------------------
+// Q8A pages (the reference's paged type: int8 codes, one f32 scale per
+// (slot, kv head), lns_decode.metal:547-593, 611-634) on the same matrix-core
+// pipeline.  A page's K rows (16 x 128 bytes) and V rows come to registers
+// as int8 with 8-byte loads, plus the K and V scales of the lane's token;
+// when the page is consumed the codes become f16 exactly (K: the A operand as
+// for f16 pages; V: written to the LDS slot in the layout the transposed
+// reads expect), and consume_page applies the scales per token: scores times
+// the K scale, softmax weights times the V scale in the P.V product (the
+// reference's q.(k8 ks) and (beta vs) v8).  Not fused with the append: a Q8A
+// append runs first (the quantizer of append_kernel).
+// ---------------------------------------------------------------------------
+
+// Exact int8 -> f16 of the four signed bytes of w: the f16 with bits
+// 0x6400 | (b + 128) is 1024 + b + 128, and subtracting 1152 leaves b.
+__device__ __forceinline__ half4 i8x4_to_f16(uint32_t w) {
+  typedef _Float16 half2q __attribute__((ext_vector_type(2)));
+  const uint32_t u = w ^ 0x80808080u;
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes u0, 0x64, u1, 0x64
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2, 0x64, u3, 0x64
+  const half2q c = {(_Float16)1152.0f, (_Float16)1152.0f};
+  const half2q x = __builtin_bit_cast(half2q, lo) - c;
+  const half2q y = __builtin_bit_cast(half2q, hi) - c;
+  return half4{x[0], x[1], y[0], y[1]};
+}
+
+__device__ __forceinline__ half8 i8x8_to_f16(uint2v w) {
+  const half4 a = i8x4_to_f16(w[0]), b = i8x4_to_f16(w[1]);
+  return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// One Q8A page in flight: K codes of token n at dims 32j + 8g.., V codes of
+// token 4g+j at the swizzled chunk n ^ sw(4j+g), the K and V scales of token
+// 4g + n%4.
+struct PageQ8 {
+  uint2v k[4];
+  uint2v v[4];
+  float ks, vs;
+};
+
+template <int REP, int DEPTH>
+__device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot, PieceLoads<REP>& pl, bool tbl_ok,
+                                             int s, int kvh, int ta, int tb, const PieceOut& po) {
+  const int lane = threadIdx.x;
+  const int g = lane >> 4, n = lane & 15;
+  constexpr int kRowQ8 = kD;  // one (token, kv head) row of int8 codes
+
+  Stream sm{};
+  sm.vring = vslot;
+  {
+    const int R = 4 * (n >> 2) + g;
+    sm.vr_off = (uint32_t)R * kRowBytes;
+    sm.vr_swz = v_swz(R);
+    sm.vr_half = 8u * (n & 1);
+    sm.vr_sub = (uint32_t)((n & 3) >> 1);
+  }
+  const uint32_t rs = (uint32_t)a.n_kv * kRowQ8;  // bytes between token rows
+  const size_t page_bytes = (size_t)kPage * rs;
+  const uint32_t kvh_off = (uint32_t)kvh * kRowQ8;
+  const uint32_t koff = (uint32_t)n * rs + 8u * g;
+  uint32_t voff[4];
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) {
-    if constexpr (REP == 1) {
-      o[0][nb] = st.acc[nb][0] + st.acc[nb][1];
-    } else if constexpr (REP == 2) {
-      o[0][nb] = st.acc[nb][0] + st.acc[nb][2];
-      o[1][nb] = st.acc[nb][1] + st.acc[nb][3];
-    } else if constexpr (REP == 4) {  // hi rows in lanes g=0, lo rows in g=1
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) o[ii][nb] = sum_xor16(st.acc[nb][ii]);
-    } else {  // REP == 8: hi rows in g=0,1, lo rows in g=2,3
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) o[ii][nb] = sum_xor32(st.acc[nb][ii]);
+  for (int j = 0; j < 4; ++j) voff[j] = (uint32_t)(4 * g + j) * rs + 8u * ((uint32_t)n ^ v_swz(4 * j + g));
+  const uint32_t soff = (uint32_t)(4 * g + (n & 3)) * (uint32_t)a.n_kv + (uint32_t)kvh;
+
+  const uint32_t* bt_row = a.bt + (size_t)s * a.bt_stride;
+  const int pg_first = ta / kPage;
+  const int npg = ta < tb ? (tb - 1) / kPage - pg_first + 1 : 0;
+  int base = pl.tbl;
+  int win = 0;
+  auto load_window = [&]() {
+    const int e = base + win + lane;
+    pl.btv = e < a.bt_stride ? bt_row[e] : 0u;
+    wait_vmcnt<0>();
+  };
+  if (!tbl_ok || pg_first < base || pg_first - base >= 64) {
+    base = pg_first;
+    load_window();
+  }
+  const int off = pg_first - base;
+  auto phys_of = [&](int i) -> uint32_t {
+    int idx = off + i - win;
+    if (idx >= 64) {
+      win += 64;
+      idx -= 64;
+      load_window();
     }
-  }
-  // l and m of the heads this lane writes (REP == 8: lanes g == 1 hold heads
-  // 4..7), broadcast while every lane is active: DPP reads of inactive lanes
-  // return nothing useful.
-  float lsel[NH], msel[NH];
-  static_for<NH>([&](auto c) {
-    constexpr int ii = decltype(c)::value;
-    lsel[ii] = (REP == 8 && g == 1) ? row_value<(4 + ii) % REP>(st.l) : row_value<ii>(st.l);
-    msel[ii] = (REP == 8 && g == 1) ? row_value<(4 + ii) % REP>(st.m) : row_value<ii>(st.m);
-  });
-  if (g == 0 || (REP == 8 && g == 1)) {
-    const int hb = REP == 8 ? 4 * g : 0;
-    static_for<NH>([&](auto c) {
-      constexpr int ii = decltype(c)::value;
-      const float lh = lsel[ii], mh = msel[ii];
-      if (po.final) {
-        const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + hb + ii;
-        const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+    return __builtin_amdgcn_readlane(pl.btv, idx);
+  };
+  asm volatile("" : "+v"(pl.btv) : : "memory");
+
+  // exactly 10 vector-memory loads; a missing page reads page 0 (masked)
+  auto issue = [&](uint32_t ph, PageQ8& pg) -> bool {
+    const bool valid = ph < a.num_pages;
+    const size_t pb = (size_t)(valid ? ph : 0u);
+    const uint8_t* kb = a.k_pages + pb * page_bytes + kvh_off;
+    const uint8_t* vb = a.v_pages + pb * page_bytes + kvh_off;
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) a.out[hrow * kD + 16 * nb + n] = gated(a, hrow * kD + 16 * nb + n, o[ii][nb] * inv);
-      } else {
-        const size_t pidx = po.pbase + (size_t)(hb + ii) * po.pstride;
+    for (int j = 0; j < 4; ++j) pg.k[j] = *reinterpret_cast<const uint2v*>(kb + koff + 32 * j);
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) a.ws_acc[pidx * kD + 16 * nb + n] = o[ii][nb];
-        if (n == 0) {
-          a.ws_ml[pidx * 2 + 0] = mh;
-          a.ws_ml[pidx * 2 + 1] = lh;
-        }
-      }
-    });
+    for (int j = 0; j < 4; ++j) pg.v[j] = *reinterpret_cast<const uint2v*>(vb + voff[j]);
+    const size_t sb = pb * kPage * (size_t)a.n_kv + soff;
+    pg.ks = a.k_scales[sb];
+    pg.vs = a.v_scales[sb];
+    return valid;
+  };
+
+  PageQ8 pbuf[DEPTH];
+  bool vld[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) vld[d] = issue(phys_of(d), pbuf[d]) && npg > d;
+  asm volatile(""
+               : "+v"(pl.qv[0]), "+v"(pl.qv[1]), "+v"(pl.qv[2]), "+v"(pl.qv[3]), "+v"(pl.qv[4]), "+v"(pl.qv[5]),
+                 "+v"(pl.qv[6]), "+v"(pl.qv[7]));
+
+  WaveState<REP> st;
+  init_wave_state<REP>(a, pl, st, n);
+
+  auto step = [&](int i, PageQ8& pg, bool& valid, bool steady) {
+    const int ahead = steady ? DEPTH - 1 : min(npg - 1 - i, DEPTH - 1);  // pages issued after page i
+    if (ahead >= 3) wait_vmcnt<30>();
+    else if (ahead == 2) wait_vmcnt<20>();
+    else if (ahead == 1) wait_vmcnt<10>();
+    else wait_vmcnt<0>();
+    const int tok0 = (pg_first + i) * kPage;
+    half8 k[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) k[j] = i8x8_to_f16(pg.k[j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *(lds_half8*)(vslot + (4 * j + g) * kRowBytes + 16 * n) = i8x8_to_f16(pg.v[j]);
+    // scales of tokens 4g+ii: lane 4*(n/4) + ii of this row holds them
+    float4v ksc, vsc;
+    ksc[0] = dpp_mov<0x00>(pg.ks);
+    ksc[1] = dpp_mov<0x55>(pg.ks);
+    ksc[2] = dpp_mov<0xAA>(pg.ks);
+    ksc[3] = dpp_mov<0xFF>(pg.ks);
+    vsc[0] = dpp_mov<0x00>(pg.vs);
+    vsc[1] = dpp_mov<0x55>(pg.vs);
+    vsc[2] = dpp_mov<0xAA>(pg.vs);
+    vsc[3] = dpp_mov<0xFF>(pg.vs);
+    if (steady && valid && tok0 >= ta && tok0 + kPage <= tb)
+      consume_page<REP, true, true>(st, sm, k, 0, tok0, valid, ta, tb, g, n, ksc, vsc);
+    else
+      consume_page<REP, false, true>(st, sm, k, 0, tok0, valid, ta, tb, g, n, ksc, vsc);
+    if (steady || i + DEPTH < npg) valid = issue(phys_of(i + DEPTH), pg);
+  };
+  int i = 0;
+  for (; i + 2 * DEPTH - 1 < npg; i += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) step(i + d, pbuf[d], vld[d], true);
   }
+#pragma unroll
+  for (int d = 0; d < 2 * DEPTH - 1; ++d)
+    if (i + d < npg) step(i + d, pbuf[d % DEPTH], vld[d % DEPTH], false);
+  wait_vmcnt<0>();  // stand-in pages of a piece with fewer than DEPTH pages
+  __builtin_amdgcn_wave_barrier();
+  finish_piece<REP>(a, st, s, kvh, po, g, n);
 }
 
 // Split-K schedule: block (kv head, partition, sequence) attends one
@@ -744,8 +955,9 @@ __device__ __forceinline__ int sk_chunk(int total, int n_waves) {
   return max(kSkMinPages, (total + n_waves - 1) / n_waves);
 }
 
-template <int REP, bool FUSED, int DEPTH, bool ROPE>
+template <int REP, bool FUSED, int DEPTH, bool ROPE, bool Q8 = false>
 __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
+  static_assert(!Q8 || (!FUSED && !ROPE), "Q8A pages: the append runs first");
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
   __shared__ __attribute__((aligned(16))) uint8_t vring_[DEPTH * kVSlot];
   __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
@@ -801,7 +1013,11 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
     po.final = i0 == 0 && i1 == np;
     po.pbase = ((size_t)wv * 2 + slot) * REP;
     po.pstride = 1;
-    run_piece<REP, FUSED, DEPTH, ROPE>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh,
+    if constexpr (Q8)
+      run_piece_q8<REP, DEPTH>(a, (lds_u8*)vring_, pl, true, s, kvh, max(p0, (pg0 + i0) * kPage),
+                               min(L, (pg0 + i1) * kPage), po);
+    else
+      run_piece<REP, FUSED, DEPTH, ROPE>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh,
                                        max(p0, (pg0 + i0) * kPage),
                           min(L, (pg0 + i1) * kPage), FUSED && i1 == np && L > 0, L - 1, po,
                           (lds_u8*)rope_table_);
@@ -875,25 +1091,39 @@ namespace {
 // issue arbitration that runs the second wave of a SIMD about 30% slower.
 constexpr int kSkDepth = 2;
 constexpr int kSkWavesPerCu = 4;
+// Q8A pages: half the bytes per page and more work per byte (int8 -> f16,
+// scales), so two waves per SIMD hide each other's per-page dependency chain:
+// c2-shaped Q8A step 57.2 us with four waves per CU, 53.7 with eight; two,
+// three or four pages in flight per wave measured the same.
+constexpr int kSkDepthQ8 = 2;
+constexpr int kSkWavesPerCuQ8 = 8;
 
-template <int REP, bool FUSED>
+template <int REP, bool FUSED, bool Q8>
 int sk_waves_of(int cus, int* waves) {
-  // the smaller occupancy of the plain and (fused) RoPE variants, so one
-  // wave count serves both
+  // f16 pages: the smaller occupancy of the plain and (fused) RoPE variants,
+  // so one wave count serves both
   int per_cu = 0, per_cu_rope = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, kSkDepth, false>, kWave,
-                                                   0) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rope, decode_sk_kernel<REP, FUSED, kSkDepth, FUSED>,
-                                                   kWave, 0) != hipSuccess ||
-      per_cu <= 0 || per_cu_rope <= 0)
-    return fail(LNSKV_ERR_HIP, "occupancy query of the stream-K decode kernel failed");
-  *waves = cus * std::min(std::min(per_cu, per_cu_rope), kSkWavesPerCu);
+  if (Q8) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, false, kSkDepthQ8, false, true>,
+                                                     kWave, 0) != hipSuccess)
+      per_cu = 0;
+    per_cu_rope = per_cu;
+  } else if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, kSkDepth, false>,
+                                                          kWave, 0) != hipSuccess ||
+             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rope, decode_sk_kernel<REP, FUSED, kSkDepth, FUSED>,
+                                                          kWave, 0) != hipSuccess) {
+    per_cu = 0;
+  }
+  if (per_cu <= 0 || per_cu_rope <= 0) return fail(LNSKV_ERR_HIP, "occupancy query of the stream-K decode kernel failed");
+  *waves = cus * std::min(std::min(per_cu, per_cu_rope), Q8 ? kSkWavesPerCuQ8 : kSkWavesPerCu);
   return LNSKV_OK;
 }
 
 template <int REP, bool FUSED>
-void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, hipStream_t st) {
-  if (FUSED && a.rope_half > 0)
+void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, bool q8, hipStream_t st) {
+  if (q8)
+    decode_sk_kernel<REP, false, kSkDepthQ8, false, true><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+  else if (FUSED && a.rope_half > 0)
     decode_sk_kernel<REP, FUSED, kSkDepth, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
   else
     decode_sk_kernel<REP, FUSED, kSkDepth, false><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
@@ -901,15 +1131,15 @@ void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, hipStream_t st) 
 }
 }  // namespace
 
-int mfma_sk_waves(int rep, bool fused, int* waves) {
+int mfma_sk_waves(int rep, bool fused, bool q8, int* waves) {
   // resident waves used per launch on the current device, kept per
-  // (device, rep, fused)
+  // (device, rep, fused, q8)
   static std::mutex mu;
-  static std::map<std::tuple<int, int, bool>, int> cache;
+  static std::map<std::tuple<int, int, bool, bool>, int> cache;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
   std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_tuple(dev, rep, fused);
+  const auto key = std::make_tuple(dev, rep, fused, q8);
   const auto it = cache.find(key);
   if (it != cache.end()) {
     *waves = it->second;
@@ -918,11 +1148,16 @@ int mfma_sk_waves(int rep, bool fused, int* waves) {
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     return fail(LNSKV_ERR_HIP, "compute-unit count query failed");
   int rc = LNSKV_ERR_UNSUPPORTED;
+  auto of = [&](auto rep_c) {
+    constexpr int R = decltype(rep_c)::value;
+    return q8 ? sk_waves_of<R, false, true>(cus, waves)
+              : (fused ? sk_waves_of<R, true, false>(cus, waves) : sk_waves_of<R, false, false>(cus, waves));
+  };
   switch (rep) {
-    case 1: rc = fused ? sk_waves_of<1, true>(cus, waves) : sk_waves_of<1, false>(cus, waves); break;
-    case 2: rc = fused ? sk_waves_of<2, true>(cus, waves) : sk_waves_of<2, false>(cus, waves); break;
-    case 4: rc = fused ? sk_waves_of<4, true>(cus, waves) : sk_waves_of<4, false>(cus, waves); break;
-    case 8: rc = fused ? sk_waves_of<8, true>(cus, waves) : sk_waves_of<8, false>(cus, waves); break;
+    case 1: rc = of(std::integral_constant<int, 1>{}); break;
+    case 2: rc = of(std::integral_constant<int, 2>{}); break;
+    case 4: rc = of(std::integral_constant<int, 4>{}); break;
+    case 8: rc = of(std::integral_constant<int, 8>{}); break;
     default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
   }
   if (rc == LNSKV_OK) cache[key] = *waves;
@@ -930,21 +1165,22 @@ int mfma_sk_waves(int rep, bool fused, int* waves) {
 }
 
 template <bool FUSED>
-int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, hipStream_t st) {
+int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, bool q8, hipStream_t st) {
   if (n_seq > kSkMaxSeqs)
     return fail(LNSKV_ERR_INVALID, "stream-K decode serves at most %d sequences", kSkMaxSeqs);
+  if (q8 && FUSED) return fail(LNSKV_ERR_INVALID, "Q8A pages: the stream-K decode is not fused with the append");
   switch (rep) {
-    case 1: launch_sk_rep<1, FUSED>(a, n_seq, n_waves, st); break;
-    case 2: launch_sk_rep<2, FUSED>(a, n_seq, n_waves, st); break;
-    case 4: launch_sk_rep<4, FUSED>(a, n_seq, n_waves, st); break;
-    case 8: launch_sk_rep<8, FUSED>(a, n_seq, n_waves, st); break;
+    case 1: launch_sk_rep<1, FUSED>(a, n_seq, n_waves, q8, st); break;
+    case 2: launch_sk_rep<2, FUSED>(a, n_seq, n_waves, q8, st); break;
+    case 4: launch_sk_rep<4, FUSED>(a, n_seq, n_waves, q8, st); break;
+    case 8: launch_sk_rep<8, FUSED>(a, n_seq, n_waves, q8, st); break;
     default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
   }
   return hip_check("stream-K decode kernel launch");
 }
 
-template int launch_decode_mfma_sk<false>(const DecodeArgs&, int, int, int, hipStream_t);
-template int launch_decode_mfma_sk<true>(const DecodeArgs&, int, int, int, hipStream_t);
+template int launch_decode_mfma_sk<false>(const DecodeArgs&, int, int, int, bool, hipStream_t);
+template int launch_decode_mfma_sk<true>(const DecodeArgs&, int, int, int, bool, hipStream_t);
 
 
 // ---------------------------------------------------------------------------

@@ -175,14 +175,16 @@ def make_c1(seed: int = 0) -> Workload:
 
 
 def make_c2(seed: int = 0, n_seq: int = 32, lo: int = 512, hi: int = 4096,
-            num_pages: int = 16384) -> Workload:
+            num_pages: int = 16384, dtype: int = DTYPE_F16) -> Workload:
+    """dtype: the page type (f16 as the config states; Q8A, the reference's
+    own paged type, or f32 to run the same shapes through those paths)."""
     rl = SplitMix64(seed, S_LEN)
     ctx = np.array([rl.randint(lo, hi) for _ in range(n_seq)], np.int32)
     pool, _ = _shuffled_pool(num_pages, SplitMix64(seed, S_PERM))
     stride = (hi + 1 + PAGE_SIZE - 1) // PAGE_SIZE
     bt = BlockTables(n_seq, stride)
     _alloc_rows(bt, pool, range(n_seq), ctx + 1)
-    w = Workload("c2", 32, 8, 128, DTYPE_F16, num_pages, ctx, np.ones(n_seq, np.int32),
+    w = Workload("c2", 32, 8, 128, dtype, num_pages, ctx, np.ones(n_seq, np.int32),
                  np.ones(n_seq, bool), None, value_scale=0.5, seed=seed, pool=pool, bt=bt)
     return _finish(w)
 

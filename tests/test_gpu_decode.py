@@ -339,3 +339,42 @@ def test_stream_k_many_sequences(gpu, n_seq):
     got, _ = host_pages(pk)
     assert np.array_equal(got.k, hp.k) and np.array_equal(got.v, hp.v)
     assert rel_err(out1, ref1).max() < TOL[DTYPE_F16]
+
+
+@pytest.mark.parametrize("force_valu", ["0", "1"])
+def test_q8a_d128_both_kernels(gpu, monkeypatch, force_valu):
+    """Q8A pages with head_dim 128 run the MFMA stream-K kernel (int8 codes
+    turned into f16 exactly, K and V scales applied per token; the fused call
+    quantizes the new token with the append kernel first); LNSKV_FORCE_VALU=1
+    the generic kernel.  Both against the f64 oracle (1e-5), rep 1/2/4/8, with
+    windows, an empty window and a missing page; pages and scales bit-exact."""
+    monkeypatch.setenv("LNSKV_FORCE_VALU", force_valu)
+    for rep in (1, 2, 4, 8):
+        say("q8a d128 force_valu", force_valu, "rep", rep)
+        n_kv = 2
+        lens = (1, 2, 16, 17, 33, 255, 256, 257, 700, 2049)
+        pk, tables, kv_len, q = _case(gpu, DTYPE_Q8A, 128, rep, n_kv, lens, seed=60 + rep)
+        p_start = np.array([0, 0, 3, 16, 0, 100, 0, 257, 650, 1000], np.int32)  # row 7: empty window
+        tables[9, 70] = NO_PAGE  # a missing page inside a window
+        rng = np.random.default_rng(rep + 7)
+        k_new = rng.standard_normal((len(lens), n_kv, 128)).astype(np.float32)
+        v_new = (rng.standard_normal((len(lens), n_kv, 128)) * 3).astype(np.float32)
+        hp, _ = host_pages(pk)
+        ref0 = O.decode_f64(hp, q, tables, kv_len, p_start, 0.0883883)
+        out0 = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                         max_kv_len=2049, scale=0.0883883, p_start=dev_i32(p_start, gpu))
+        sync()
+        o0 = out0.cpu().numpy()
+        assert (o0[7] == 0).all()
+        assert rel_err(o0, ref0).max() < TOL[DTYPE_Q8A], rep
+        O.append(hp, k_new, v_new, np.arange(len(lens), dtype=np.int32), kv_len - 1, tables)
+        ref1 = O.decode_f64(hp, q, tables, kv_len, p_start, 0.0883883)
+        out1 = pk.append_decode(dev_f32(q, gpu), dev_f32(k_new, gpu), dev_f32(v_new, gpu), dev_i32(tables, gpu),
+                                dev_i32(kv_len, gpu), n_heads=n_kv * rep, max_kv_len=2049, scale=0.0883883,
+                                p_start=dev_i32(p_start, gpu))
+        sync()
+        got, _ = host_pages(pk)
+        assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8))
+        assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8))
+        assert np.array_equal(got.ks, hp.ks) and np.array_equal(got.vs, hp.vs)
+        assert rel_err(out1, ref1).max() < TOL[DTYPE_Q8A], rep

@@ -96,7 +96,7 @@ def test_prefill_many_chunks(gpu):
     for i in range(70):
         row = i % n_rows
         cap = ctx_pages[row] * 16
-        ln = int(rng.integers(1, 41))
+        ln = int(rng.integers(1, min(41, cap + 1)))
         pos0 = int(rng.integers(0, cap - ln + 1))
         chunks.append((row, pos0, ln))
     chunks[33] = (n_rows + 3, 0, 8)
