@@ -712,9 +712,14 @@ struct PageQ8 {
   float ks, vs;
 };
 
-template <int REP, int DEPTH>
-__device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot, PieceLoads<REP>& pl, bool tbl_ok,
-                                             int s, int kvh, int ta, int tb, const PieceOut& po) {
+// FUSED: when `append`, this piece holds position pos = L-1; the wave
+// quantizes the new token (the quantizer of append_kernel: absmax / 127,
+// IEEE divide, round half away from zero, clamp 127), stores its codes and
+// scales to the slot, and substitutes them into the page data it loaded.
+template <int REP, int DEPTH, bool FUSED>
+__device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot, lds_u8* newtok, PieceLoads<REP>& pl,
+                                             bool tbl_ok, int s, int kvh, int ta, int tb, bool append, int pos,
+                                             const PieceOut& po) {
   const int lane = threadIdx.x;
   const int g = lane >> 4, n = lane & 15;
   constexpr int kRowQ8 = kD;  // one (token, kv head) row of int8 codes
@@ -785,7 +790,39 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
   for (int d = 0; d < DEPTH; ++d) vld[d] = issue(phys_of(d), pbuf[d]) && npg > d;
   asm volatile(""
                : "+v"(pl.qv[0]), "+v"(pl.qv[1]), "+v"(pl.qv[2]), "+v"(pl.qv[3]), "+v"(pl.qv[4]), "+v"(pl.qv[5]),
-                 "+v"(pl.qv[6]), "+v"(pl.qv[7]));
+                 "+v"(pl.qv[6]), "+v"(pl.qv[7]), "+v"(pl.knew), "+v"(pl.vnew));
+
+  // Fused append: quantize the new token (lane: elements 2*lane, 2*lane+1),
+  // store codes and scales to its slot, stage the codes in LDS.
+  float new_ks = 1.0f, new_vs = 1.0f;
+  if constexpr (FUSED) {
+    if (append) {
+      auto quant = [&](float2v x, float& sc) -> uint32_t {
+        const float amax = group_max<kWave>(fmaxf(fabsf(x.x), fabsf(x.y)));
+        sc = amax == 0.0f ? 1.0f : amax / 127.0f;
+        return ((uint32_t)to_q8(x.x, sc) & 0xFFu) | (((uint32_t)to_q8(x.y, sc) & 0xFFu) << 8);
+      };
+      const uint32_t kc = quant(pl.knew, new_ks);
+      const uint32_t vc = quant(pl.vnew, new_vs);
+      typedef __attribute__((address_space(3))) uint16_t lds_u16;
+      ((lds_u16*)newtok)[lane] = (uint16_t)kc;
+      ((lds_u16*)(newtok + kRowQ8))[lane] = (uint16_t)vc;
+      const int ip = pos / kPage - base - win;  // the page is normally in the table window
+      const uint32_t ph = ip >= 0 && ip < 64 && pos / kPage - pg_first < npg ? __builtin_amdgcn_readlane(pl.btv, ip)
+                                                                              : bt_row[pos / kPage];
+      if (ph < a.num_pages) {
+        const size_t row = ((size_t)ph * kPage + (size_t)(pos % kPage)) * a.n_kv + kvh;
+        *reinterpret_cast<uint16_t*>(a.k_pages_w + row * kRowQ8 + 2 * lane) = (uint16_t)kc;
+        *reinterpret_cast<uint16_t*>(a.v_pages_w + row * kRowQ8 + 2 * lane) = (uint16_t)vc;
+        if (lane == 0) {
+          a.k_scales_w[row] = new_ks;
+          a.v_scales_w[row] = new_vs;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  const bool attend_new = FUSED && append && pos >= ta;
 
   WaveState<REP> st;
   init_wave_state<REP>(a, pl, st, n);
@@ -797,6 +834,23 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
     else if (ahead == 1) wait_vmcnt<10>();
     else wait_vmcnt<0>();
     const int tok0 = (pg_first + i) * kPage;
+    if (attend_new && pos / kPage == pg_first + i) {
+      // the loads may predate the store: take the new token's codes and
+      // scales from the staged copy
+      typedef __attribute__((address_space(3))) uint2v lds_uint2v;
+      const int t = pos % kPage;
+      if (n == t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pg.k[j] = *(const lds_uint2v*)(newtok + 32 * j + 8 * g);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (4 * g + j == t) pg.v[j] = *(const lds_uint2v*)(newtok + kRowQ8 + 8 * ((uint32_t)n ^ v_swz(4 * j + g)));
+      if (4 * g + (n & 3) == t) {
+        pg.ks = new_ks;
+        pg.vs = new_vs;
+      }
+    }
     half8 k[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) k[j] = i8x8_to_f16(pg.k[j]);
@@ -957,7 +1011,7 @@ __device__ __forceinline__ int sk_chunk(int total, int n_waves) {
 
 template <int REP, bool FUSED, int DEPTH, bool ROPE, bool Q8 = false>
 __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
-  static_assert(!Q8 || (!FUSED && !ROPE), "Q8A pages: the append runs first");
+  static_assert(!Q8 || !ROPE, "Q8A pages: RoPE runs as a pass before the kernel");
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
   __shared__ __attribute__((aligned(16))) uint8_t vring_[DEPTH * kVSlot];
   __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
@@ -1014,8 +1068,9 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
     po.pbase = ((size_t)wv * 2 + slot) * REP;
     po.pstride = 1;
     if constexpr (Q8)
-      run_piece_q8<REP, DEPTH>(a, (lds_u8*)vring_, pl, true, s, kvh, max(p0, (pg0 + i0) * kPage),
-                               min(L, (pg0 + i1) * kPage), po);
+      run_piece_q8<REP, DEPTH, FUSED>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh,
+                                      max(p0, (pg0 + i0) * kPage), min(L, (pg0 + i1) * kPage),
+                                      FUSED && i1 == np && L > 0, L - 1, po);
     else
       run_piece<REP, FUSED, DEPTH, ROPE>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh,
                                        max(p0, (pg0 + i0) * kPage),
@@ -1104,7 +1159,7 @@ int sk_waves_of(int cus, int* waves) {
   // so one wave count serves both
   int per_cu = 0, per_cu_rope = 0;
   if (Q8) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, false, kSkDepthQ8, false, true>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, kSkDepthQ8, false, true>,
                                                      kWave, 0) != hipSuccess)
       per_cu = 0;
     per_cu_rope = per_cu;
@@ -1122,7 +1177,7 @@ int sk_waves_of(int cus, int* waves) {
 template <int REP, bool FUSED>
 void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, bool q8, hipStream_t st) {
   if (q8)
-    decode_sk_kernel<REP, false, kSkDepthQ8, false, true><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+    decode_sk_kernel<REP, FUSED, kSkDepthQ8, false, true><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
   else if (FUSED && a.rope_half > 0)
     decode_sk_kernel<REP, FUSED, kSkDepth, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
   else
@@ -1150,8 +1205,8 @@ int mfma_sk_waves(int rep, bool fused, bool q8, int* waves) {
   int rc = LNSKV_ERR_UNSUPPORTED;
   auto of = [&](auto rep_c) {
     constexpr int R = decltype(rep_c)::value;
-    return q8 ? sk_waves_of<R, false, true>(cus, waves)
-              : (fused ? sk_waves_of<R, true, false>(cus, waves) : sk_waves_of<R, false, false>(cus, waves));
+    if (q8) return fused ? sk_waves_of<R, true, true>(cus, waves) : sk_waves_of<R, false, true>(cus, waves);
+    return fused ? sk_waves_of<R, true, false>(cus, waves) : sk_waves_of<R, false, false>(cus, waves);
   };
   switch (rep) {
     case 1: rc = of(std::integral_constant<int, 1>{}); break;
@@ -1168,7 +1223,6 @@ template <bool FUSED>
 int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, bool q8, hipStream_t st) {
   if (n_seq > kSkMaxSeqs)
     return fail(LNSKV_ERR_INVALID, "stream-K decode serves at most %d sequences", kSkMaxSeqs);
-  if (q8 && FUSED) return fail(LNSKV_ERR_INVALID, "Q8A pages: the stream-K decode is not fused with the append");
   switch (rep) {
     case 1: launch_sk_rep<1, FUSED>(a, n_seq, n_waves, q8, st); break;
     case 2: launch_sk_rep<2, FUSED>(a, n_seq, n_waves, q8, st); break;

@@ -343,8 +343,7 @@ int launch_decode_valu(const DecodeArgs& a, int d, int rep, int n_seq, hipStream
 template <bool FUSED>
 int launch_decode_mfma_f16_d128(const DecodeArgs& a, int rep, int n_seq, hipStream_t st);
 // Stream-K schedule of the MFMA kernel (n_seq <= kSkMaxSeqs): n_waves single-wave
-// blocks, workspace of n_waves * 2 * rep partial rows.  q8: Q8A pages (not
-// fused: the append runs first).
+// blocks, workspace of n_waves * 2 * rep partial rows.  q8: Q8A pages.
 template <bool FUSED>
 int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, bool q8, hipStream_t st);
 // Waves of the stream-K kernel resident at once on the current device.

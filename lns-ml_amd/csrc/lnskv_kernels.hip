@@ -51,12 +51,6 @@ struct AppendArgs {
   const float* rope_inv;  // append_vec_kernel: K turns by tok_pos with these inverse frequencies
   int32_t rope_half;      // rotary_dim / 2 (a multiple of 8, half/8 a power of two); 0: none
   int32_t head_dim;
-  // tok_seq == nullptr: token t is sequence t's newest, at position L - 1 for
-  // L = kv_len[t] (kv_len_scalar when kv_len is null) clamped to max_kv_len
-  // and the table (as the fused decode clamps it); none when L <= 0
-  const int32_t* kv_len;
-  int32_t kv_len_scalar;
-  int32_t max_kv_len;
 };
 
 template <int DT, int D>
@@ -93,14 +87,7 @@ __global__ __launch_bounds__(kBlock) void append_kernel(AppendArgs a) {
   const int64_t item = (int64_t)blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
   if (item >= (int64_t)a.n_tok * a.n_kv) return;  // wave-uniform
   const int t = (int)(item / a.n_kv), h = (int)(item % a.n_kv);
-  int seq = t, pos;
-  if (a.tok_seq) {
-    seq = a.tok_seq[t];
-    pos = a.tok_pos[t];
-  } else {
-    const int L = a.kv_len ? a.kv_len[t] : a.kv_len_scalar;
-    pos = min(max(L, 0), min(a.max_kv_len, a.bt_stride * kPage)) - 1;
-  }
+  const int seq = a.tok_seq[t], pos = a.tok_pos[t];
   if (seq < 0 || seq >= a.n_rows || pos < 0 || pos / kPage >= a.bt_stride) return;
   const uint32_t phys = a.bt[(size_t)seq * a.bt_stride + pos / kPage];
   if (phys >= a.num_pages) return;  // LNSKV_NO_PAGE or outside the pool
@@ -411,13 +398,12 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
   const bool q8 = mfma_q8_path((int)c->dtype, d, rep);
   if (split_tokens == 0 && (mfma_path((int)c->dtype, d, rep) || q8) && n_seq <= kSkMaxSeqs &&
       units < ((int64_t)1 << 30)) {
-    // fused < 0: either kind (the workspace query), sized for the larger;
-    // Q8A pages run the unfused kernel after the append
+    // fused < 0: either kind (the workspace query), sized for the larger
     int w0 = 0, w1 = 0;
-    if (fused <= 0 || q8)
+    if (fused <= 0)
       if (int rc = mfma_sk_waves(rep, false, q8, &w0)) return rc;
-    if (fused != 0 && !q8)
-      if (int rc = mfma_sk_waves(rep, true, false, &w1)) return rc;
+    if (fused != 0)
+      if (int rc = mfma_sk_waves(rep, true, q8, &w1)) return rc;
     p->sk_waves = std::max(w0, w1);
     // partial rows (acc, then (m, l)) of two pieces per wave, then one
     // 16-byte descriptor per wave
@@ -578,32 +564,8 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
     a.ws_acc = static_cast<float*>(ws);
     a.ws_ml = a.ws_acc + (size_t)plan.sk_waves * 2 * rep * c->head_dim;
     a.sk_desc = reinterpret_cast<int4*>(a.ws_ml + (size_t)plan.sk_waves * 2 * rep * 2);
-    if (c->dtype == LNSKV_DTYPE_Q8A) {
-      // the new token is quantized into its slot first (append_kernel), then
-      // the unfused kernel attends it with the rest of the window
-      if constexpr (FUSED) {
-        AppendArgs ap{};
-        ap.k_pages = static_cast<uint8_t*>(c->k_pages);
-        ap.v_pages = static_cast<uint8_t*>(c->v_pages);
-        ap.k_scales = c->k_scales;
-        ap.v_scales = c->v_scales;
-        ap.k_new = k_new;
-        ap.v_new = v_new;
-        ap.bt = bt;
-        ap.bt_stride = bt_stride;
-        ap.n_rows = n_seq;
-        ap.n_tok = n_seq;
-        ap.n_kv = (int32_t)c->n_kv_heads;
-        ap.num_pages = c->num_pages;
-        ap.head_dim = (int32_t)c->head_dim;
-        ap.kv_len = kv_len;
-        ap.kv_len_scalar = kv_len_scalar;
-        ap.max_kv_len = max_kv_len;
-        if (int rc = launch_append_dt<LNSKV_DTYPE_Q8A>(ap, (int)c->head_dim, (hipStream_t)stream)) return rc;
-      }
-      return launch_decode_mfma_sk<false>(a, rep, n_seq, plan.sk_waves, true, (hipStream_t)stream);
-    }
-    return launch_decode_mfma_sk<FUSED>(a, rep, n_seq, plan.sk_waves, false, (hipStream_t)stream);
+    return launch_decode_mfma_sk<FUSED>(a, rep, n_seq, plan.sk_waves, c->dtype == LNSKV_DTYPE_Q8A,
+                                        (hipStream_t)stream);
   }
   if (need > 0) {
     a.ws_acc = static_cast<float*>(ws);

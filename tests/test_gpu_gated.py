@@ -9,8 +9,9 @@ path, the scalar path (head_dim not a multiple of 4), an unaligned buffer.
 lnskv_gated_append_decode: the stored output equals, bit for bit, the
 ungated call's output times the gate (one f32 multiply as the row is
 written), on every schedule that writes output rows -- stream-K MFMA with its
-combine, split-K MFMA with combine_kernel, the generic kernel (f32, Q8A, f16
-forced), fused RoPE and the RoPE pre-pass -- and the appended pages are the
+combine (f16, and Q8A after its quantizing append), split-K MFMA with
+combine_kernel, the generic kernel (f32, Q8A, f16 forced), fused RoPE and the
+RoPE pre-pass -- and the appended pages are the
 ungated call's; one case is also checked against the f64 oracle times the
 gate."""
 import numpy as np
@@ -54,6 +55,7 @@ CASES = [  # dtype, head_dim, rep, split, force_valu, rotary_dim
     (DTYPE_F16, 128, 4, 0, "1", 0),      # generic kernel, f16
     (DTYPE_F32, 64, 2, 0, "0", 0),       # generic kernel, f32
     (DTYPE_Q8A, 128, 4, 32, "0", 0),     # generic kernel, Q8A, split-K
+    (DTYPE_Q8A, 128, 4, 0, "0", 0),      # Q8A stream-K MFMA after the quantizing append
     (DTYPE_F16, 128, 4, 0, "0", 128),    # RoPE turned inside the MFMA kernel
     (DTYPE_F16, 128, 8, 0, "0", 96),     # RoPE pre-pass (rotary 96), REP 8
 ]
