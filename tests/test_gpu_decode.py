@@ -223,6 +223,35 @@ def test_reference_single_sequence_call_c1_shape(gpu):
         assert rel_err(out, ref).max() < TOL[dtype]
 
 
+def test_reference_single_sequence_call_q8a_d128(gpu):
+    """lnskv_attention_paged with the reference's own page type at head_dim
+    128 (the matrix-core Q8A path: the new token quantized and stored by the
+    decode kernel itself): Hq32/Hkv8, 700 context tokens, windows 0 and 650;
+    codes and scales bit-exact, output within 1e-5."""
+    for p_start in (0, 650):
+        say("attention_paged q8a d128 p_start", p_start)
+        rng = np.random.default_rng(p_start + 1)
+        pk = PagedKV(64, 8, 128, DTYPE_Q8A, gpu)
+        fill_pages(pk, seed=2)
+        perm = rng.permutation(64).astype(np.uint32)
+        bt = np.full(512, NO_PAGE, np.uint32)
+        bt[:44] = perm[:44]
+        q = rng.standard_normal((32, 128)).astype(np.float32)
+        k_in = (rng.standard_normal(8 * 128) * 2).astype(np.float32)
+        v_in = (rng.standard_normal(8 * 128) * 2).astype(np.float32)
+        hp, _ = host_pages(pk)
+        O.append(hp, k_in[None], v_in[None], np.zeros(1, np.int32), np.array([700], np.int32), bt[None])
+        ref = O.decode_f64(hp, q[None], bt[None], np.array([701], np.int32), np.array([p_start], np.int32),
+                           1.0 / np.sqrt(128.0))[0]
+        out = pk.attention_paged(dev_f32(q, gpu), dev_f32(k_in, gpu), dev_f32(v_in, gpu), dev_i32(bt, gpu),
+                                 pos=700, n_heads=32, p_start=p_start, dispatch=True)
+        got, _ = host_pages(pk)
+        assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8))
+        assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8))
+        assert np.array_equal(got.ks, hp.ks) and np.array_equal(got.vs, hp.vs)
+        assert rel_err(out, ref).max() < TOL[DTYPE_Q8A]
+
+
 def _sk_lens(n, seed):
     """Lengths for a stream-K batch: empty, sub-page, page-edge and long
     sequences, so that waves hold several pieces and segments span waves."""
