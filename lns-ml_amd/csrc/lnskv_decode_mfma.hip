@@ -309,7 +309,11 @@ struct PieceLoads {
   float2v knew, vnew;
 };
 
-template <int REP, bool FUSED, bool ROPE>
+// Q8: the contraction order of the Q8A kernel, where lane (g, n) holds dims
+// 32g + 8j .. 32g + 8j + 7 for product j (a contiguous 32-dim slice per lane,
+// so that a page row's codes come in two 16-byte loads); otherwise dims
+// 32j + 8g .. 32j + 8g + 7.
+template <int REP, bool FUSED, bool ROPE, bool Q8 = false>
 __device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh, int tbl, PieceLoads<REP>& pl) {
   const int lane = threadIdx.x;
   const int g = lane >> 4, n = lane & 15;
@@ -318,12 +322,12 @@ __device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh,
   pl.tbl = tbl;
   const bool qcol = n < 2 * REP;
   const int hq = qcol ? (n < REP ? n : n - REP) : 0;  // other columns load head 0 and drop it
-  const float4v* qh =
-      reinterpret_cast<const float4v*>(a.q + ((size_t)s * a.n_heads + (size_t)kvh * REP + hq) * kD + 8 * g);
+  const float4v* qh = reinterpret_cast<const float4v*>(a.q + ((size_t)s * a.n_heads + (size_t)kvh * REP + hq) * kD +
+                                                      (Q8 ? 32 * g : 8 * g));
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    pl.qv[2 * j] = qh[8 * j];
-    pl.qv[2 * j + 1] = qh[8 * j + 1];
+    pl.qv[2 * j] = qh[Q8 ? 2 * j : 8 * j];
+    pl.qv[2 * j + 1] = qh[Q8 ? 2 * j + 1 : 8 * j + 1];
   }
   // Every piece of a fused call loads the new token's row (the same 1 KiB
   // per sequence and kv head, so the repeats hit L2): a load under a branch
@@ -703,12 +707,12 @@ __device__ __forceinline__ half8 i8x8_to_f16(uint2v w) {
   return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// One Q8A page in flight: K codes of token n at dims 32j + 8g.., V codes of
-// token 4g+j at the swizzled chunk n ^ sw(4j+g), the K and V scales of token
-// 4g + n%4.
+// One Q8A page in flight: K codes of token n, dims 32g .. 32g+31 (product j
+// takes dims 32g + 8j ..); V codes of token 8h + lane/8, dims 16 (lane%8) ..
+// +15 for load h; the K and V scales of token 4g + n%4.
 struct PageQ8 {
-  uint2v k[4];
-  uint2v v[4];
+  u32x4 k[2];
+  u32x4 v[2];
   float ks, vs;
 };
 
@@ -736,10 +740,20 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
   const uint32_t rs = (uint32_t)a.n_kv * kRowQ8;  // bytes between token rows
   const size_t page_bytes = (size_t)kPage * rs;
   const uint32_t kvh_off = (uint32_t)kvh * kRowQ8;
-  const uint32_t koff = (uint32_t)n * rs + 8u * g;
-  uint32_t voff[4];
+  const uint32_t koff = (uint32_t)n * rs + 32u * g;
+  // V load h: token 8h + lane/8, 16 codes from dim 16 * (lane % 8); they go
+  // to the LDS row of that token (row 4 (t % 4) + t / 4, the layout of the
+  // transposed reads) as f16 chunks 2c and 2c + 1, each at chunk ^ sw(row)
+  const int vc = lane & 7;
+  uint32_t voff[2], vlds[2][2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) voff[j] = (uint32_t)(4 * g + j) * rs + 8u * ((uint32_t)n ^ v_swz(4 * j + g));
+  for (int h = 0; h < 2; ++h) {
+    const int t = 8 * h + (lane >> 3);
+    const int R = 4 * (t & 3) + (t >> 2);
+    voff[h] = (uint32_t)t * rs + 16u * (uint32_t)vc;
+    vlds[h][0] = (uint32_t)R * kRowBytes + 16u * ((uint32_t)(2 * vc) ^ v_swz(R));
+    vlds[h][1] = (uint32_t)R * kRowBytes + 16u * ((uint32_t)(2 * vc + 1) ^ v_swz(R));
+  }
   const uint32_t soff = (uint32_t)(4 * g + (n & 3)) * (uint32_t)a.n_kv + (uint32_t)kvh;
 
   const uint32_t* bt_row = a.bt + (size_t)s * a.bt_stride;
@@ -768,16 +782,16 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
   };
   asm volatile("" : "+v"(pl.btv) : : "memory");
 
-  // exactly 10 vector-memory loads; a missing page reads page 0 (masked)
+  // exactly 6 vector-memory loads; a missing page reads page 0 (masked)
   auto issue = [&](uint32_t ph, PageQ8& pg) -> bool {
     const bool valid = ph < a.num_pages;
     const size_t pb = (size_t)(valid ? ph : 0u);
     const uint8_t* kb = a.k_pages + pb * page_bytes + kvh_off;
     const uint8_t* vb = a.v_pages + pb * page_bytes + kvh_off;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pg.k[j] = *reinterpret_cast<const uint2v*>(kb + koff + 32 * j);
+    for (int h = 0; h < 2; ++h) pg.k[h] = *reinterpret_cast<const u32x4*>(kb + koff + 16 * h);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pg.v[j] = *reinterpret_cast<const uint2v*>(vb + voff[j]);
+    for (int h = 0; h < 2; ++h) pg.v[h] = *reinterpret_cast<const u32x4*>(vb + voff[h]);
     const size_t sb = pb * kPage * (size_t)a.n_kv + soff;
     pg.ks = a.k_scales[sb];
     pg.vs = a.v_scales[sb];
@@ -829,23 +843,22 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
 
   auto step = [&](int i, PageQ8& pg, bool& valid, bool steady) {
     const int ahead = steady ? DEPTH - 1 : min(npg - 1 - i, DEPTH - 1);  // pages issued after page i
-    if (ahead >= 3) wait_vmcnt<30>();
-    else if (ahead == 2) wait_vmcnt<20>();
-    else if (ahead == 1) wait_vmcnt<10>();
+    if (ahead >= 3) wait_vmcnt<18>();
+    else if (ahead == 2) wait_vmcnt<12>();
+    else if (ahead == 1) wait_vmcnt<6>();
     else wait_vmcnt<0>();
     const int tok0 = (pg_first + i) * kPage;
     if (attend_new && pos / kPage == pg_first + i) {
       // the loads may predate the store: take the new token's codes and
       // scales from the staged copy
-      typedef __attribute__((address_space(3))) uint2v lds_uint2v;
       const int t = pos % kPage;
       if (n == t) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pg.k[j] = *(const lds_uint2v*)(newtok + 32 * j + 8 * g);
+        for (int h = 0; h < 2; ++h) pg.k[h] = *(const lds_u32x4*)(newtok + 32 * g + 16 * h);
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (4 * g + j == t) pg.v[j] = *(const lds_uint2v*)(newtok + kRowQ8 + 8 * ((uint32_t)n ^ v_swz(4 * j + g)));
+      for (int h = 0; h < 2; ++h)
+        if (8 * h + (lane >> 3) == t) pg.v[h] = *(const lds_u32x4*)(newtok + kRowQ8 + 16 * vc);
       if (4 * g + (n & 3) == t) {
         pg.ks = new_ks;
         pg.vs = new_vs;
@@ -853,10 +866,12 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
     }
     half8 k[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) k[j] = i8x8_to_f16(pg.k[j]);
+    for (int j = 0; j < 4; ++j) k[j] = i8x8_to_f16(uint2v{pg.k[j >> 1][2 * (j & 1)], pg.k[j >> 1][2 * (j & 1) + 1]});
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *(lds_half8*)(vslot + (4 * j + g) * kRowBytes + 16 * n) = i8x8_to_f16(pg.v[j]);
+    for (int h = 0; h < 2; ++h) {
+      *(lds_half8*)(vslot + vlds[h][0]) = i8x8_to_f16(uint2v{pg.v[h][0], pg.v[h][1]});
+      *(lds_half8*)(vslot + vlds[h][1]) = i8x8_to_f16(uint2v{pg.v[h][2], pg.v[h][3]});
+    }
     // scales of tokens 4g+ii: lane 4*(n/4) + ii of this row holds them
     float4v ksc, vsc;
     ksc[0] = dpp_mov<0x00>(pg.ks);
@@ -1062,7 +1077,7 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
       desc = make_int4(s, kvh, wa, (wv - wa + 1) * 2 + (seg0 == wa * chunk ? 0 : 1));
     }
     PieceLoads<REP> pl;
-    piece_loads<REP, FUSED, ROPE>(a, s, kvh, pg0 + i0, pl);
+    piece_loads<REP, FUSED, ROPE, Q8>(a, s, kvh, pg0 + i0, pl);
     PieceOut po;
     po.final = i0 == 0 && i1 == np;
     po.pbase = ((size_t)wv * 2 + slot) * REP;
