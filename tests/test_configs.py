@@ -44,6 +44,20 @@ def test_c2_lengths_and_bytes():
     assert 200e6 < b["total"] < 400e6
 
 
+def test_c2_page_types_share_the_draw_and_count_their_bytes():
+    """make("c2", dtype=...) keeps lengths and tables; K+V bytes per token
+    are 2*Hkv*d*e_kv, plus 2*Hkv*4 of scales for Q8A (int8 codes)."""
+    f16 = make("c2")
+    for dtype, e, extra in ((0, 4, 0), (2, 1, 2 * 8 * 4)):
+        w = make("c2", dtype=dtype)
+        assert w.dtype == dtype
+        assert np.array_equal(w.kv_len, f16.kv_len) and np.array_equal(w.tables, f16.tables)
+        b = w.algorithmic_bytes()
+        per_tok = 2 * 8 * 128 * e + extra
+        assert b["kv_read"] == int(w.kv_len.sum()) * per_tok
+        assert b["append"] == 32 * (2 * 8 * 128 * 4 + per_tok)
+
+
 def test_c3_c4_shapes():
     w3 = make("c3")
     assert w3.split == 512 and (w3.kv_len == 32769).all() and w3.num_pages == 4 * 2049
