@@ -680,13 +680,14 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
 // Q8A pages (the reference's paged type: int8 codes, one f32 scale per
 // (slot, kv head), lns_decode.metal:547-593, 611-634) on the same matrix-core
 // pipeline.  A page's K rows (16 x 128 bytes) and V rows come to registers
-// as int8 with 8-byte loads, plus the K and V scales of the lane's token;
-// when the page is consumed the codes become f16 exactly (K: the A operand as
-// for f16 pages; V: written to the LDS slot in the layout the transposed
-// reads expect), and consume_page applies the scales per token: scores times
-// the K scale, softmax weights times the V scale in the P.V product (the
-// reference's q.(k8 ks) and (beta vs) v8).  Not fused with the append: a Q8A
-// append runs first (the quantizer of append_kernel).
+// as int8 codes with 16-byte loads, plus the K and V scales of the lane's
+// token; when the page is consumed the codes become f16 exactly (K: the A
+// operand, in a contraction order that gives each lane a contiguous 32-dim
+// slice; V: written to the LDS slot in the layout the transposed reads
+// expect), and consume_page applies the scales per token: scores times the
+// K scale, softmax weights times the V scale in the P.V product (the
+// reference's q.(k8 ks) and (beta vs) v8).  A fused call quantizes the new
+// token in the wave that holds it.
 // ---------------------------------------------------------------------------
 
 // Exact int8 -> f16 of the four signed bytes of w: the f16 with bits
