@@ -1484,10 +1484,31 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
   const int lane = (int)(threadIdx.x & (kWave - 1)), w = (int)(threadIdx.x / kWave);
   const int g = lane >> 4, n = lane & 15;
 
-  // block -> (chunk, tile, kv head); the kv head varies fastest
+  // block -> (chunk, tile, kv head); the kv head varies fastest.  Up to 64
+  // chunks are taken longest first (by the position after their last token,
+  // ties by index), so that the last workgroups a CU receives are short ones;
+  // more chunks are taken in index order.
   const int kvh = (int)(blockIdx.x % (unsigned)a.n_kv);
   int slot = (int)(blockIdx.x / (unsigned)a.n_kv), c = -1, tile = 0, nt_c = 0;
-  for (int c0 = 0; c0 < a.n_chunks; c0 += kWave) {  // wave-uniform; identical in every wave
+  if (a.n_chunks <= kWave) {
+    const int nt = pf_tiles<QT>(a, lane);
+    const int4 chl = a.chunks[lane < a.n_chunks ? lane : 0];
+    const int key = nt > 0 ? (int)min((int64_t)chl.y + chl.z, (int64_t)INT32_MAX) : -1;
+    int before = 0;  // tiles of the chunks taken before this one
+    for (int j = 0; j < a.n_chunks; ++j) {
+      const int kj = __builtin_amdgcn_readlane(key, j);
+      const int ntj = __builtin_amdgcn_readlane(nt, j);
+      if (kj > key || (kj == key && j < lane)) before += ntj;
+    }
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < a.n_chunks && nt > 0 && before <= slot &&
+                                                     slot < before + nt);
+    if (hit) {
+      const int idx = (int)__builtin_ctzll(hit);
+      c = idx;
+      nt_c = __builtin_amdgcn_readlane(nt, idx);
+      tile = slot - __builtin_amdgcn_readlane(before, idx);
+    }
+  } else for (int c0 = 0; c0 < a.n_chunks; c0 += kWave) {  // wave-uniform; identical in every wave
     const int nt = pf_tiles<QT>(a, c0 + lane);
     const int incl = wave_incl_scan(nt);
     const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
