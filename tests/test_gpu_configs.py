@@ -3,7 +3,7 @@
 Per config: the step (page copies, chunk appends, fused append + decode) runs
 on the GPU; the oracle replays it on a host copy of every page the step can
 touch.  Pages must match bit for bit; attention outputs must be within the
-row-normwise tolerance (1e-3 f16, 1e-5 f32) of the f64 oracle over the exact
+row-normwise tolerance (1e-3 f16, 1e-5 f32 and Q8A) of the f64 oracle over the exact
 stored values, and within the same tolerance of the reference-order f32 scan
 (the reference CPU path)."""
 import numpy as np
@@ -11,7 +11,7 @@ import pytest
 
 import oracle as O
 from gpu_util import TOL, host_pages, rel_err, remap_tables, say
-from lnskv import NO_PAGE
+from lnskv import DTYPE_Q8A, NO_PAGE
 from lnskv.configs import make, used_pages
 from lnskv.device import sync
 from lnskv.step import StepRunner
@@ -19,10 +19,12 @@ from lnskv.step import StepRunner
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5", "c2-q8a"])
 def test_config_step(gpu, name):
+    """c2-q8a: the c2 draw with the reference's own page type (int8 codes
+    and scales; the matrix-core Q8A decode with its in-kernel quantizer)."""
     say("config", name, "build")
-    w = make(name)
+    w = make("c2", dtype=DTYPE_Q8A) if name == "c2-q8a" else make(name)
     r = StepRunner(w, gpu, n_layers=1, seed=17)
     pk = r.layers[0]
     pages = used_pages(w.tables)
@@ -51,6 +53,8 @@ def test_config_step(gpu, name):
     got, _ = host_pages(pk, pages)
     assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8)), "K pages differ"
     assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8)), "V pages differ"
+    if w.dtype == DTYPE_Q8A:
+        assert np.array_equal(got.ks, hp.ks) and np.array_equal(got.vs, hp.vs), "scales differ"
 
     q = r.q.cpu().numpy()
     o = out.cpu().numpy()
@@ -59,7 +63,7 @@ def test_config_step(gpu, name):
     err = rel_err(o, ref)
     say("config", name, "max rel err vs f64", float(err.max()))
     assert err.max() < TOL[w.dtype]
-    if name in ("c1", "c2"):
+    if name in ("c1", "c2", "c2-q8a"):
         scan = O.decode_refscan(hp, q, dec_tables, kv_len, None, w.scale)
         assert rel_err(o, scan.astype(np.float64)).max() < TOL[w.dtype]
     # pages outside the step's footprint are untouched: a second step is
