@@ -154,6 +154,23 @@ int lnskv_append_decode(const lnskv_pages* c, const float* q_dev, const float* k
                         int32_t split_tokens, void* workspace_dev, size_t ws_bytes,
                         lnskv_stream_t stream);
 
+/* lnskv_append_decode without a workspace argument, allocating nothing: no
+ * counterpart in the reference.  It is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The partial results live in a static device array of
+ * LNSKV_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call
+ * whose schedule needs more (lnskv_decode_workspace_size) returns
+ * LNSKV_ERR_WORKSPACE before launching anything.  Every call on one GPU shares
+ * that array: calls that overlap in time on one GPU race and give wrong
+ * results.  Same kernels, same results bit for bit as lnskv_append_decode. */
+#define LNSKV_NOALLOC_SCRATCH_BYTES ((size_t)24 << 20)
+int lnskv_append_decode_noalloc(const lnskv_pages* c, const float* q_dev, const float* k_new_dev,
+                                const float* v_new_dev, float* out_dev,
+                                const uint32_t* block_tables_dev, int32_t bt_stride,
+                                const int32_t* kv_len_dev, const int32_t* p_start_dev,
+                                int32_t n_seq, int32_t n_heads, int32_t max_kv_len, float scale,
+                                int32_t split_tokens, lnskv_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * RoPE fused into the append.  The reference rotates q and k in place with
  * rope_with_freqs (lns_decode.metal:154-191; angle_i = pos * inv_freqs[i], the

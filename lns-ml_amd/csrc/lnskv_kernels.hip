@@ -460,6 +460,47 @@ int library_buffer(int which, size_t need, void** out) {
   return LNSKV_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Static scratch of lnskv_append_decode_noalloc: the decode workspace (partial
+// rows and stream-K segment descriptors) for callers that cannot allocate
+// device memory.  Every GPU the library runs on holds its own copy until the
+// process ends.  The host name `scratch` is only a stand-in for the device
+// array: its device address is looked up once per device and used from then
+// on.  Nothing in it has to start at zero (every word a call reads was written
+// earlier in the same call); calls that overlap in time on one device race on
+// it.
+namespace {
+constexpr size_t kNoAllocScratchBytes = LNSKV_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
+}  // namespace
+
+// The current device's scratch address.  The first call on a device looks the
+// address up and fills the host-side schedule caches the decode consults, so
+// later calls allocate nothing, on the device or on the host.
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices) return fail(LNSKV_ERR_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(LNSKV_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    for (int rep : {1, 2, 4, 8})
+      for (bool q8 : {false, true}) {
+        int waves = 0;
+        if (int rc = mfma_sk_waves(rep, true, q8, &waves)) return rc;
+      }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LNSKV_OK;
+}
+
 namespace {
 int library_workspace(size_t need, void** out) { return library_buffer(0, need, out); }
 
@@ -742,6 +783,18 @@ int lnskv_append_decode(const lnskv_pages* c, const float* q, const float* k_new
   if (!kv_len) return fail(LNSKV_ERR_INVALID, "kv_len must be non-null");
   return decode_entry<true>(c, q, k_new, v_new, out, bt, bt_stride, kv_len, 0, p_start, 0, n_seq,
                             n_heads, max_kv_len, scale, split_tokens, ws, ws_bytes, stream);
+}
+
+int lnskv_append_decode_noalloc(const lnskv_pages* c, const float* q, const float* k_new, const float* v_new,
+                                float* out, const uint32_t* bt, int32_t bt_stride, const int32_t* kv_len,
+                                const int32_t* p_start, int32_t n_seq, int32_t n_heads, int32_t max_kv_len,
+                                float scale, int32_t split_tokens, lnskv_stream_t stream) {
+  clear_error();
+  if (!kv_len) return fail(LNSKV_ERR_INVALID, "kv_len must be non-null");
+  void* ws = nullptr;
+  if (int rc = noalloc_scratch(&ws)) return rc;
+  return decode_entry<true>(c, q, k_new, v_new, out, bt, bt_stride, kv_len, 0, p_start, 0, n_seq, n_heads,
+                            max_kv_len, scale, split_tokens, ws, kNoAllocScratchBytes, stream);
 }
 
 int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const float* q, const float* k_new,

@@ -75,6 +75,8 @@ SIGNATURES = {
     "lnskv_decode": (C.c_int, [_P, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _sz, _vp]),
     "lnskv_append_decode": (
         C.c_int, [_P, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _sz, _vp]),
+    "lnskv_append_decode_noalloc": (
+        C.c_int, [_P, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp]),
     "lnskv_attention_paged": (C.c_int, [_vp, _vp, _vp, _P, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
     "lnskv_dispatch_attention_paged": (
         C.c_int, [_vp, _vp, _vp, _P, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
