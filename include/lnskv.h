@@ -117,6 +117,9 @@ int lnskv_append(const lnskv_pages* c, const float* k_new_dev, const float* v_ne
  *   and p_start is kv_p_start, engine.rs:3008-3013).
  *   out = softmax(scale * q.K^T) . V, by online softmax (metal:595-645).
  *   max_kv_len: host upper bound of kv_len over the batch (sizes the grid).
+ *   A sequence whose kv_len exceeds max_kv_len or 16 * bt_stride is out of
+ *   range: its output row is zero and the fused variants store nothing for
+ *   it (as lnskv_append skips tokens outside the table).
  *   split_tokens: tokens per split-K partition (multiple of 16), or 0 to let
  *   the library schedule: f16 pages with head_dim 128 and at most 4096
  *   sequences then run stream-K (every resident wave of the device takes an
@@ -125,10 +128,10 @@ int lnskv_append(const lnskv_pages* c, const float* k_new_dev, const float* v_ne
  *   workspace_dev/ws_bytes: 16-byte aligned device scratch of at least
  *   lnskv_decode_workspace_size(...) bytes (same n_seq, n_heads, max_kv_len
  *   and split_tokens, same current device), or NULL/0 to use a buffer the
- *   library keeps per device (grown with hipMalloc on demand; calls that use
- *   it must not overlap in time).  The workspace holds the partial results of
- *   one call; nothing carries over between calls.  Calls that overlap in
- *   time need distinct workspaces.
+ *   library keeps per device (calls that use it must not overlap in time; see
+ *   lnskv_workspace_reserve for how it grows).  The workspace holds the partial
+ *   results of one call; nothing carries over between calls.  Calls that
+ *   overlap in time need distinct workspaces.
  * Pages in the window whose table entry is LNSKV_NO_PAGE or >= num_pages are
  * skipped (contribute nothing).  An empty window gives a zero output row.
  * ------------------------------------------------------------------------- */
@@ -204,15 +207,30 @@ typedef struct lnskv_rope {
 
 /* lnskv_append with K rotated first: token t's K (every kv head) turns by
  * position tok_pos_dev[t] before it is converted and stored; V is stored as
- * given. */
+ * given.  f32/f16 pages with a rotary half that is a multiple of 8 (half/8 a
+ * power of two) and 16-byte aligned inputs turn K inside the append; other
+ * shapes (Q8A pages among them) first write the rotated K rows to
+ * workspace_dev, which then needs lnskv_rope_append_workspace_size bytes
+ * (16-byte aligned).  workspace_dev NULL: a buffer the library keeps per
+ * device instead (calls that use it must not overlap in time). */
+int lnskv_rope_append_workspace_size(const lnskv_pages* c, const lnskv_rope* rope, int32_t n_tok,
+                                     size_t* bytes);
 int lnskv_rope_append(const lnskv_pages* c, const lnskv_rope* rope, const float* k_new_dev,
                       const float* v_new_dev, const int32_t* tok_seq_dev, const int32_t* tok_pos_dev,
                       int32_t n_tok, const uint32_t* block_tables_dev, int32_t bt_stride, int32_t n_rows,
-                      lnskv_stream_t stream);
+                      void* workspace_dev, size_t ws_bytes, lnskv_stream_t stream);
 
 /* lnskv_append_decode with q_dev and k_new_dev before the rotation: both turn
  * by the new token's position kv_len_dev[s]-1, then the token is stored and
- * attended to as lnskv_append_decode does. */
+ * attended to as lnskv_append_decode does.  f16 pages with head_dim 128 and a
+ * rotary width of 64 or 128 turn q and K inside the decode; other shapes (Q8A
+ * pages among them) first write the rotated q and K rows into the workspace,
+ * after the decode's partial results.  A caller's workspace therefore needs
+ * lnskv_rope_decode_workspace_size bytes (it covers both cases); NULL uses the
+ * library's per-device buffers (calls that use them must not overlap). */
+int lnskv_rope_decode_workspace_size(const lnskv_pages* c, const lnskv_rope* rope, int32_t n_seq,
+                                     int32_t n_heads, int32_t max_kv_len, int32_t split_tokens,
+                                     size_t* bytes);
 int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const float* q_dev,
                              const float* k_new_dev, const float* v_new_dev, float* out_dev,
                              const uint32_t* block_tables_dev, int32_t bt_stride,
@@ -233,13 +251,16 @@ int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const
  *   [first token, first token + length), at positions first position + 0,
  *   1, ...; chunks outside [0, n_rows) x [0, n_tok) are skipped.
  *   q_dev / out_dev: [n_tok][n_heads][head_dim] f32; p_start_dev: per table
- *   row (NULL = 0).  f16 pages with head_dim 128 only (LNSKV_ERR_UNSUPPORTED
- *   otherwise).
+ *   row (NULL = 0).  window > 0 (a sliding-window layer): query row t attends
+ *   [max(p_start, pos(t) - window + 1), pos(t)], each prompt token its own
+ *   kv_p_start as the reference's per-token loop gives it (engine.rs:
+ *   3007-3013); window = 0: [p_start, pos(t)].  f16 pages with head_dim 128
+ *   only (LNSKV_ERR_UNSUPPORTED otherwise).
  * ------------------------------------------------------------------------- */
 int lnskv_prefill_attention(const lnskv_pages* c, const float* q_dev, float* out_dev,
                             const int32_t* chunks_dev, int32_t n_chunks, int32_t n_tok,
                             const uint32_t* block_tables_dev, int32_t bt_stride, int32_t n_rows,
-                            const int32_t* p_start_dev, int32_t n_heads, float scale,
+                            const int32_t* p_start_dev, int32_t window, int32_t n_heads, float scale,
                             lnskv_stream_t stream);
 
 /* ---------------------------------------------------------------------------
@@ -350,6 +371,22 @@ int lnskv_gather(const lnskv_pages* c, const uint32_t* block_table_dev, int32_t 
  * dispatch_*, lib.rs:1091-1092). */
 int lnskv_sync(lnskv_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * The library's own device buffers (no counterpart in the reference, whose
+ * Metal calls need none).  Entry points given a NULL workspace use a buffer
+ * the library keeps per device: the decode workspace, the rotated RoPE rows,
+ * the Q4L GEMV operands.  When one is too small a call allocates a larger one
+ * (hipMalloc, no device synchronization) and keeps the old one alive, since
+ * work queued earlier may still use it; while the call's stream is being
+ * captured into a graph it fails with LNSKV_ERR_WORKSPACE instead.
+ * lnskv_workspace_reserve grows them ahead of time (call it before capturing
+ * a graph that passes NULL workspaces); lnskv_workspace_release waits for the
+ * current device (hipDeviceSynchronize) and frees them all, outgrown ones
+ * included.  Both act on the current device.
+ * ------------------------------------------------------------------------- */
+int lnskv_workspace_reserve(size_t decode_bytes, size_t rope_bytes, size_t q4l_bytes);
+int lnskv_workspace_release(void);
+
 /* ===========================================================================
  * Host-side page bookkeeping (no device memory; usable without a GPU).
  * ========================================================================= */
@@ -398,6 +435,19 @@ int lnskv_evict_kv_pages(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t s
                          int32_t pos, int32_t window);
 /* kv_p_start (engine.rs:3007-3013): pos - window + 1 clamped at 0, or 0. */
 int32_t lnskv_kv_p_start(int32_t pos, int32_t window);
+/* The per-token page step of a sliding-window layer with the reference's
+ * exhaustion fixed: evict_kv_pages(pos, window) first, then
+ * ensure_kv_page(pos).  The reference calls them the other way round
+ * (engine.rs:1601-1603, 3231-3232) on a pool of ceil(window/16) pages
+ * (engine.rs:726-730), which runs dry as soon as a window starts mid-page.
+ * With window <= 0 it is ensure_kv_page alone. */
+int lnskv_step_pages(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t layer, int32_t seq,
+                     int32_t pos, int32_t window);
+/* Pages a pool needs per sequence so that lnskv_step_pages never exhausts it
+ * for a window of `window` tokens: the most pages any window of that many
+ * consecutive positions touches, (window + 14) / 16 + 1.  0 for window <= 0
+ * (full attention: the context length decides). */
+int32_t lnskv_window_pages(int32_t window);
 /* Free every page of row seq (sequence finished or evicted) and empty it. */
 int lnskv_free_sequence(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t seq);
 /* Copy-on-write fork: row child becomes a view of the first n_tok tokens of

@@ -473,7 +473,6 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
                                           const PieceOut& po, lds_u8* rope_table = nullptr) {
   const int lane = threadIdx.x;
   const int g = lane >> 4, n = lane & 15;
-  const bool qcol = n < 2 * REP;
 
   Stream sm;
   sm.k_pages = a.k_pages;
@@ -943,7 +942,7 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
 // Sequences are taken 64 at a time: group g holds sequences 64g .. 64g+63,
 // one per lane.  Per-lane view of sequence 64g + lane (past n_seq: empty).
 struct SkSeq {
-  int L;     // length, clamped as seq_window clamps it
+  int L;     // length, 0 when out of range (as in seq_window)
   int p0;    // window start
   int lo;    // first position that owns a page of the segment
   int np;    // pages per (sequence, kv head) segment
@@ -959,7 +958,9 @@ __device__ __forceinline__ SkSeq sk_fields(const DecodeArgs& a, int s, int n_seq
     L = a.kv_len ? a.kv_len[s] : a.kv_len_scalar;
     p0 = a.p_start ? a.p_start[s] : a.p_start_scalar;
   }
-  L = min(max(L, 0), min(a.max_kv_len, a.bt_stride * kPage));
+  // a length past what the grid or the table row can address marks the
+  // sequence out of range: empty window, nothing stored
+  L = L > min(a.max_kv_len, a.bt_stride * kPage) ? 0 : max(L, 0);
   p0 = min(max(p0, 0), L);
   int lo = p0;
   if (FUSED && L > 0) lo = min(lo, L - 1);
@@ -1256,7 +1257,8 @@ template int launch_decode_mfma_sk<true>(const DecodeArgs&, int, int, int, bool,
 // ---------------------------------------------------------------------------
 // Chunked prefill over pages.  The chunk's K/V are already in the pages; a
 // query at position P attends the window [p_start, P] of its sequence, as the
-// decode would with kv_len = P + 1.
+// decode would with kv_len = P + 1 -- or, for a sliding window w > 0,
+// [max(p_start, P - w + 1), P], the reference's per-token kv_p_start.
 //
 // Workgroup = (tile of QT queries of one chunk, kv head), eight waves.  The
 // workgroup streams the tile's window two pages (32 tokens) at a time through
@@ -1347,14 +1349,16 @@ __device__ __forceinline__ void pf_issue(const PrefillArgs& a, const PfLanes& pl
 }
 
 // MODE 0: every token of the pair is attended by every query of the wave;
-// 1: causal masks only; 2: some tokens are outside the window or on a missing
+// 1: per-query masks only (causal, and the query's own sliding window
+// [qlo, qpos]); 2: some tokens are outside the tile's window or on a missing
 // page: mask them and zero their V rows (stale LDS or page bytes may hold NaN
 // patterns, and 0 * NaN would reach the accumulators).
 template <int HW, int MODE>
 __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW], float (&l)[HW],
                                            const half8 (&qh)[HW][4], const half8 (&ql)[HW][4],
                                            const float (&qexp)[HW], const PfLanes& pl, lds_u8* slot, int tok0,
-                                           bool v0, bool v1, int ta, int tb, int qpos, bool qok, int g, int n) {
+                                           bool v0, bool v1, int ta, int tb, int qpos, int qlo, bool qok, int g,
+                                           int n) {
   if constexpr (MODE == 2) {
 #pragma unroll
     for (int p = 0; p < 2; ++p)
@@ -1422,7 +1426,7 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int t = tok0 + 16 * (e >> 2) + 4 * g + (e & 3);
-        if (!(qok && ((e >> 2) ? v1 : v0) && t >= ta && t < tb && t <= qpos)) s[e] = -INFINITY;
+        if (!(qok && ((e >> 2) ? v1 : v0) && t >= qlo && t < tb && t <= qpos)) s[e] = -INFINITY;
       }
     }
     float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
@@ -1530,7 +1534,10 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
   const int p_last = pos0 + qn - 1;
   int p0 = a.p_start ? a.p_start[s] : 0;
   p0 = min(max(p0, 0), p_last);
-  const int ta = p0, tb = min(p_last + 1, a.bt_stride * kPage);
+  // a sliding window gives query P the start max(p0, P - window + 1); the
+  // tile reads from its first query's start
+  const int ta = a.window > 0 ? max(p0, pos0 - a.window + 1) : p0;
+  const int tb = min(p_last + 1, a.bt_stride * kPage);
 
   // this wave: queries [wq, wq + qn_w) of the tile, heads h0 .. h0 + HW - 1
   const int qg = w / WPQ;
@@ -1541,6 +1548,10 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
   const int h0 = kvh * REP + (w % WPQ) * HW;
   const bool qok = n < qn_w;
   const int qpos = wq + n;
+  const int qlo = a.window > 0 ? max(ta, qpos - a.window + 1) : ta;  // this lane's query's window start
+  // the largest window start among the wave's queries: pairs from there on
+  // need no window mask
+  const int wlo = a.window > 0 ? max(ta, wq + max(qn_w, 1) - a.window) : ta;
 
   // table window of 64 entries (lane j: entry base + j)
   const uint32_t* bt_row = a.bt + (size_t)s * a.bt_stride;
@@ -1662,12 +1673,12 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
       const bool v0 = (vbits >> (2 * sl)) & 1u, v1 = (vbits >> (2 * sl + 1)) & 1u;
       const int tok0 = (pg_first + 2 * i) * kPage;
       const bool whole = v0 && v1 && tok0 >= ta && tok0 + 2 * kPage <= tb;
-      if (whole && tok0 + 2 * kPage - 1 <= wq)
-        pf_consume<HW, 0>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qok, g, n);
+      if (whole && tok0 + 2 * kPage - 1 <= wq && tok0 >= wlo)
+        pf_consume<HW, 0>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n);
       else if (whole)
-        pf_consume<HW, 1>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qok, g, n);
+        pf_consume<HW, 1>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n);
       else
-        pf_consume<HW, 2>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qok, g, n);
+        pf_consume<HW, 2>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n);
     }
   }
   if (!active) return;

@@ -186,11 +186,11 @@ __device__ __forceinline__ void fused_new_token(const DecodeArgs& a, WaveState<D
   } else if constexpr (DT == LNSKV_DTYPE_F16) {
 #pragma unroll
     for (int e = 0; e < G::EPL; ++e) {
-      const _Float16 hk = (_Float16)kx[e], hv = (_Float16)vx[e];
-      kst[e] = (float)hk;
-      vst[e] = (float)hv;
-      kw[e / 2] |= (uint32_t)__builtin_bit_cast(uint16_t, hk) << (16 * (e & 1));
-      vw[e / 2] |= (uint32_t)__builtin_bit_cast(uint16_t, hv) << (16 * (e & 1));
+      const uint32_t hk = to_f16_bits(kx[e]), hv = to_f16_bits(vx[e]);
+      kst[e] = (float)__builtin_bit_cast(_Float16, (uint16_t)hk);
+      vst[e] = (float)__builtin_bit_cast(_Float16, (uint16_t)hv);
+      kw[e / 2] |= hk << (16 * (e & 1));
+      vw[e / 2] |= hv << (16 * (e & 1));
     }
   } else {
     float ka = 0.0f, va = 0.0f;

@@ -104,11 +104,16 @@ __device__ __forceinline__ void rope_sincos(float theta, float* s, float* c) {
 }
 
 // Converts one f32 to the page dtype's bits; Q8A needs the head's scale.
-// f16: v_cvt_f16_f32 under the default round-to-nearest-even mode.
+// f16: v_cvt_f16_f32 under the default round-to-nearest-even mode for numbers.
 // Q8A: IEEE division (HIP's correctly rounded f32 divide), roundf = half away
 // from zero, clamp to [-127, 127] (metal:562-567).
+// A NaN becomes the quiet f16 NaN with its sign and the top 10 bits of its
+// payload (the IEEE conversion's narrowing; the hardware conversion would
+// return its own canonical NaN).
 __device__ __forceinline__ uint32_t to_f16_bits(float x) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const uint32_t h = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+  return (u & 0x7FFFFFFFu) > 0x7F800000u ? (((u >> 16) & 0x8000u) | 0x7E00u | ((u >> 13) & 0x3FFu)) : h;
 }
 __device__ __forceinline__ int32_t to_q8(float x, float sc) {
   float r = roundf(x / sc);
@@ -159,7 +164,7 @@ __device__ __forceinline__ float gated(const DecodeArgs& a, size_t idx, float v)
 }
 
 struct SeqWindow {
-  int L;       // kv_len clamped to what the grid and the table can address
+  int L;       // kv_len; 0 when it is past what the grid or the table row can address
   int p0;      // window start
   int jf;      // first partition index
   int nparts;  // partitions of this sequence
@@ -169,7 +174,9 @@ template <bool FUSED>
 __device__ __forceinline__ SeqWindow seq_window(const DecodeArgs& a, int s) {
   SeqWindow w;
   int L = a.kv_len ? a.kv_len[s] : a.kv_len_scalar;
-  L = min(max(L, 0), min(a.max_kv_len, a.bt_stride * kPage));
+  // a length past what the grid or the table row can address marks the
+  // sequence out of range: empty window, nothing stored
+  L = L > min(a.max_kv_len, a.bt_stride * kPage) ? 0 : max(L, 0);
   int p0 = a.p_start ? a.p_start[s] : a.p_start_scalar;
   p0 = min(max(p0, 0), L);
   int lo = p0;
@@ -358,6 +365,7 @@ struct PrefillArgs {
   const int4* chunks;      // [n_chunks]: {table row, first position, length, first token}
   const uint32_t* bt;      // [n_rows][bt_stride]
   const int32_t* p_start;  // [n_rows] window starts, or nullptr (0)
+  int32_t window;          // > 0: sliding window, query P starts at max(p_start, P - window + 1)
   int32_t n_chunks;
   int32_t n_tok;
   int32_t n_rows;
@@ -372,10 +380,11 @@ int prefill_queries_per_tile(int rep);
 int launch_prefill_mfma(const PrefillArgs& a, int rep, int n_tiles, hipStream_t st);
 
 int hip_check(const char* what);
-// A device buffer the library keeps per device and grows on demand (hipMalloc;
-// growing synchronizes the device first): 0 the decode workspace, 1 RoPE'd
-// q/k rows, 2 the Q4L GEMV's x operands.  Calls that share one must not
-// overlap in time.
-int library_buffer(int which, size_t need, void** out);
+// A device buffer the library keeps per device: 0 the decode workspace, 1
+// RoPE'd q/k rows, 2 the Q4L GEMV's x operands.  Growing it allocates a new
+// buffer and keeps the old one until lnskv_workspace_release (no device
+// synchronization inside a call); during stream capture it fails with
+// LNSKV_ERR_WORKSPACE instead.  Calls that share one must not overlap in time.
+int library_buffer(int which, size_t need, void** out, hipStream_t stream);
 
 }  // namespace lnskv

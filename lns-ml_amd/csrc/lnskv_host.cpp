@@ -290,6 +290,24 @@ int lnskv_evict_kv_pages(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t s
   return LNSKV_OK;
 }
 
+// The engine sizes a sliding-window layer's pool at ceil(w/16) pages
+// (engine.rs:726-730) and calls ensure_kv_page before evict_kv_pages
+// (engine.rs:1601-1603, 3231-3232).  A window whose start is not page-aligned
+// spans one page more than that, so the pool runs dry at the first position
+// where it does.  lnskv_step_pages evicts first and then ensures, and
+// lnskv_window_pages gives the page count that order needs.
+int32_t lnskv_window_pages(int32_t window) {
+  if (window <= 0) return 0;
+  // [p, p + w - 1] touches pages p/16 .. (p + w - 1)/16: at most (w - 1 + 15)/16 + 1
+  return (int32_t)(((int64_t)window + LNSKV_PAGE_SIZE - 2) / LNSKV_PAGE_SIZE + 1);
+}
+
+int lnskv_step_pages(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t layer, int32_t seq, int32_t pos,
+                     int32_t window) {
+  if (int rc = lnskv_evict_kv_pages(t, pool, seq, pos, window)) return rc;
+  return lnskv_ensure_kv_page(t, pool, layer, seq, pos);
+}
+
 int lnskv_free_sequence(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t seq) {
   if (!row_ok(t, seq) || !pool) return fail(LNSKV_ERR_INVALID, "bad table/pool or seq %d", seq);
   uint32_t* row = t->table.data() + (size_t)seq * (size_t)t->max_pages;

@@ -422,8 +422,12 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
 
 }  // namespace
 
-// Library-kept buffers per device, grown on demand: 0 decode workspace,
-// 1 RoPE rows, 2 Q4L x operands.
+// Library-kept buffers per device: 0 decode workspace, 1 RoPE rows, 2 Q4L x
+// operands.  A call that finds its buffer too small allocates a larger one and
+// keeps the old one alive (kernels queued earlier may still read it) until
+// lnskv_workspace_release: no call that enqueues work synchronizes the device
+// or frees memory.  While the call's stream is being captured into a graph it
+// allocates nothing and fails instead (reserve the buffers before capturing).
 namespace {
 constexpr int kLibraryBuffers = 3;
 struct DeviceWorkspace {
@@ -431,32 +435,50 @@ struct DeviceWorkspace {
   size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::vector<DeviceWorkspace> g_ws;  // [device * kLibraryBuffers + which]
+std::vector<DeviceWorkspace> g_ws;       // [device * kLibraryBuffers + which]
+std::vector<std::pair<int, void*>> g_ws_retired;  // (device, pointer) outgrown, freed on release
+
+const char* kBufferName[kLibraryBuffers] = {"decode workspace", "RoPE rows", "Q4L operands"};
+
+// grows buffer `which` of device `dev` to at least `need` bytes (lock held)
+int grow_locked(int dev, int which, size_t need) {
+  const size_t slot = (size_t)dev * kLibraryBuffers + (size_t)which;
+  if (g_ws.size() <= slot) g_ws.resize((size_t)(dev + 1) * kLibraryBuffers);
+  DeviceWorkspace& w = g_ws[slot];
+  if (w.bytes >= need) return LNSKV_OK;
+  const size_t grow = std::max({need, (size_t)1 << 20, w.bytes + w.bytes / 2});
+  void* p = nullptr;
+  if (hipMalloc(&p, grow) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(LNSKV_ERR_NOMEM, "library %s of %zu bytes: hipMalloc failed", kBufferName[which], grow);
+  }
+  if (w.ptr) g_ws_retired.emplace_back(dev, w.ptr);
+  w.ptr = p;
+  w.bytes = grow;
+  return LNSKV_OK;
+}
 }  // namespace
 
-int library_buffer(int which, size_t need, void** out) {
+int library_buffer(int which, size_t need, void** out, hipStream_t stream) {
   if (which < 0 || which >= kLibraryBuffers) return fail(LNSKV_ERR_INVALID, "library buffer %d", which);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
   std::lock_guard<std::mutex> lock(g_ws_mutex);
   const size_t slot = (size_t)dev * kLibraryBuffers + (size_t)which;
-  if (g_ws.size() <= slot) g_ws.resize((size_t)(dev + 1) * kLibraryBuffers);
-  DeviceWorkspace& w = g_ws[slot];
-  if (w.bytes < need) {
-    if (w.ptr) {
-      // Kernels queued earlier may still use the old buffer.
-      if (hipDeviceSynchronize() != hipSuccess) return fail(LNSKV_ERR_HIP, "hipDeviceSynchronize failed");
-      (void)hipFree(w.ptr);
-      w = DeviceWorkspace{};
+  if (g_ws.size() <= slot || g_ws[slot].bytes < need) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(LNSKV_ERR_HIP, "hipStreamIsCapturing failed");
     }
-    const size_t grow = std::max(need, (size_t)1 << 20);
-    if (hipMalloc(&w.ptr, grow) != hipSuccess) {
-      w = DeviceWorkspace{};
-      return fail(LNSKV_ERR_NOMEM, "workspace of %zu bytes: hipMalloc failed", grow);
-    }
-    w.bytes = grow;
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(LNSKV_ERR_WORKSPACE,
+                  "the library %s holds %zu bytes, this call needs %zu, and the stream is being captured: "
+                  "pass a workspace or call lnskv_workspace_reserve before capturing",
+                  kBufferName[which], g_ws.size() > slot ? g_ws[slot].bytes : (size_t)0, need);
+    if (int rc = grow_locked(dev, which, need)) return rc;
   }
-  *out = w.ptr;
+  *out = g_ws[slot].ptr;
   return LNSKV_OK;
 }
 
@@ -502,7 +524,7 @@ int noalloc_scratch(void** out) {
 }
 
 namespace {
-int library_workspace(size_t need, void** out) { return library_buffer(0, need, out); }
+int library_workspace(size_t need, void** out, hipStream_t st) { return library_buffer(0, need, out, st); }
 
 // Checks a RoPE descriptor against head_dim; half = rotary_dim / 2.
 int check_rope(const lnskv_rope* rope, int d, int* half) {
@@ -513,6 +535,10 @@ int check_rope(const lnskv_rope* rope, int d, int* half) {
   return LNSKV_OK;
 }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Where the rotated q/k rows of a RoPE call start in a caller's workspace:
+// after the decode's part, on a 256-byte boundary.
+size_t rope_rows_offset(size_t decode_bytes) { return (decode_bytes + 255) & ~(size_t)255; }
 
 template <bool FUSED>
 int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const float* v_new,
@@ -535,42 +561,49 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
   const int rep = n_heads / (int)c->n_kv_heads;
   const int d = (int)c->head_dim;
   // RoPE: turned inside the MFMA kernels for rotary widths 64 and 128 of
-  // 128-wide heads; otherwise q and k_new are turned into a library buffer
-  // first and that is what the decode reads
+  // 128-wide heads; otherwise q and k_new are turned first into rows that the
+  // decode then reads: in the caller's workspace after the decode's part, or
+  // in a library buffer when the caller passes none
   int rope_half = 0;
+  bool rope_rows = false;
   if (rope) {
     if (!FUSED) return fail(LNSKV_ERR_INVALID, "RoPE needs the fused append");
     if (int rc = check_rope(rope, d, &rope_half)) return rc;
-    const bool in_kernel = mfma_path((int)c->dtype, d, rep) && d == 128 && (rope_half == 32 || rope_half == 64) &&
-                           aligned16(rope->inv_freqs_dev);
-    if (!in_kernel) {
-      const size_t qn = (size_t)n_seq * n_heads * d, kn = (size_t)n_seq * c->n_kv_heads * d;
-      void* buf = nullptr;
-      if (int rc = library_buffer(1, (qn + kn) * sizeof(float), &buf)) return rc;
-      float* qr = static_cast<float*>(buf);
-      float* kr = qr + qn;
-      const hipStream_t st = (hipStream_t)stream;
-      rope_rows_kernel<<<(unsigned)n_seq, kBlock, 0, st>>>(q, qr, n_heads, d, rope_half, rope->inv_freqs_dev, kv_len,
-                                                          kv_len_scalar, nullptr);
-      rope_rows_kernel<<<(unsigned)n_seq, kBlock, 0, st>>>(k_new, kr, (int)c->n_kv_heads, d, rope_half,
-                                                          rope->inv_freqs_dev, kv_len, kv_len_scalar, nullptr);
-      if (int rc = hip_check("rope kernel launch")) return rc;
-      q = qr;
-      k_new = kr;
-      rope_half = 0;
-    }
+    rope_rows = !(mfma_path((int)c->dtype, d, rep) && d == 128 && (rope_half == 32 || rope_half == 64) &&
+                  aligned16(rope->inv_freqs_dev));
   }
   DecodePlan plan;
   if (int rc = plan_decode(c, n_seq, n_heads, max_kv_len, split, FUSED ? 1 : 0, &plan)) return rc;
   const size_t need = plan.ws_bytes;
-  if (need > 0) {
-    if (ws == nullptr) {
-      if (int rc = library_workspace(need, &ws)) return rc;
-    } else if (ws_bytes < need) {
-      return fail(LNSKV_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed", ws_bytes, need);
-    } else if (reinterpret_cast<uintptr_t>(ws) % 16 != 0) {
-      return fail(LNSKV_ERR_WORKSPACE, "workspace must be 16-byte aligned");
-    }
+  const size_t qn = (size_t)n_seq * n_heads * d, kn = (size_t)n_seq * c->n_kv_heads * d;
+  const size_t rope_off = rope_rows_offset(need);
+  const size_t rope_bytes = rope_rows ? (qn + kn) * sizeof(float) : 0;
+  const hipStream_t st = (hipStream_t)stream;
+  void* rope_buf = nullptr;
+  if (ws == nullptr) {
+    if (need > 0)
+      if (int rc = library_workspace(need, &ws, st)) return rc;
+    if (rope_rows)
+      if (int rc = library_buffer(1, rope_bytes, &rope_buf, st)) return rc;
+  } else {
+    if (reinterpret_cast<uintptr_t>(ws) % 16 != 0) return fail(LNSKV_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+    const size_t total = rope_rows ? rope_off + rope_bytes : need;
+    if (ws_bytes < total)
+      return fail(LNSKV_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed%s", ws_bytes, total,
+                  rope_rows ? " (decode partials, then the rotated q and k rows)" : "");
+    if (rope_rows) rope_buf = static_cast<uint8_t*>(ws) + rope_off;
+  }
+  if (rope_rows) {
+    float* qr = static_cast<float*>(rope_buf);
+    float* kr = qr + qn;
+    rope_rows_kernel<<<(unsigned)n_seq, kBlock, 0, st>>>(q, qr, n_heads, d, rope_half, rope->inv_freqs_dev, kv_len,
+                                                        kv_len_scalar, nullptr);
+    rope_rows_kernel<<<(unsigned)n_seq, kBlock, 0, st>>>(k_new, kr, (int)c->n_kv_heads, d, rope_half,
+                                                        rope->inv_freqs_dev, kv_len, kv_len_scalar, nullptr);
+    if (int rc = hip_check("rope kernel launch")) return rc;
+    q = qr;
+    k_new = kr;
+    rope_half = 0;
   }
   DecodeArgs a{};
   a.k_pages = static_cast<const uint8_t*>(c->k_pages);
@@ -676,7 +709,7 @@ namespace lnskv {
 namespace {
 int append_entry(const lnskv_pages* c, const lnskv_rope* rope, const float* k_new, const float* v_new,
                  const int32_t* tok_seq, const int32_t* tok_pos, int32_t n_tok, const uint32_t* bt,
-                 int32_t bt_stride, int32_t n_rows, lnskv_stream_t stream) {
+                 int32_t bt_stride, int32_t n_rows, void* ws, size_t ws_bytes, lnskv_stream_t stream) {
   clear_error();
   if (int rc = check_pages(c)) return rc;
   if (n_tok < 0) return fail(LNSKV_ERR_INVALID, "n_tok %d is negative", n_tok);
@@ -707,8 +740,8 @@ int append_entry(const lnskv_pages* c, const lnskv_rope* rope, const float* k_ne
   const hipStream_t st = (hipStream_t)stream;
   if (rope) {
     // turned in the vector kernel when its lanes can pair up (half a multiple
-    // of 8 with half/8 a power of two); otherwise K goes through a library
-    // buffer first
+    // of 8 with half/8 a power of two); otherwise K is turned first into rows
+    // in the caller's workspace (or a library buffer when there is none)
     int half = 0;
     if (int rc = check_rope(rope, d, &half)) return rc;
     const int m = half / 8;
@@ -720,7 +753,16 @@ int append_entry(const lnskv_pages* c, const lnskv_rope* rope, const float* k_ne
       a.rope_half = half;
     } else {
       void* buf = nullptr;
-      if (int rc = library_buffer(1, (size_t)n_tok * c->n_kv_heads * d * sizeof(float), &buf)) return rc;
+      const size_t need = (size_t)n_tok * c->n_kv_heads * d * sizeof(float);
+      if (ws == nullptr) {
+        if (int rc = library_buffer(1, need, &buf, st)) return rc;
+      } else if (ws_bytes < need) {
+        return fail(LNSKV_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed for the rotated K rows", ws_bytes, need);
+      } else if (!aligned16(ws)) {
+        return fail(LNSKV_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+      } else {
+        buf = ws;
+      }
       rope_rows_kernel<<<(unsigned)n_tok, kBlock, 0, st>>>(k_new, static_cast<float*>(buf), (int)c->n_kv_heads, d,
                                                           half, rope->inv_freqs_dev, nullptr, 0, tok_pos);
       if (int rc = hip_check("rope kernel launch")) return rc;
@@ -739,17 +781,17 @@ int append_entry(const lnskv_pages* c, const lnskv_rope* rope, const float* k_ne
 int lnskv_append(const lnskv_pages* c, const float* k_new, const float* v_new,
                  const int32_t* tok_seq, const int32_t* tok_pos, int32_t n_tok,
                  const uint32_t* bt, int32_t bt_stride, int32_t n_rows, lnskv_stream_t stream) {
-  return append_entry(c, nullptr, k_new, v_new, tok_seq, tok_pos, n_tok, bt, bt_stride, n_rows, stream);
+  return append_entry(c, nullptr, k_new, v_new, tok_seq, tok_pos, n_tok, bt, bt_stride, n_rows, nullptr, 0, stream);
 }
 
 int lnskv_rope_append(const lnskv_pages* c, const lnskv_rope* rope, const float* k_new, const float* v_new,
                       const int32_t* tok_seq, const int32_t* tok_pos, int32_t n_tok, const uint32_t* bt,
-                      int32_t bt_stride, int32_t n_rows, lnskv_stream_t stream) {
+                      int32_t bt_stride, int32_t n_rows, void* ws, size_t ws_bytes, lnskv_stream_t stream) {
   if (!rope) {
     clear_error();
     return fail(LNSKV_ERR_INVALID, "rope must be non-null");
   }
-  return append_entry(c, rope, k_new, v_new, tok_seq, tok_pos, n_tok, bt, bt_stride, n_rows, stream);
+  return append_entry(c, rope, k_new, v_new, tok_seq, tok_pos, n_tok, bt, bt_stride, n_rows, ws, ws_bytes, stream);
 }
 
 int lnskv_decode_workspace_size(const lnskv_pages* c, int32_t n_seq, int32_t n_heads,
@@ -763,6 +805,71 @@ int lnskv_decode_workspace_size(const lnskv_pages* c, int32_t n_seq, int32_t n_h
   DecodePlan plan;
   if (int rc = plan_decode(c, n_seq, n_heads, max_kv_len, split_tokens, -1, &plan)) return rc;
   *bytes = plan.ws_bytes;
+  return LNSKV_OK;
+}
+
+int lnskv_rope_decode_workspace_size(const lnskv_pages* c, const lnskv_rope* rope, int32_t n_seq, int32_t n_heads,
+                                     int32_t max_kv_len, int32_t split_tokens, size_t* bytes) {
+  clear_error();
+  if (!bytes) return fail(LNSKV_ERR_INVALID, "bytes is NULL");
+  *bytes = 0;
+  if (int rc = check_geometry(c)) return rc;
+  if (n_seq <= 0 || n_heads <= 0 || max_kv_len < 0 || split_tokens < 0 || n_heads % (int)c->n_kv_heads != 0)
+    return fail(LNSKV_ERR_INVALID, "bad shape");
+  int half = 0;
+  if (int rc = check_rope(rope, (int)c->head_dim, &half)) return rc;
+  DecodePlan plan;
+  if (int rc = plan_decode(c, n_seq, n_heads, max_kv_len, split_tokens, 1, &plan)) return rc;
+  // room for the rotated rows whatever path the call takes
+  *bytes = rope_rows_offset(plan.ws_bytes) + (size_t)n_seq * (n_heads + c->n_kv_heads) * c->head_dim * sizeof(float);
+  return LNSKV_OK;
+}
+
+int lnskv_rope_append_workspace_size(const lnskv_pages* c, const lnskv_rope* rope, int32_t n_tok, size_t* bytes) {
+  clear_error();
+  if (!bytes) return fail(LNSKV_ERR_INVALID, "bytes is NULL");
+  *bytes = 0;
+  if (int rc = check_geometry(c)) return rc;
+  if (n_tok < 0) return fail(LNSKV_ERR_INVALID, "n_tok %d is negative", n_tok);
+  int half = 0;
+  if (int rc = check_rope(rope, (int)c->head_dim, &half)) return rc;
+  *bytes = (size_t)n_tok * c->n_kv_heads * c->head_dim * sizeof(float);
+  return LNSKV_OK;
+}
+
+int lnskv_workspace_reserve(size_t decode_bytes, size_t rope_bytes, size_t q4l_bytes) {
+  clear_error();
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  const size_t want[kLibraryBuffers] = {decode_bytes, rope_bytes, q4l_bytes};
+  for (int i = 0; i < kLibraryBuffers; ++i)
+    if (want[i] > 0)
+      if (int rc = grow_locked(dev, i, want[i])) return rc;
+  return LNSKV_OK;
+}
+
+int lnskv_workspace_release(void) {
+  clear_error();
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  if (hipDeviceSynchronize() != hipSuccess) return fail(LNSKV_ERR_HIP, "hipDeviceSynchronize failed");
+  for (auto it = g_ws_retired.begin(); it != g_ws_retired.end();) {
+    if (it->first == dev) {
+      (void)hipFree(it->second);
+      it = g_ws_retired.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  for (int i = 0; i < kLibraryBuffers; ++i) {
+    const size_t slot = (size_t)dev * kLibraryBuffers + (size_t)i;
+    if (slot < g_ws.size() && g_ws[slot].ptr) {
+      (void)hipFree(g_ws[slot].ptr);
+      g_ws[slot] = DeviceWorkspace{};
+    }
+  }
   return LNSKV_OK;
 }
 
@@ -823,7 +930,8 @@ int lnskv_gated_append_decode(const lnskv_pages* c, const lnskv_rope* rope, cons
 
 int lnskv_prefill_attention(const lnskv_pages* c, const float* q, float* out, const int32_t* chunks,
                             int32_t n_chunks, int32_t n_tok, const uint32_t* bt, int32_t bt_stride, int32_t n_rows,
-                            const int32_t* p_start, int32_t n_heads, float scale, lnskv_stream_t stream) {
+                            const int32_t* p_start, int32_t window, int32_t n_heads, float scale,
+                            lnskv_stream_t stream) {
   clear_error();
   if (int rc = check_pages(c)) return rc;
   if (!q || !out || !chunks || !bt) return fail(LNSKV_ERR_INVALID, "q, out, chunks and block tables must be non-null");
@@ -834,6 +942,7 @@ int lnskv_prefill_attention(const lnskv_pages* c, const float* q, float* out, co
   if (n_heads <= 0 || n_heads % (int)c->n_kv_heads != 0)
     return fail(LNSKV_ERR_INVALID, "n_heads %d is not a multiple of n_kv_heads %u", n_heads, c->n_kv_heads);
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(LNSKV_ERR_INVALID, "scale must be positive and finite");
+  if (window < 0) return fail(LNSKV_ERR_INVALID, "window %d is negative", window);
   if (c->dtype != LNSKV_DTYPE_F16 || c->head_dim != 128)
     return fail(LNSKV_ERR_UNSUPPORTED, "prefill attention is built for f16 pages with head_dim 128");
   if (!aligned16(chunks) || !aligned16(q)) return fail(LNSKV_ERR_INVALID, "chunks and q must be 16-byte aligned");
@@ -845,6 +954,7 @@ int lnskv_prefill_attention(const lnskv_pages* c, const float* q, float* out, co
   a.chunks = reinterpret_cast<const int4*>(chunks);
   a.bt = bt;
   a.p_start = p_start;
+  a.window = window;
   a.n_chunks = n_chunks;
   a.n_tok = n_tok;
   a.n_rows = n_rows;

@@ -339,7 +339,7 @@ extern "C" int lnskv_q4l_gemv_accumulate(const void* blocks_dev, const float* x_
   }
   const size_t need = q4l_ws_bytes(cols, n_vec);
   if (ws == nullptr) {
-    if (int rc = library_buffer(2, need, &ws)) return rc;
+    if (int rc = library_buffer(2, need, &ws, st)) return rc;
   } else if (ws_bytes < need) {
     return fail(LNSKV_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed", ws_bytes, need);
   } else if ((reinterpret_cast<uintptr_t>(ws) & 15) != 0) {

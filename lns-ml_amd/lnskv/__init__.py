@@ -8,7 +8,7 @@ Python surface over liblnskv.so (C ABI in include/lnskv.h):
 """
 from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_NAMES, DTYPE_Q8A, LIB_PATH, NO_PAGE, PAGE_SIZE,
                    SIGNATURES, LnskvError, lib)
-from .host import BlockTables, PagePool, kv_p_start
+from .host import BlockTables, PagePool, kv_p_start, window_pages
 
 __all__ = ["DTYPE_F16", "DTYPE_F32", "DTYPE_Q8A", "DTYPE_NAMES", "LIB_PATH", "NO_PAGE", "PAGE_SIZE",
-           "SIGNATURES", "LnskvError", "lib", "BlockTables", "PagePool", "kv_p_start"]
+           "SIGNATURES", "LnskvError", "lib", "BlockTables", "PagePool", "kv_p_start", "window_pages"]

@@ -83,6 +83,8 @@ SIGNATURES = {
     "lnskv_page_copy": (C.c_int, [_P, _vp, _vp, _i32, _vp]),
     "lnskv_gather": (C.c_int, [_P, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "lnskv_sync": (C.c_int, [_vp]),
+    "lnskv_workspace_reserve": (C.c_int, [_sz, _sz, _sz]),
+    "lnskv_workspace_release": (C.c_int, []),
     "lnskv_page_pool_create": (C.c_int, [_u32, C.POINTER(_vp)]),
     "lnskv_page_pool_destroy": (None, [_vp]),
     "lnskv_page_pool_alloc": (C.c_int, [_vp, C.POINTER(_u32)]),
@@ -101,16 +103,21 @@ SIGNATURES = {
     "lnskv_ensure_kv_page": (C.c_int, [_vp, _vp, _i32, _i32, _i32]),
     "lnskv_evict_kv_pages": (C.c_int, [_vp, _vp, _i32, _i32, _i32]),
     "lnskv_kv_p_start": (_i32, [_i32, _i32]),
+    "lnskv_step_pages": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32]),
+    "lnskv_window_pages": (_i32, [_i32]),
     "lnskv_free_sequence": (C.c_int, [_vp, _vp, _i32]),
     "lnskv_fork_sequence": (
         C.c_int, [_vp, _vp, _i32, _i32, _i32, C.POINTER(_u32), C.POINTER(_u32), C.POINTER(_i32)]),
     "lnskv_block_tables_upload": (C.c_int, [_vp, _vp, _vp]),
     "lnskv_rope_dim": (_i32, [_i32, _f32]),
     "lnskv_rope_inv_freqs": (C.c_int, [_i32, _f32, _i32, _vp, _vp]),
-    "lnskv_rope_append": (C.c_int, [_P, _R, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp]),
+    "lnskv_rope_append_workspace_size": (C.c_int, [_P, _R, _i32, C.POINTER(_sz)]),
+    "lnskv_rope_append": (C.c_int, [_P, _R, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _sz, _vp]),
+    "lnskv_rope_decode_workspace_size": (C.c_int, [_P, _R, _i32, _i32, _i32, _i32, C.POINTER(_sz)]),
     "lnskv_rope_append_decode": (
         C.c_int, [_P, _R, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _sz, _vp]),
-    "lnskv_prefill_attention": (C.c_int, [_P, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _i32, _f32, _vp]),
+    "lnskv_prefill_attention": (C.c_int, [_P, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _i32, _i32, _f32,
+                                          _vp]),
     "lnskv_split_gated_query": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "lnskv_gated_append_decode": (
         C.c_int, [_P, _R, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _sz,

@@ -150,8 +150,23 @@ class PagedKV:
                                         _stream(self.device)))
         return out
 
-    def rope_append(self, rope: "RopeTable", k_new, v_new, tok_seq, tok_pos, tables) -> None:
-        """lnskv_rope_append: lnskv_append with K turned by tok_pos first."""
+    def rope_decode_workspace_size(self, rope: "RopeTable", n_seq: int, n_heads: int, max_kv_len: int,
+                                   split: int = 0) -> int:
+        """Bytes of workspace lnskv_rope_append_decode / lnskv_gated_append_decode
+        with this rope need (the decode's partials, then the rotated rows)."""
+        out = C.c_size_t()
+        check(lib().lnskv_rope_decode_workspace_size(C.byref(self.desc), C.byref(rope.desc), n_seq, n_heads,
+                                                     max_kv_len, split, C.byref(out)))
+        return out.value
+
+    def rope_append_workspace_size(self, rope: "RopeTable", n_tok: int) -> int:
+        out = C.c_size_t()
+        check(lib().lnskv_rope_append_workspace_size(C.byref(self.desc), C.byref(rope.desc), n_tok, C.byref(out)))
+        return out.value
+
+    def rope_append(self, rope: "RopeTable", k_new, v_new, tok_seq, tok_pos, tables, workspace=None) -> None:
+        """lnskv_rope_append: lnskv_append with K turned by tok_pos first
+        (workspace None: the library's buffer for shapes that rotate first)."""
         n_tok = int(tok_seq.numel())
         _need(k_new, "k_new", torch.float32, n_tok * self.row_elems, self.device)
         _need(v_new, "v_new", torch.float32, n_tok * self.row_elems, self.device)
@@ -159,9 +174,10 @@ class PagedKV:
         _need(tok_pos, "tok_pos", torch.int32, n_tok, self.device)
         if tables.dim() != 2:
             raise ValueError("block tables must be 2-D")
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
         check(lib().lnskv_rope_append(C.byref(self.desc), C.byref(rope.desc), _ptr(k_new), _ptr(v_new),
                                       _ptr(tok_seq), _ptr(tok_pos), n_tok, _ptr(tables), int(tables.shape[1]),
-                                      int(tables.shape[0]), _stream(self.device)))
+                                      int(tables.shape[0]), _ptr(workspace), ws_bytes, _stream(self.device)))
 
     def rope_append_decode(self, rope: "RopeTable", q, k_new, v_new, tables, kv_len, *, n_heads: int,
                            max_kv_len: int, scale: float, p_start=None, split: int = 0, workspace=None,
@@ -201,10 +217,11 @@ class PagedKV:
                                               _stream(self.device)))
         return out
 
-    def prefill_attention(self, q, chunks, tables, *, n_heads: int, scale: float, p_start=None,
+    def prefill_attention(self, q, chunks, tables, *, n_heads: int, scale: float, p_start=None, window: int = 0,
                           out=None) -> torch.Tensor:
         """lnskv_prefill_attention: q [n_tok][n_heads][d]; chunks int32
-        [n_chunks][4] = (table row, first position, length, first token)."""
+        [n_chunks][4] = (table row, first position, length, first token);
+        window > 0: each query attends its own sliding window."""
         n_tok = q.numel() // (n_heads * self.head_dim)
         _need(q, "q", torch.float32, n_tok * n_heads * self.head_dim, self.device)
         if chunks.dtype != torch.int32 or chunks.dim() != 2 or chunks.shape[1] != 4 or not chunks.is_contiguous():
@@ -216,7 +233,7 @@ class PagedKV:
         _need(out, "out", torch.float32, n_tok * n_heads * self.head_dim, self.device)
         check(lib().lnskv_prefill_attention(C.byref(self.desc), _ptr(q), _ptr(out), _ptr(chunks),
                                             int(chunks.shape[0]), n_tok, _ptr(tables), int(tables.shape[1]),
-                                            int(tables.shape[0]), _ptr(p_start), n_heads, scale,
+                                            int(tables.shape[0]), _ptr(p_start), window, n_heads, scale,
                                             _stream(self.device)))
         return out
 

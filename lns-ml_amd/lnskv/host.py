@@ -110,6 +110,11 @@ class BlockTables:
     def evict_kv_pages(self, pool: PagePool, seq: int, pos: int, window: int) -> None:
         check(lib().lnskv_evict_kv_pages(self._h, pool.handle, seq, pos, window))
 
+    def step_pages(self, pool: PagePool, seq: int, pos: int, window: int, layer: int = 0) -> None:
+        """lnskv_step_pages: evict_kv_pages then ensure_kv_page, the order that
+        needs only window_pages(window) pages per sequence."""
+        check(lib().lnskv_step_pages(self._h, pool.handle, layer, seq, pos, window))
+
     def free_sequence(self, pool: PagePool, seq: int) -> None:
         check(lib().lnskv_free_sequence(self._h, pool.handle, seq))
 
@@ -128,4 +133,10 @@ def kv_p_start(pos: int, window: int) -> int:
     return lib().lnskv_kv_p_start(pos, window)
 
 
-__all__ = ["PagePool", "BlockTables", "kv_p_start", "LnskvError", "NO_PAGE", "PAGE_SIZE"]
+def window_pages(window: int) -> int:
+    """Pages per sequence that lnskv_step_pages needs for a sliding window
+    (0 for full attention)."""
+    return lib().lnskv_window_pages(window)
+
+
+__all__ = ["PagePool", "BlockTables", "kv_p_start", "window_pages", "LnskvError", "NO_PAGE", "PAGE_SIZE"]

@@ -66,8 +66,15 @@ class StepRunner:
         self.chunk_v = torch.randn((len(cs), nkv, d), generator=g, device=self.dev) * w.value_scale
         self.copy_src = _i32(np.array([c[0] for c in w.copies], np.uint32), self.dev)
         self.copy_dst = _i32(np.array([c[1] for c in w.copies], np.uint32), self.dev)
-        ws = self.layers[0].workspace_size(max(self.n_dec, 1), hq, self.max_kv_len, w.split)
-        self.workspace = torch.zeros(max(ws, 4), dtype=torch.uint8, device=self.dev)
+        if self.rope is not None:
+            ws = self.layers[0].rope_decode_workspace_size(self.rope, max(self.n_dec, 1), hq, self.max_kv_len,
+                                                           w.split)
+            ws_chunk = self.layers[0].rope_append_workspace_size(self.rope, len(cs))
+            self.chunk_workspace = torch.empty(max(ws_chunk, 16), dtype=torch.uint8, device=self.dev)
+        else:
+            ws = self.layers[0].workspace_size(max(self.n_dec, 1), hq, self.max_kv_len, w.split)
+            self.chunk_workspace = None
+        self.workspace = torch.zeros(max(ws, 16), dtype=torch.uint8, device=self.dev)
 
     def fill(self, pk: PagedKV, seed: int) -> None:
         g = torch.Generator(device=self.dev)
@@ -88,7 +95,8 @@ class StepRunner:
             pk.page_copy(self.copy_src, self.copy_dst)
         if self.n_chunk_tok:
             if self.rope is not None:
-                pk.rope_append(self.rope, self.chunk_k, self.chunk_v, self.chunk_seq, self.chunk_pos, self.tables)
+                pk.rope_append(self.rope, self.chunk_k, self.chunk_v, self.chunk_seq, self.chunk_pos, self.tables,
+                               workspace=self.chunk_workspace)
             else:
                 pk.append(self.chunk_k, self.chunk_v, self.chunk_seq, self.chunk_pos, self.tables)
         if self.n_dec:
@@ -104,7 +112,9 @@ class StepRunner:
 
     def capture(self, layer: int = 0) -> "torch.cuda.CUDAGraph":
         """One layer's step recorded in a HIP graph (run it eagerly first, so
-        the library's per-device caches are filled before the capture)."""
+        the library's per-device caches are filled before the capture; every
+        call of the step passes its own workspace, so nothing is allocated
+        while capturing)."""
         self.run(layer)
         torch.cuda.synchronize(self.dev)
         g = torch.cuda.CUDAGraph()

@@ -92,3 +92,17 @@ def test_workspace_size_formula():
 @pytest.mark.parametrize("name", ["lnskv_last_error", "lnskv_version"])
 def test_string_entry_points(name):
     assert isinstance(getattr(_lib.lib(), name)(), bytes)
+
+
+def test_rope_workspace_queries_and_reserve_arguments():
+    lib = _lib.lib()
+    pages = Pages(None, None, None, None, 64, 8, 128, _lib.DTYPE_Q8A)
+    out = C.c_size_t(123)
+    rc, msg = _status(lib.lnskv_rope_decode_workspace_size, C.byref(pages), None, 4, 32, 100, 0, C.byref(out))
+    assert rc == _lib.ERR_INVALID and "rope" in msg and out.value == 0
+    rope = _lib.Rope(C.c_void_p(256), 128)
+    assert lib.lnskv_rope_append_workspace_size(C.byref(pages), C.byref(rope), 10, C.byref(out)) == 0
+    assert out.value == 10 * 8 * 128 * 4          # the rotated K rows
+    odd = _lib.Rope(C.c_void_p(256), 127)
+    rc, msg = _status(lib.lnskv_rope_append_workspace_size, C.byref(pages), C.byref(odd), 10, C.byref(out))
+    assert rc == _lib.ERR_INVALID and "rotary_dim" in msg

@@ -58,7 +58,8 @@ def test_append_bit_exact(gpu, dtype, d):
 @pytest.mark.parametrize("part", range(8))
 def test_f16_append_exhaustive_all_f32_patterns(gpu, part):
     """Every f32 bit pattern (in 8 parts of 2^29) through the GPU append;
-    non-NaN inputs must give the oracle's RNE bits, NaN inputs a binary16 NaN."""
+    every one must give the oracle's bits (RNE for numbers; for NaNs the quiet
+    NaN with the input's sign and top 10 payload bits)."""
     n_kv, d = 8, 128
     chunk = 1 << 26
     tok = chunk // (n_kv * d)
@@ -77,11 +78,7 @@ def test_f16_append_exhaustive_all_f32_patterns(gpu, part):
         pk.append(x, x, tok_seq, tok_pos, tables)
         got = pk.k.view(torch.int16).reshape(-1).cpu().numpy().view(np.uint16)
         exp = O.f16_of_patterns(lo, chunk)
-        pat = np.arange(lo, lo + chunk, dtype=np.uint64).astype(np.uint32)
-        nan_in = ((pat & 0x7F800000) == 0x7F800000) & ((pat & 0x7FFFFF) != 0)
-        assert np.array_equal(got[~nan_in], exp[~nan_in]), f"chunk {c}"
-        g = got[nan_in]
-        assert (((g & 0x7C00) == 0x7C00) & ((g & 0x3FF) != 0)).all(), f"chunk {c} NaN"
+        assert np.array_equal(got, exp), f"chunk {c}"
 
 
 @pytest.mark.parametrize("d", [64, 128, 256])

@@ -261,17 +261,18 @@ def _sk_lens(n, seed):
     return tuple(int(x) for x in lens[:n])
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_Q8A])
 @pytest.mark.parametrize("rep", [1, 2, 4, 8])
-def test_stream_k_schedule(gpu, rep):
+def test_stream_k_schedule(gpu, rep, dtype):
     """split_tokens = 0 on the MFMA path runs the stream-K schedule (every
     wave an equal share of all pages; pieces merged by combine_sk_kernel).
-    64 sequences (its limit) with empty, short and long lengths, windows,
+    64 sequences (one group) with empty, short and long lengths, windows,
     a missing page; unfused and fused, against the f64 oracle and against
-    the split-K schedule."""
-    say("stream-K rep", rep)
+    the split-K schedule; f16 and Q8A pages (pages and scales bit-exact)."""
+    say("stream-K rep", rep, DTYPE_NAMES[dtype])
     n_kv, d = 8, 128
     lens = _sk_lens(64, seed=rep)
-    pk, tables, kv_len, q = _case(gpu, DTYPE_F16, d, rep, n_kv, lens, seed=90 + rep)
+    pk, tables, kv_len, q = _case(gpu, dtype, d, rep, n_kv, lens, seed=90 + rep)
     tables[5, 0] = NO_PAGE  # a missing page: its tokens are skipped
     rng = np.random.default_rng(rep + 7)
     p_start = np.zeros(len(lens), np.int32)
@@ -285,7 +286,7 @@ def test_stream_k_schedule(gpu, rep):
                         split=split)
         sync()
         err = rel_err(out, ref)
-        assert err.max() < TOL[DTYPE_F16], (split, err.max())
+        assert err.max() < TOL[dtype], (split, err.max())
         assert np.all(out.cpu().numpy()[0] == 0.0)  # empty sequence
     # fused: every sequence gains one token
     kv1 = np.minimum(kv_len + 1, (tables.shape[1]) * 16).astype(np.int32)
@@ -299,7 +300,10 @@ def test_stream_k_schedule(gpu, rep):
     sync()
     got, _ = host_pages(pk)
     assert np.array_equal(got.k, hp.k) and np.array_equal(got.v, hp.v)
-    assert rel_err(out1, ref1).max() < TOL[DTYPE_F16]
+    if dtype == DTYPE_Q8A:
+        assert np.array_equal(got.ks.view(np.uint32), hp.ks.view(np.uint32))
+        assert np.array_equal(got.vs.view(np.uint32), hp.vs.view(np.uint32))
+    assert rel_err(out1, ref1).max() < TOL[dtype]
 
 
 def test_stream_k_caller_workspace_and_fallback(gpu):
@@ -334,19 +338,22 @@ def test_stream_k_caller_workspace_and_fallback(gpu):
     assert e.value.status == ERR_WORKSPACE
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_Q8A])
 @pytest.mark.parametrize("n_seq", [130, 4096])
-def test_stream_k_many_sequences(gpu, n_seq):
+def test_stream_k_many_sequences(gpu, n_seq, dtype):
     """More than 64 sequences on the stream-K schedule (groups of 64, one
     lane per sequence): a whole group of empty sequences, ragged lengths and
-    windows, unfused and fused, against the f64 oracle."""
-    say("stream-K n_seq", n_seq)
+    windows, unfused and fused, against the f64 oracle; f16 and Q8A pages
+    (the Q8A fused call quantizes each new token in the wave that holds it;
+    pages and scales bit-exact)."""
+    say("stream-K n_seq", n_seq, DTYPE_NAMES[dtype])
     n_kv, d, rep = 8, 128, 4
     rng = np.random.default_rng(n_seq)
     hi = 700 if n_seq < 1000 else 48
     lens = [int(x) for x in rng.integers(0, hi, n_seq)]
     lens[64:128] = [0] * 64  # group 1 holds no units
     lens[0], lens[-1] = hi, 1
-    pk, tables, kv_len, q = _case(gpu, DTYPE_F16, d, rep, n_kv, tuple(lens), seed=n_seq)
+    pk, tables, kv_len, q = _case(gpu, dtype, d, rep, n_kv, tuple(lens), seed=n_seq)
     p_start = np.minimum(rng.integers(0, 40, n_seq), kv_len).astype(np.int32)
     hp, _ = host_pages(pk)
     scale = 1.0 / np.sqrt(d)
@@ -354,7 +361,7 @@ def test_stream_k_many_sequences(gpu, n_seq):
     out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
                     max_kv_len=int(kv_len.max()), scale=float(scale), p_start=dev_i32(p_start, gpu), split=0)
     sync()
-    assert rel_err(out, ref).max() < TOL[DTYPE_F16]
+    assert rel_err(out, ref).max() < TOL[dtype]
     assert np.all(out.cpu().numpy()[64:128] == 0.0)
     kv1 = np.minimum(kv_len + 1, tables.shape[1] * 16).astype(np.int32)
     k_new = rng.standard_normal((n_seq, n_kv, d)).astype(np.float32)
@@ -367,14 +374,17 @@ def test_stream_k_many_sequences(gpu, n_seq):
     sync()
     got, _ = host_pages(pk)
     assert np.array_equal(got.k, hp.k) and np.array_equal(got.v, hp.v)
-    assert rel_err(out1, ref1).max() < TOL[DTYPE_F16]
+    if dtype == DTYPE_Q8A:
+        assert np.array_equal(got.ks.view(np.uint32), hp.ks.view(np.uint32))
+        assert np.array_equal(got.vs.view(np.uint32), hp.vs.view(np.uint32))
+    assert rel_err(out1, ref1).max() < TOL[dtype]
 
 
 @pytest.mark.parametrize("force_valu", ["0", "1"])
 def test_q8a_d128_both_kernels(gpu, monkeypatch, force_valu):
     """Q8A pages with head_dim 128 run the MFMA stream-K kernel (int8 codes
-    turned into f16 exactly, K and V scales applied per token; the fused call
-    quantizes the new token with the append kernel first); LNSKV_FORCE_VALU=1
+    turned into f16 exactly, K and V scales applied per token; in the fused
+    call the wave that holds the new token quantizes and stores it); LNSKV_FORCE_VALU=1
     the generic kernel.  Both against the f64 oracle (1e-5), rep 1/2/4/8, with
     windows, an empty window and a missing page; pages and scales bit-exact."""
     monkeypatch.setenv("LNSKV_FORCE_VALU", force_valu)
@@ -407,3 +417,39 @@ def test_q8a_d128_both_kernels(gpu, monkeypatch, force_valu):
         assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8))
         assert np.array_equal(got.ks, hp.ks) and np.array_equal(got.vs, hp.vs)
         assert rel_err(out1, ref1).max() < TOL[DTYPE_Q8A], rep
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_Q8A])
+def test_out_of_range_kv_len_stores_nothing(gpu, dtype):
+    # kv_len past max_kv_len, or past 16 * bt_stride: the row is out of range.
+    # The fused call stores nothing for it (no existing token is overwritten)
+    # and its output row is zero; the other rows are unaffected.
+    say("out-of-range kv_len", DTYPE_NAMES[dtype])
+    d, rep, n_kv = 128, 4, 2
+    lens = (300, 200, 500, 64)
+    pk, tables, kv_len, q = _case(gpu, dtype, d, rep, n_kv, lens, seed=21)
+    stride = tables.shape[1]
+    kv = kv_len.copy()
+    kv[1] = 301                  # > max_kv_len (300): out of range
+    kv[3] = 16 * stride + 5      # past the table row: out of range
+    kv[2] = 300                  # in range
+    rng = np.random.default_rng(2)
+    k_new = rng.standard_normal((len(lens), n_kv, d)).astype(np.float32)
+    v_new = rng.standard_normal((len(lens), n_kv, d)).astype(np.float32)
+    hp, _ = host_pages(pk)
+    in_range = np.array([True, False, True, False])
+    O.append(hp, k_new[in_range], v_new[in_range], np.arange(2, dtype=np.int32), kv[in_range] - 1,
+             tables[in_range])
+    ref = O.decode_f64(hp, q[in_range], tables[in_range], kv[in_range], None, 0.1)
+    for split in (0, 64):
+        out = pk.append_decode(dev_f32(q, gpu), dev_f32(k_new, gpu), dev_f32(v_new, gpu), dev_i32(tables, gpu),
+                               dev_i32(kv, gpu), n_heads=n_kv * rep, max_kv_len=300, scale=0.1, split=split)
+        sync()
+        o = out.cpu().numpy()
+        assert (o[1] == 0).all() and (o[3] == 0).all()
+        assert rel_err(o[in_range], ref).max() < TOL[dtype]
+        # every page byte equals the oracle's after the in-range appends
+        hp_now, _ = host_pages(pk)
+        assert np.array_equal(hp_now.k, hp.k) and np.array_equal(hp_now.v, hp.v), split
+        if hp.ks is not None:
+            assert np.array_equal(hp_now.ks, hp.ks) and np.array_equal(hp_now.vs, hp.vs)

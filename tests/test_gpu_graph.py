@@ -35,3 +35,42 @@ def test_graph_replay_matches_eager(gpu, name):
             assert torch.equal(got, eager[layer]), (name, rep, layer)
             assert torch.equal(r.layers[layer].k, pages[layer][0])
             assert torch.equal(r.layers[layer].v, pages[layer][1])
+
+
+def test_library_workspace_under_capture(gpu):
+    """A call with a NULL workspace whose library buffer is too small does not
+    allocate while its stream is being captured: it fails with
+    LNSKV_ERR_WORKSPACE before enqueuing anything.  After
+    lnskv_workspace_reserve the same capture succeeds and every replay
+    matches the eager call."""
+    from lnskv._lib import ERR_WORKSPACE, LnskvError, check, lib
+
+    say("library workspace under capture")
+    w = make("c2", n_seq=6, lo=40, hi=1500, num_pages=1024)
+    r = StepRunner(w, gpu, n_layers=1, seed=5)
+    pk = r.layers[0]
+    kw = dict(n_heads=w.n_heads, max_kv_len=r.max_kv_len, scale=w.scale)
+    torch.cuda.synchronize()
+    check(lib().lnskv_workspace_release())
+    need = pk.workspace_size(r.n_dec, w.n_heads, r.max_kv_len, 0)
+    assert need > 0
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(LnskvError) as e:
+        with torch.cuda.graph(g):
+            pk.decode(r.q, r.dec_tables, r.dec_kv_len, out=r.out, **kw)
+    assert e.value.status == ERR_WORKSPACE and "lnskv_workspace_reserve" in e.value.message
+    torch.cuda.synchronize()
+    check(lib().lnskv_workspace_reserve(need, 0, 0))
+    eager = pk.decode(r.q, r.dec_tables, r.dec_kv_len, **kw).clone()
+    torch.cuda.synchronize()
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        pk.decode(r.q, r.dec_tables, r.dec_kv_len, out=r.out, **kw)
+    for _ in range(3):
+        r.out.zero_()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(r.out, eager)
+    del g, g2
+    torch.cuda.synchronize()
+    check(lib().lnskv_workspace_release())

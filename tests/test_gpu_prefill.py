@@ -19,8 +19,9 @@ from lnskv.device import PagedKV, sync
 pytestmark = pytest.mark.gpu
 
 
-def _run(gpu, rep, chunks, ctx_pages, p_start=None, missing=(), n_kv=2, seed=0, extra_rows=0):
-    """chunks: list of (table row, first position, length); tokens laid out in list order."""
+def _run(gpu, rep, chunks, ctx_pages, p_start=None, missing=(), n_kv=2, seed=0, extra_rows=0, window=0):
+    """chunks: list of (table row, first position, length); tokens laid out in list order.
+    window > 0: every token's reference start is max(p_start, kv_p_start(pos, window))."""
     d = 128
     rng = np.random.default_rng(seed)
     n_rows = len(ctx_pages)
@@ -47,7 +48,8 @@ def _run(gpu, rep, chunks, ctx_pages, p_start=None, missing=(), n_kv=2, seed=0, 
     ps = None if p_start is None else np.array(p_start, np.int32)
     out = torch.full((n_tok, n_heads, d), 7.0, device=gpu)
     pk.prefill_attention(dev_f32(q, gpu), torch.tensor(desc, dtype=torch.int32, device=gpu), dev_i32(tables, gpu),
-                         n_heads=n_heads, scale=scale, p_start=None if ps is None else dev_i32(ps, gpu), out=out)
+                         n_heads=n_heads, scale=scale, p_start=None if ps is None else dev_i32(ps, gpu),
+                         window=window, out=out)
     sync()
     hp, _ = host_pages(pk)
     rows, kvl, pst, idx = [], [], [], []
@@ -57,7 +59,10 @@ def _run(gpu, rep, chunks, ctx_pages, p_start=None, missing=(), n_kv=2, seed=0, 
         for i in range(ln):
             rows.append(tables[row])
             kvl.append(pos0 + i + 1)
-            pst.append(0 if ps is None else ps[row])
+            p0 = 0 if ps is None else int(ps[row])
+            if window > 0:
+                p0 = max(p0, max(0, pos0 + i - window + 1))  # kv_p_start(pos, window), engine.rs:3007-3013
+            pst.append(p0)
             idx.append(t0 + i)
     idx = np.array(idx)
     ref = O.decode_f64(hp, q[idx], np.array(rows, np.uint32), np.array(kvl, np.int32), np.array(pst, np.int32),
@@ -102,3 +107,20 @@ def test_prefill_many_chunks(gpu):
     chunks[33] = (n_rows + 3, 0, 8)
     for rep in (4, 8):
         _run(gpu, rep, chunks, ctx_pages, seed=20 + rep)
+
+
+@pytest.mark.parametrize("rep", [2, 4, 8])
+def test_prefill_sliding_window(gpu, rep):
+    """A sliding-window layer: each prompt token attends its own window
+    [pos - w + 1, pos] (the reference's per-token kv_p_start), checked token by
+    token against the oracle.  Chunks that cross the window (longer than it,
+    starting before and after it fills), windows of 1 and 16 tokens, unaligned
+    windows, a row start past some tokens' windows, and a missing page."""
+    chunks = [(0, 0, 200),     # starts empty and runs past a 100-token window
+              (1, 700, 130),   # long context: every tile's first pages leave the window
+              (2, 37, 64),     # window larger than the context at first
+              (3, 500, 40)]    # row p_start 520 inside the chunk: early tokens have empty windows
+    ctx_pages = [13, 53, 7, 35]
+    for w in (100, 1, 16, 33):
+        _run(gpu, rep, chunks, ctx_pages, p_start=[0, 0, 0, 520], missing=[(1, 44)], seed=30 + rep + w,
+             window=w)

@@ -59,8 +59,13 @@ def _check_pages(got, exp, before, dtype):
         assert np.array_equal(g[~touched].view(np.uint8), e[~touched].view(np.uint8)), which
         assert _ulp_close(g[touched], e[touched], dtype), which
     if dtype == DTYPE_Q8A:
-        np.testing.assert_allclose(got.ks, exp.ks, rtol=1e-5)
-        np.testing.assert_allclose(got.vs, exp.vs, rtol=1e-5)
+        # V is stored unrotated: its scales are bit-exact.  K's scale is
+        # amax/127 of the rotated row, whose largest element carries the
+        # rotation's error bound (one ulp plus 4e-6 of the row's largest
+        # value, as the rows above): the scale within the same bound.
+        assert np.array_equal(got.vs.view(np.uint32), exp.vs.view(np.uint32))
+        e64 = exp.ks.astype(np.float64)
+        assert np.all(np.abs(got.ks.astype(np.float64) - e64) <= np.spacing(np.abs(exp.ks)) + 4e-6 * np.abs(e64))
 
 
 CASES = [  # dtype, head_dim, rep, rotary_dim, split, force_valu
@@ -109,7 +114,11 @@ def test_rope_append_decode(gpu, monkeypatch, dtype, d, rep, rd, split, valu):
     # stored values: compare against the oracle over the GPU's pages too
     ref_gpu_pages = O.decode_f64(got, q_r, tables, lens, None, scale)
     assert rel_err(out, ref_gpu_pages).max() < TOL[dtype]
-    assert rel_err(out, ref).max() < max(TOL[dtype], 2e-3)
+    # against the oracle's own pages: f32 pages within the f32 bound; f16 and
+    # Q8A pages may hold a value one f16 ulp or one int8 code away from the
+    # oracle's (the rotation's rounding), which moves the output by up to that
+    # much on its own
+    assert rel_err(out, ref).max() < (TOL[dtype] if dtype == DTYPE_F32 else 2e-3)
 
 
 APPEND_CASES = [  # dtype, head_dim, rotary_dim

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lnskv import NO_PAGE, BlockTables, LnskvError, PagePool, kv_p_start
+from lnskv import NO_PAGE, BlockTables, LnskvError, PagePool, kv_p_start, window_pages
 from lnskv import _lib
 
 
@@ -119,6 +119,50 @@ def test_swa_pool_sized_to_window_exhausts_at_pos_w():
         bt2.evict_kv_pages(pool2, 0, pos, w)
         live = bt2.array()[0]
         assert (live != NO_PAGE).sum() <= w // 16 + 1
+
+
+@pytest.mark.parametrize("w", [1, 2, 15, 16, 17, 31, 32, 33, 64, 100, 4096])
+def test_step_pages_never_exhausts_a_window_sized_pool(w):
+    # lnskv_step_pages (evict, then ensure) on a pool of window_pages(w) pages
+    # runs 10k positions without exhausting it; at every position every page
+    # the window [kv_p_start, pos] touches is mapped and no page outside it is
+    # held.  The bound is tight: some position holds exactly window_pages(w)
+    # pages, and a pool one page smaller runs dry.
+    n_pos = 10_000
+    need = window_pages(w)
+    assert need == (w + 14) // 16 + 1
+    pool, bt = PagePool(need), BlockTables(1, n_pos // 16 + 1)
+    most = 0
+    for pos in range(n_pos):
+        bt.step_pages(pool, 0, pos, w)
+        row = bt.array()[0]
+        lo, hi = kv_p_start(pos, w) // 16, pos // 16
+        live = np.nonzero(row != NO_PAGE)[0]
+        assert live.min() == lo and live.max() == hi and len(live) == hi - lo + 1, (w, pos)
+        most = max(most, len(live))
+        assert pool.num_free == need - len(live)
+    assert most == need
+    small, bt_small = PagePool(need - 1), BlockTables(1, n_pos // 16 + 1)
+    with pytest.raises(LnskvError) as e:
+        for pos in range(n_pos):
+            bt_small.step_pages(small, 0, pos, w, layer=3)
+    assert e.value.status == _lib.ERR_POOL_EXHAUSTED and "at layer 3" in e.value.message
+
+
+def test_step_pages_matches_evict_then_ensure_of_the_oracle():
+    lib = O.lib()
+    for window in (0, 20, 48):
+        a_pool, a_bt = PagePool(48), BlockTables(1, 64)
+        b_pool = lib.orc_pool_new(48)
+        b_row = np.full(64, NO_PAGE, np.uint32)
+        b_len = C.c_int(0)
+        for pos in range(700):
+            a_bt.step_pages(a_pool, 0, pos, window)
+            lib.orc_evict_kv_pages(b_pool, b_row.ctypes.data, b_len.value, pos, window)
+            assert lib.orc_ensure_kv_page(b_pool, b_row.ctypes.data, C.byref(b_len), 64, pos) == 0
+            assert np.array_equal(a_bt.array()[0], b_row), (window, pos)
+        lib.orc_pool_delete(b_pool)
+    assert window_pages(0) == 0 and window_pages(-5) == 0
 
 
 def test_table_overflow_is_an_error_not_a_write():
