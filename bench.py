@@ -63,6 +63,9 @@ def parse():
                    help="launches of the o_proj Q4L GEMV-accumulate at the config's shape (0 = skip)")
     p.add_argument("--prefill-reps", type=int, default=20,
                    help="launches of chunked-prefill attention over the config's pages (0 = skip)")
+    p.add_argument("--extras", type=int, default=1,
+                   help="c2 only: also measure c1/c3/c4/c5, c2 on Q8A pages, the reference's one-sequence call and "
+                        "the block-table upload (0 = skip)")
     p.add_argument("--copy-only", action="store_true",
                    help="run only the plain copy (the calibration kernel for HBM byte counters)")
     return p.parse_args()
@@ -94,8 +97,10 @@ def pattern_ceiling(w, runner, dev, reps: int) -> dict | None:
     events: lnskv_read_units over the same (page, kv head) units as the
     decode, in its order ((sequence, kv head, page)) and its stream-K wave
     split (CUs x 4 waves), cycling the same layers' pools (no cache reuse
-    between launches).  Bytes per launch: units x 2 pools x 16 rows x 256 B.
-    None for shapes the probe does not read (kv-head rows other than 256 B)."""
+    between launches).  Bytes per launch: units x 2 pools x 16 rows x 256 B
+    (f16 d128 / f32 d64), or x (128 B + a 4-byte scale) for Q8A d128 pages,
+    whose decode runs 8 waves per CU.  None for shapes the probe does not
+    read."""
     import ctypes as C
 
     import numpy as np
@@ -103,7 +108,9 @@ def pattern_ceiling(w, runner, dev, reps: int) -> dict | None:
 
     from lnskv._lib import check, lib
 
-    if reps <= 0 or runner.n_dec == 0 or w.head_dim * {0: 4, 1: 2, 2: 1}[w.dtype] != 256:
+    row_bytes = w.head_dim * {0: 4, 1: 2, 2: 1}[w.dtype]
+    q8 = w.dtype == 2
+    if reps <= 0 or runner.n_dec == 0 or not (row_bytes == 256 and not q8 or row_bytes == 128 and q8):
         return None
     pages, kvhs = [], []
     for s in runner.dec_rows:
@@ -115,7 +122,7 @@ def pattern_ceiling(w, runner, dev, reps: int) -> dict | None:
     unit_page = np.concatenate(pages)
     unit_kvh = np.concatenate(kvhs)
     n_units = len(unit_page)
-    waves = torch.cuda.get_device_properties(dev).multi_processor_count * 4
+    waves = torch.cuda.get_device_properties(dev).multi_processor_count * (8 if q8 else 4)
     chunk = max(4, -(-n_units // waves))
     start = np.minimum(np.arange(waves + 1, dtype=np.int64) * chunk, n_units).astype(np.int32)
     d_page = torch.from_numpy(unit_page.view(np.int32)).to(dev)
@@ -139,7 +146,7 @@ def pattern_ceiling(w, runner, dev, reps: int) -> dict | None:
     e.record(stream)
     torch.cuda.synchronize()
     dt = s.elapsed_time(e) / 1e3 / reps
-    nbytes = n_units * 2 * 16 * 256
+    nbytes = n_units * 2 * 16 * (row_bytes + (4 if q8 else 0))
     return {"bytes_per_launch": int(nbytes), "us_per_launch": round(dt * 1e6, 2),
             "gb_per_s": round(nbytes / dt / 1e9, 1), "waves": int(waves), "units": int(n_units)}
 
@@ -277,6 +284,184 @@ def prefill_measure(w, runner, dev, reps: int, chunk: int = 256) -> dict | None:
     return res
 
 
+def step_distribution(step, stream, n: int) -> dict:
+    """Per-step HIP-event durations of n more steps (an event pair around
+    each step, on the kernels' stream): median and spread, in µs."""
+    import numpy as np
+    import torch
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        step(i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    t = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
+    return {"steps": n, "median": round(float(np.median(t)), 2), "p10": round(float(np.percentile(t, 10)), 2),
+            "p90": round(float(np.percentile(t, 90)), 2), "min": round(float(t.min()), 2)}
+
+
+def timed_steps(step, stream, steps: int, warmup: int) -> tuple[float, float]:
+    """(event mean, wall mean) seconds per step over exactly `steps` steps
+    after `warmup`, one event pair around all of them."""
+    import torch
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(steps):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps, (time.perf_counter() - t0) / steps
+
+
+def config_measure(name: str, dev, steps: int, layers: int = 2, kv_dtype: int | None = None,
+                   pattern_reps: int = 0) -> dict:
+    """One configuration's step (its own workload and pools, `layers` of them
+    cycled): event mean over `steps` steps, median of per-step events,
+    algorithmic GB/s and fraction of 8 TB/s; optionally the load ceiling of
+    its page pattern.  c5 adds the full-copy fork variant."""
+    import torch
+
+    from lnskv.configs import make
+    from lnskv.step import StepRunner
+
+    w = make(name) if kv_dtype is None else make(name, dtype=kv_dtype)
+    runner = StepRunner(w, dev, n_layers=layers, seed=1)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    step = lambda i: runner.run(i % layers)  # noqa: E731
+    ev, wall = timed_steps(step, stream, steps, 10)
+    dist = step_distribution(step, stream, min(steps, 200))
+    nb = w.algorithmic_bytes()["total"]
+    res = {"us_per_step_events": round(ev * 1e6, 2), "us_per_step_wall": round(wall * 1e6, 2),
+           "us_per_step_median": dist["median"], "algorithmic_bytes": int(nb),
+           "gb_per_s": round(nb / ev / 1e9, 1), "frac_of_hbm_peak": round(nb / ev / 1e9 / HBM_PEAK_GBS, 4)}
+    if pattern_reps > 0:
+        pc = pattern_ceiling(w, runner, dev, pattern_reps)
+        if pc:
+            res["pattern_ceiling_us"] = pc["us_per_launch"]
+            res["frac_of_pattern_ceiling"] = round(pc["us_per_launch"] / (ev * 1e6), 4)
+    if name == "c5" and w.info.get("parents"):
+        res["full_copy_fork"] = full_copy_fork(w, runner, dev)
+    del runner
+    torch.cuda.empty_cache()
+    return res
+
+
+def full_copy_fork(w, runner, dev, reps: int = 20) -> dict:
+    """c5's fork with every page of the 8 children copied (no sharing): one
+    lnskv_page_copy of all their pages, K and V, read and written."""
+    import numpy as np
+    import torch
+
+    n_seq = w.n_seq - len(w.info["parents"])
+    src_pages = []
+    for i, parent in enumerate(w.info["parents"]):
+        npg = (int(w.ctx_len[n_seq + i]) + 15) // 16
+        src_pages += [int(p) for p in w.tables[parent][:npg] if p != 0xFFFFFFFF]
+    # destinations: other pages of the pool (this runner is not stepped again)
+    dst_pages = np.setdiff1d(np.arange(w.num_pages), np.array(src_pages))[:len(src_pages)]
+    src_pages = src_pages[:len(dst_pages)]
+    src = torch.tensor(np.array(src_pages, np.uint32).view(np.int32), device=dev)
+    dst = torch.tensor(dst_pages.astype(np.uint32).view(np.int32), device=dev)
+    pk = runner.layers[0]
+    pk.page_copy(src, dst)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        pk.page_copy(src, dst)
+    b.record()
+    torch.cuda.synchronize()
+    dt = a.elapsed_time(b) / 1e3 / reps
+    nbytes = len(src_pages) * 2 * 2 * 16 * w.n_kv * w.head_dim * w.elem_bytes
+    return {"pages": len(src_pages), "bytes": int(nbytes), "us": round(dt * 1e6, 1),
+            "gb_per_s": round(nbytes / dt / 1e9, 1),
+            "note": "every page of the 8 forked children copied (the page-sharing fork copies only tail pages)"}
+
+
+def reference_call_measure(dev, calls: int = 400, n_layers: int = 32) -> dict:
+    """The reference's own call: lnskv_attention_paged (encode_attention_paged_q8a's
+    arguments) for ONE sequence, Hq32/Hkv8/d128 on Q8A pages, appending the
+    token at pos 4095 and attending [0, 4095]: 256 pages x 8 kv heads.  A
+    32-layer model's worth of pools is cycled (8.6 MB per call, 276 MB over
+    the layers, more than the 256 MB last-level cache).  Wall time per call is
+    the host launch loop's rate (asynchronous calls back to back); event time
+    per call is the GPU's."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    from lnskv import DTYPE_Q8A
+    from lnskv.device import PagedKV
+
+    pos, hq, hkv, d = 4095, 32, 8, 128
+    npg = pos // 16 + 1
+    layers = []
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    for _ in range(n_layers):
+        pk = PagedKV(npg + 8, hkv, d, DTYPE_Q8A, dev)
+        for t in (pk.k, pk.v):
+            t.copy_(torch.randint(-127, 128, t.shape, generator=g, device=dev, dtype=torch.int8))
+        for t in (pk.ks, pk.vs):
+            t.copy_(torch.rand(t.shape, generator=g, device=dev) * 0.02 + 0.001)
+        layers.append(pk)
+    table = torch.from_numpy(np.random.default_rng(1).permutation(npg + 8)[:npg].astype(np.int32)).to(dev)
+    q = torch.randn(hq * d, device=dev)
+    k_in = torch.randn(hkv * d, device=dev)
+    v_in = torch.randn(hkv * d, device=dev)
+    out = torch.empty(hq * d, device=dev)
+    call = lambda i: layers[i % n_layers].attention_paged(q, k_in, v_in, table, pos, hq, out=out)  # noqa: E731
+    stream = torch.cuda.current_stream(dev)
+    ev, wall = timed_steps(call, stream, calls, 2 * n_layers)
+    dist = step_distribution(call, stream, 200)
+    nbytes = (pos + 1) * 2 * hkv * (d + 4) + 2 * hkv * d * 4 + 2 * hq * d * 4 + npg * 4
+    del layers
+    torch.cuda.empty_cache()
+    return {"shape": "1 sequence, Hq32/Hkv8/d128, Q8A pages, pos 4095 (append + attend 4096 tokens)",
+            "us_per_call_events": round(ev * 1e6, 2), "us_per_call_median": dist["median"],
+            "us_per_call_wall": round(wall * 1e6, 2), "bytes_per_call": int(nbytes),
+            "gb_per_s": round(nbytes / ev / 1e9, 1), "layers_cycled": n_layers}
+
+
+def table_upload_measure(w, dev, reps: int = 200) -> dict:
+    """upload_block_table's replacement timed on its own: lnskv_block_tables_upload
+    of the configuration's [n_seq][stride] table from host memory (the
+    library's C++ tables) to the device, HIP events around `reps` uploads."""
+    import torch
+
+    from lnskv.host import BlockTables, PagePool
+
+    bt = BlockTables(w.n_seq, w.tables.shape[1])
+    pool = PagePool(w.num_pages)
+    for s in range(w.n_seq):
+        for lp in range(int((w.tables[s] != 0xFFFFFFFF).sum())):
+            bt.ensure_kv_page(pool, s, lp * 16)
+    dst = torch.empty(w.n_seq * w.tables.shape[1], dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    bt.upload(dst.data_ptr(), stream.cuda_stream)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record(stream)
+    for _ in range(reps):
+        bt.upload(dst.data_ptr(), stream.cuda_stream)
+    b.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / reps
+    return {"bytes": int(dst.numel() * 4), "us_per_upload_events": round(a.elapsed_time(b) * 1e3 / reps, 2),
+            "us_per_upload_wall": round(wall * 1e6, 2),
+            "note": "hipMemcpyAsync from pageable host memory; the step's kernels are not in the timed region"}
+
+
 def measured_traffic(name: str):
     """HBM bytes per step from the committed counter summary, or None."""
     path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
@@ -377,23 +562,12 @@ def main():
         step = lambda i: graphs[i % args.layers].replay()  # noqa: E731  (slower than eager on ROCm 7: measured)
     else:
         step = lambda i: runner.run(i % args.layers)  # noqa: E731
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
     # timed region: exactly K steps, synchronized on both sides; one pair of
     # HIP events on the kernels' stream brackets the K steps (an event pair
-    # per step would add its own gaps between the steps)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record(stream)
-    for i in range(args.steps):
-        step(i)
-    end.record(stream)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / args.steps
-    ev_mean = start.elapsed_time(end) / 1e3 / args.steps
+    # per step would add its own gaps between the steps); the per-step
+    # distribution comes from a second run of steps with an event pair each
+    ev_mean, wall = timed_steps(step, stream, args.steps, args.warmup)
+    dist = step_distribution(step, stream, max(100, min(args.steps, 400)))
 
     gbs_wall = nb["total"] / wall / 1e9
     gbs_ev = nb["total"] / ev_mean / 1e9
@@ -401,6 +575,14 @@ def main():
     pattern = pattern_ceiling(w, runner, dev, args.pattern_reps)
     oproj = oproj_measure(w, runner, dev, args.oproj_reps)
     prefill = prefill_measure(w, runner, dev, args.prefill_reps)
+    extras = None
+    if args.extras and w.name == "c2" and args.kv_dtype == "config" and not args.rope:
+        extras = {"c2_q8a_pages": config_measure("c2", dev, args.steps, layers=args.layers, kv_dtype=2,
+                                                 pattern_reps=args.pattern_reps),
+                  "reference_call_b1_q8a": reference_call_measure(dev),
+                  "block_table_upload": table_upload_measure(w, dev)}
+        for name in ("c1", "c3", "c4", "c5"):
+            extras[name] = config_measure(name, dev, min(args.steps, 100))
     cpu = None
     if args.cpu_seconds > 0:
         threads = args.cpu_threads or len(os.sched_getaffinity(0))
@@ -417,6 +599,8 @@ def main():
         "ms_per_step": round(wall * 1e3, 5),
         "us_per_step": round(wall * 1e6, 2),
         "us_per_step_events": round(ev_mean * 1e6, 2),
+        "us_per_step_median": dist["median"],
+        "step_event_distribution_us": dist,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -456,6 +640,7 @@ def main():
             "frac_of_pattern_ceiling": round(gbs_ev / pattern["gb_per_s"], 4) if pattern else None,
         },
         "cpu_baseline": cpu,
+        "more_measurements": extras,
         "after_the_path": {"o_proj_q4l_gemv_accumulate": oproj},
         "prefill": {"chunked_prefill_attention": prefill},
     }

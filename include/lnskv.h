@@ -467,17 +467,20 @@ int lnskv_block_tables_upload(const lnskv_block_tables* t, uint32_t* dst_dev,
  * Measurement (no counterpart in the reference)
  * ---------------------------------------------------------------------------
  * lnskv_read_units: loads, with plain 16-byte loads and no arithmetic, the K
- * and V rows of units (unit_page[u], unit_kvh[u]) -- the 16 x 256 bytes one
- * kv head holds in one page, per pool -- wave w taking units
- * [wave_start[w], wave_start[w + 1]) with two units in flight.  Given the
- * units of a decode step in the decode's order and wave split, its duration
- * is the load ceiling of that step's page pattern.  Needs head_dim x dtype
- * bytes = 256; page ids >= num_pages and kv heads outside [0, n_kv_heads)
+ * and V rows of units (unit_page[u], unit_kvh[u]) -- the 16 rows one kv head
+ * holds in one page, per pool, and for Q8A pages their 16 K and 16 V scales --
+ * wave w taking units [wave_start[w], wave_start[w + 1]) with two units in
+ * flight.  Given the units of a decode step in the decode's order and wave
+ * split, its duration is the load ceiling of that step's page pattern.  Rows
+ * of 256 bytes (head_dim x dtype bytes: f16 d128, f32 d64) or Q8A rows of 128
+ * bytes (d128); page ids >= num_pages and kv heads outside [0, n_kv_heads)
  * read page 0 / kv head 0.  wave_start holds n_waves + 1 non-decreasing
  * indices into the unit lists.  sink[w * 64 + lane] receives the XOR of the
- * 32-bit words lane (r, c) = (lane / 16, lane % 16) loaded for wave w's
- * units, each unit once: 16-byte chunk c of rows r, r + 4, r + 8, r + 12 of
- * the unit's K and V rows. */
+ * 32-bit words lane loaded for wave w's units, each unit once: 256-byte rows,
+ * lane (r, c) = (lane / 16, lane % 16): 16-byte chunk c of rows r, r + 4,
+ * r + 8, r + 12 of K and V; Q8A, lane (r, c) = (lane / 8, lane % 8): chunk c
+ * of rows r and r + 8 of K and V, and the scale of token lane % 16 (V for
+ * lanes with bit 4 set, K otherwise). */
 int lnskv_read_units(const lnskv_pages* c, const uint32_t* unit_page, const int32_t* unit_kvh,
                      const int32_t* wave_start, int32_t n_waves, uint32_t* sink,
                      lnskv_stream_t stream);

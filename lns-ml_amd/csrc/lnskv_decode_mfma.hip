@@ -130,6 +130,10 @@ struct WaveState {
   float m;          // lanes with lane%16 < REP: running max of head lane%16
   float l;          // partial softmax sum over this lane's tokens
   float qexp;       // 2^E undoing the per-head normalisation of q
+  // Q8A pages: acc holds the P.V sums divided by vnorm, a power of two that
+  // follows the pages' largest V scale (0 until a page sets it); vinv = 1/vnorm
+  float vnorm;
+  float vinv;
 };
 
 // Multiplies the result rows 4g+ii of this lane by their head's alpha: row r
@@ -241,11 +245,11 @@ __device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& s
 
   // A operand of P.V: row n < REP: f16(p) of head n; REP <= n < 2REP: the
   // remainder of head n-REP; other rows zero.
-  // SC: the weights carry vs / vmax (vmax the page's largest V scale) so
-  // that their f16 lo parts stay normal numbers, and the page's products are
-  // multiplied by vmax in f32.  Masked tokens' scales (stale bytes) are left
-  // out of the max.
-  float vmax = 1.0f;
+  // SC: the weights carry vs / vnorm, vnorm the power of two at or just above
+  // the largest V scale seen (kept within 16x of each page's largest), so that
+  // their f16 lo parts stay normal numbers; acc accumulates in units of vnorm
+  // and is rescaled, exactly, only when a page's largest scale leaves
+  // [vnorm/16, vnorm].  Masked tokens' scales (stale bytes) are left out.
   if constexpr (SC) {
     if constexpr (!FULL) {
 #pragma unroll
@@ -254,11 +258,24 @@ __device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& s
         if (!(valid && t >= ta && t < tb)) vsc[ii] = 0.0f;
       }
     }
-    vmax = fmaxf(fmaxf(vsc[0], vsc[1]), fmaxf(vsc[2], vsc[3]));
-    vmax = max_xor16(max_xor32(vmax));  // over the page's 16 tokens
-    const float inv = vmax > 0.0f ? 1.0f / vmax : 0.0f;
+    float vmax = fmaxf(fmaxf(vsc[0], vsc[1]), fmaxf(vsc[2], vsc[3]));
+    vmax = max_xor16(max_xor32(vmax));  // over the page's 16 tokens; wave-uniform
+    if ((vmax > st.vnorm || vmax * 16.0f < st.vnorm) && vmax > 0.0f) {
+      int e = 0;
+      (void)frexpf(vmax, &e);
+      const float nn = ldexpf(1.0f, e);  // >= vmax, < 2 vmax
+      if (st.vnorm > 0.0f) {
+        const float r = st.vnorm * ldexpf(1.0f, -e);  // a power of two: exact
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) pr[ii] *= vsc[ii] * inv;
+        for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) st.acc[nb][q] *= r;
+      }
+      st.vnorm = nn;
+      st.vinv = ldexpf(1.0f, -e);
+    }
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) pr[ii] *= vsc[ii] * st.vinv;
   }
   half4 pa;
 #pragma unroll
@@ -288,14 +305,7 @@ __device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& s
                : "memory");
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb)
-    if constexpr (SC) {
-      const float4v t = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]),
-                                                             float4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) st.acc[nb][e] = fmaf(vmax, t[e], st.acc[nb][e]);
-    } else {
-      st.acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]), st.acc[nb], 0, 0, 0);
-    }
+    st.acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]), st.acc[nb], 0, 0, 0);
 }
 
 // Loads of one piece that do not depend on the sequence's length, issued
@@ -397,12 +407,15 @@ __device__ __forceinline__ void init_wave_state(const DecodeArgs& a, const Piece
     for (int nb = 0; nb < 8; ++nb) st.acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
     st.m = kMInit;
     st.l = 0.0f;
+    st.vnorm = 0.0f;
+    st.vinv = 0.0f;
   }
 }
 
 // The end of a piece: sums over the lanes, then the normalised output rows
 // or the partial rows the piece leaves for a merge.
-template <int REP>
+// SC (Q8A pages): acc is in units of st.vnorm.
+template <int REP, bool SC = false>
 __device__ __forceinline__ void finish_piece(const DecodeArgs& a, WaveState<REP>& st, int s, int kvh,
                                              const PieceOut& po, int g, int n) {
   // Denominators: sum this head's lanes over the four 16-lane rows.
@@ -443,13 +456,13 @@ __device__ __forceinline__ void finish_piece(const DecodeArgs& a, WaveState<REP>
       const float lh = lsel[ii], mh = msel[ii];
       if (po.final) {
         const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + hb + ii;
-        const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+        const float inv = lh > 0.0f ? (SC ? st.vnorm : 1.0f) / lh : 0.0f;
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) a.out[hrow * kD + 16 * nb + n] = gated(a, hrow * kD + 16 * nb + n, o[ii][nb] * inv);
       } else {
         const size_t pidx = po.pbase + (size_t)(hb + ii) * po.pstride;
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) a.ws_acc[pidx * kD + 16 * nb + n] = o[ii][nb];
+        for (int nb = 0; nb < 8; ++nb) a.ws_acc[pidx * kD + 16 * nb + n] = SC ? o[ii][nb] * st.vnorm : o[ii][nb];
         if (n == 0) {
           a.ws_ml[pidx * 2 + 0] = mh;
           a.ws_ml[pidx * 2 + 1] = lh;
@@ -898,7 +911,7 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
     if (i + d < npg) step(i + d, pbuf[d % DEPTH], vld[d % DEPTH], false);
   wait_vmcnt<0>();  // stand-in pages of a piece with fewer than DEPTH pages
   __builtin_amdgcn_wave_barrier();
-  finish_piece<REP>(a, st, s, kvh, po, g, n);
+  finish_piece<REP, true>(a, st, s, kvh, po, g, n);
 }
 
 // Split-K schedule: block (kv head, partition, sequence) attends one

@@ -1,7 +1,8 @@
 """GPU load probe (lnskv_read_units, measurement only): every lane's XOR word
 equals the host XOR of exactly the bytes the header says it loads -- each
 unit once, empty waves zero, odd and even unit counts, page ids and kv heads
-outside the pools reading page 0 / kv head 0."""
+outside the pools reading page 0 / kv head 0; 256-byte rows (f16 d128, f32
+d64) and Q8A rows (128 bytes plus the K and V scales)."""
 import ctypes as C
 
 import numpy as np
@@ -9,7 +10,7 @@ import pytest
 import torch
 
 from gpu_util import fill_pages, say
-from lnskv import DTYPE_F16, DTYPE_F32
+from lnskv import DTYPE_F16, DTYPE_F32, DTYPE_Q8A
 from lnskv._lib import check, lib
 from lnskv.device import PagedKV, _stream, sync
 
@@ -34,7 +35,28 @@ def _expected(k32, v32, pages, kvhs, start, num_pages, n_kv):
     return out.reshape(-1)
 
 
-@pytest.mark.parametrize("dtype,d", [(DTYPE_F16, 128), (DTYPE_F32, 64)])
+def _expected_q8(k32, v32, ks, vs, pages, kvhs, start, num_pages, n_kv):
+    """Q8A rows (128 bytes): sink[w*64 + 8r + c] XORs, over the wave's units,
+    chunk c of rows r and r + 8 of K and V, plus one scale word: the V scale
+    of token lane % 16 for lanes with bit 4 set, the K scale otherwise."""
+    n_waves = len(start) - 1
+    out = np.zeros((n_waves, 64), np.uint32)
+    lane = np.arange(64)
+    for w in range(n_waves):
+        acc = np.zeros(64, np.uint32)
+        for u in range(start[w], start[w + 1]):
+            p = int(pages[u]) if pages[u] < num_pages else 0
+            h = int(kvhs[u]) if 0 <= kvhs[u] < n_kv else 0
+            for pool in (k32, v32):
+                chunk = np.bitwise_xor.reduce(pool[p, :, h, :].reshape(16, 8, 4), axis=2)  # row, chunk
+                acc ^= (chunk[:8] ^ chunk[8:]).reshape(64)
+            sc = np.where(lane & 16, vs[p * 16 + (lane & 15), h], ks[p * 16 + (lane & 15), h])
+            acc ^= sc
+        out[w] = acc
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("dtype,d", [(DTYPE_F16, 128), (DTYPE_F32, 64), (DTYPE_Q8A, 128)])
 def test_read_units_checksum(gpu, dtype, d):
     say("read_units", dtype, d)
     n_kv, num_pages = 4, 40
@@ -60,6 +82,11 @@ def test_read_units_checksum(gpu, dtype, d):
     sync()
     k32 = pk.k.view(torch.int32).cpu().numpy().view(np.uint32).reshape(num_pages, 16, n_kv, -1)
     v32 = pk.v.view(torch.int32).cpu().numpy().view(np.uint32).reshape(num_pages, 16, n_kv, -1)
-    exp = _expected(k32, v32, pages, kvhs, start, num_pages, n_kv)
+    if dtype == DTYPE_Q8A:
+        ks = pk.ks.view(torch.int32).cpu().numpy().view(np.uint32)
+        vs = pk.vs.view(torch.int32).cpu().numpy().view(np.uint32)
+        exp = _expected_q8(k32, v32, ks, vs, pages, kvhs, start, num_pages, n_kv)
+    else:
+        exp = _expected(k32, v32, pages, kvhs, start, num_pages, n_kv)
     got = sink.cpu().numpy().view(np.uint32)
     assert np.array_equal(got, exp)
