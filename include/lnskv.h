@@ -121,20 +121,28 @@ int lnskv_append(const lnskv_pages* c, const float* k_new_dev, const float* v_ne
  *   range: its output row is zero and the fused variants store nothing for
  *   it (as lnskv_append skips tokens outside the table).
  *   split_tokens: tokens per split-K partition (multiple of 16), or 0 to let
- *   the library schedule: f16 pages with head_dim 128 and at most 4096
- *   sequences then run stream-K (every resident wave of the device takes an
- *   equal share of all the batch's pages; a second kernel merges the pieces),
- *   other shapes split-K with a partition size chosen from the batch.
+ *   the library schedule.  f16 and Q8A pages with head_dim 128 and at most
+ *   4096 sequences then run one of two schedules, each giving every
+ *   workgroup an equal share of all the batch's pages: a small batch (at most
+ *   16 pages per compute unit, bounded from max_kv_len) one kernel whose
+ *   workgroups merge the pieces they share; a larger one stream-K (one wave
+ *   per resident slot, then a merge kernel).  The environment variable
+ *   LNSKV_DECODE_SCHEDULE=stream-k or =workgroup forces one of the two (the
+ *   workspace query must see the same setting).  Other shapes run split-K
+ *   with a partition size chosen from the batch.
  *   workspace_dev/ws_bytes: 16-byte aligned device scratch of at least
  *   lnskv_decode_workspace_size(...) bytes (same n_seq, n_heads, max_kv_len
  *   and split_tokens, same current device), or NULL/0 to use a buffer the
  *   library keeps per device (calls that use it must not overlap in time; see
- *   lnskv_workspace_reserve for how it grows).  The workspace holds the partial
- *   results of one call; nothing carries over between calls.  Calls that
- *   overlap in time need distinct workspaces.
+ *   lnskv_workspace_reserve for how it grows).  Its first
+ *   LNSKV_WORKSPACE_HEADER_BYTES bytes must be zero before its first use
+ *   (hipMemset once); every call leaves them zero again.  The rest holds the
+ *   partial results of one call.  Calls that overlap in time need distinct
+ *   workspaces.
  * Pages in the window whose table entry is LNSKV_NO_PAGE or >= num_pages are
  * skipped (contribute nothing).  An empty window gives a zero output row.
  * ------------------------------------------------------------------------- */
+#define LNSKV_WORKSPACE_HEADER_BYTES 4096
 int lnskv_decode_workspace_size(const lnskv_pages* c, int32_t n_seq, int32_t n_heads,
                                 int32_t max_kv_len, int32_t split_tokens, size_t* bytes);
 int lnskv_decode(const lnskv_pages* c, const float* q_dev, float* out_dev,

@@ -28,6 +28,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 // that an all-masked page leaves alpha = exp2(0) = 1 instead of NaN.
 constexpr float kMInit = -1e30f;
 constexpr int kSkMaxSeqs = kWave * kWave;  // stream-K: 64 groups of 64 sequences
+// Every decode workspace starts with this many bytes of per-workgroup counts
+// (the workgroup schedule's), zero before the first call and after every
+// call; the other schedules leave them alone.
+constexpr size_t kWsHeaderBytes = LNSKV_WORKSPACE_HEADER_BYTES;
+constexpr int kWgMaxGroups = (int)(kWsHeaderBytes / 4);
+// The workgroup schedule serves batches of at most this many (sequence, kv
+// head, page) units per workgroup (upper bound from max_kv_len); stream-K the
+// larger ones.
+constexpr int kWgSmallPages = 8;
 
 // ---------------------------------------------------------------------------
 // Storage traits: bytes per element.
@@ -141,6 +150,8 @@ struct DecodeArgs {
   float* ws_acc;        // [n_seq][n_heads][max_parts][D] partial numerators
   float* ws_ml;         // [n_seq][n_heads][max_parts][2] partial (max, sum)
   int4* sk_desc;        // stream-K: per wave, the segment its first piece closes
+  uint32_t* wg_cnt;     // workgroup schedule: per workgroup, a count of the workgroups done
+                        // with the segment that starts in it (zero between calls)
   const float* gate;      // gated attention: out *= gate ([n_seq][n_heads][D]); nullptr: none
   const float* rope_inv;  // fused RoPE in the MFMA kernels: inverse frequencies
   int32_t rope_half;      // fused RoPE: rotary_dim / 2, 32 or 64; 0: none (the kernels without RoPE run)
@@ -355,6 +366,13 @@ template <bool FUSED>
 int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, bool q8, hipStream_t st);
 // Waves of the stream-K kernel resident at once on the current device.
 int mfma_sk_waves(int rep, bool fused, bool q8, int* waves);
+// Workgroup schedule of the MFMA kernels (n_seq <= kSkMaxSeqs): n_wg
+// workgroups, one per CU (mfma_wg_count); the workspace holds the header of
+// kWsHeaderBytes (a count per workgroup, zero between calls) and then 2 * rep
+// partial rows per workgroup.
+template <bool FUSED>
+int launch_decode_mfma_wg(const DecodeArgs& a, int rep, int n_seq, int n_wg, bool q8, hipStream_t st);
+int mfma_wg_count(int* n_wg);
 
 // Chunked prefill over f16 pages with head_dim 128 (lnskv_prefill_attention).
 struct PrefillArgs {

@@ -15,6 +15,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -379,16 +380,33 @@ __global__ __launch_bounds__(kBlock) void split_gated_query_vec_kernel(const flo
   }
 }
 
-// How one decode call runs.  Stream-K (one wave per resident slot, each
-// taking an equal share of all pages) when the caller leaves the split to
-// the library, the MFMA kernel serves the pages and there are at most
-// kSkMaxSeqs sequences; split-K partitions of `split` tokens otherwise.
+// How one decode call runs, when the caller leaves the split to the library,
+// the MFMA kernel serves the pages and there are at most kSkMaxSeqs
+// sequences: a small batch (at most kWgSmallPages units per workgroup) runs
+// the workgroup schedule, one kernel whose workgroups merge what they share;
+// a larger one stream-K (one wave per resident slot, each taking an equal
+// share of all pages, then a merge kernel), which measured faster there.
+// Split-K partitions of `split` tokens otherwise.
 struct DecodePlan {
   int split = 0;      // split-K: tokens per partition
   int max_parts = 1;  // split-K: partitions of the longest sequence
   int sk_waves = 0;   // > 0: stream-K with this many waves
+  int wg = 0;         // > 0: the workgroup schedule with this many workgroups
   size_t ws_bytes = 0;
 };
+
+// LNSKV_DECODE_SCHEDULE=stream-k or =workgroup forces that schedule wherever
+// the library would choose between the two (tests, tuning); unset or any
+// other value: by batch size.  Read on every plan, so that a workspace query
+// and the call it sizes see the same setting.
+enum { kScheduleAuto = 0, kScheduleStreamK = 1, kScheduleWorkgroup = 2 };
+int schedule_setting() {
+  const char* v = std::getenv("LNSKV_DECODE_SCHEDULE");
+  if (v == nullptr) return kScheduleAuto;
+  if (std::strcmp(v, "stream-k") == 0) return kScheduleStreamK;
+  if (std::strcmp(v, "workgroup") == 0) return kScheduleWorkgroup;
+  return kScheduleAuto;
+}
 
 int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, int split_tokens, int fused,
                 DecodePlan* p) {
@@ -398,16 +416,28 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
   const bool q8 = mfma_q8_path((int)c->dtype, d, rep);
   if (split_tokens == 0 && (mfma_path((int)c->dtype, d, rep) || q8) && n_seq <= kSkMaxSeqs &&
       units < ((int64_t)1 << 30)) {
-    // fused < 0: either kind (the workspace query), sized for the larger
+    int n_wg = 0;
+    if (int rc = mfma_wg_count(&n_wg)) return rc;
+    const int setting = schedule_setting();
+    if (setting == kScheduleWorkgroup ||
+        (setting == kScheduleAuto && units <= (int64_t)kWgSmallPages * n_wg)) {
+      // a small batch: the workgroup schedule (one kernel); the header, then
+      // 2 * rep partial rows of (acc[d], m, l) per workgroup
+      p->wg = n_wg;
+      p->ws_bytes = kWsHeaderBytes + (size_t)n_wg * 2 * rep * ((size_t)d + 2) * sizeof(float);
+      return LNSKV_OK;
+    }
+    // stream-K; fused < 0: either kind (the workspace query), sized for the
+    // larger
     int w0 = 0, w1 = 0;
     if (fused <= 0)
       if (int rc = mfma_sk_waves(rep, false, q8, &w0)) return rc;
     if (fused != 0)
       if (int rc = mfma_sk_waves(rep, true, q8, &w1)) return rc;
     p->sk_waves = std::max(w0, w1);
-    // partial rows (acc, then (m, l)) of two pieces per wave, then one
-    // 16-byte descriptor per wave
-    p->ws_bytes = (size_t)p->sk_waves * (2 * rep * ((size_t)d + 2) * sizeof(float) + 16);
+    // the header, then partial rows (acc, then (m, l)) of two pieces per
+    // wave, then one 16-byte descriptor per wave
+    p->ws_bytes = kWsHeaderBytes + (size_t)p->sk_waves * (2 * rep * ((size_t)d + 2) * sizeof(float) + 16);
     return LNSKV_OK;
   }
   p->split = split_tokens ? split_tokens : choose_split(n_seq, n_kv, max_kv_len);
@@ -416,7 +446,8 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
   p->max_parts = std::max(1, (max_kv_len + p->split - 1) / p->split);
   if (p->max_parts > 65535)
     return fail(LNSKV_ERR_INVALID, "max_kv_len %d needs more than 65535 partitions", max_kv_len);
-  p->ws_bytes = workspace_bytes(n_seq, n_heads, d, p->max_parts);
+  const size_t part = workspace_bytes(n_seq, n_heads, d, p->max_parts);
+  p->ws_bytes = part > 0 ? kWsHeaderBytes + part : 0;
   return LNSKV_OK;
 }
 
@@ -477,6 +508,9 @@ int library_buffer(int which, size_t need, void** out, hipStream_t stream) {
                   "pass a workspace or call lnskv_workspace_reserve before capturing",
                   kBufferName[which], g_ws.size() > slot ? g_ws[slot].bytes : (size_t)0, need);
     if (int rc = grow_locked(dev, which, need)) return rc;
+    // a decode workspace starts with its counts at zero
+    if (which == 0 && hipMemsetAsync(g_ws[slot].ptr, 0, kWsHeaderBytes, stream) != hipSuccess)
+      return fail(LNSKV_ERR_HIP, "hipMemsetAsync of the workspace header failed");
   }
   *out = g_ws[slot].ptr;
   return LNSKV_OK;
@@ -517,6 +551,8 @@ int noalloc_scratch(void** out) {
         int waves = 0;
         if (int rc = mfma_sk_waves(rep, true, q8, &waves)) return rc;
       }
+    int n_wg = 0;
+    if (int rc = mfma_wg_count(&n_wg)) return rc;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -634,15 +670,21 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
   a.rope_half = rope_half;
   a.rope_inv = rope_half > 0 ? rope->inv_freqs_dev : nullptr;
   a.gate = gate;
+  if (plan.wg > 0) {
+    a.wg_cnt = static_cast<uint32_t*>(ws);
+    a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeaderBytes);
+    a.ws_ml = a.ws_acc + (size_t)plan.wg * 2 * rep * c->head_dim;
+    return launch_decode_mfma_wg<FUSED>(a, rep, n_seq, plan.wg, c->dtype == LNSKV_DTYPE_Q8A, (hipStream_t)stream);
+  }
   if (plan.sk_waves > 0) {
-    a.ws_acc = static_cast<float*>(ws);
+    a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeaderBytes);
     a.ws_ml = a.ws_acc + (size_t)plan.sk_waves * 2 * rep * c->head_dim;
     a.sk_desc = reinterpret_cast<int4*>(a.ws_ml + (size_t)plan.sk_waves * 2 * rep * 2);
     return launch_decode_mfma_sk<FUSED>(a, rep, n_seq, plan.sk_waves, c->dtype == LNSKV_DTYPE_Q8A,
                                         (hipStream_t)stream);
   }
   if (need > 0) {
-    a.ws_acc = static_cast<float*>(ws);
+    a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeaderBytes);
     a.ws_ml = a.ws_acc + (size_t)n_seq * n_heads * plan.max_parts * c->head_dim;
   }
   return launch_decode<FUSED>(a, c->dtype, (int)c->head_dim, rep, n_seq, (hipStream_t)stream);
@@ -843,9 +885,14 @@ int lnskv_workspace_reserve(size_t decode_bytes, size_t rope_bytes, size_t q4l_b
   if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
   std::lock_guard<std::mutex> lock(g_ws_mutex);
   const size_t want[kLibraryBuffers] = {decode_bytes, rope_bytes, q4l_bytes};
-  for (int i = 0; i < kLibraryBuffers; ++i)
-    if (want[i] > 0)
-      if (int rc = grow_locked(dev, i, want[i])) return rc;
+  for (int i = 0; i < kLibraryBuffers; ++i) {
+    if (want[i] == 0) continue;
+    const size_t slot = (size_t)dev * kLibraryBuffers + (size_t)i;
+    const bool grows = g_ws.size() <= slot || g_ws[slot].bytes < want[i];
+    if (int rc = grow_locked(dev, i, want[i])) return rc;
+    if (grows && i == 0 && hipMemset(g_ws[slot].ptr, 0, kWsHeaderBytes) != hipSuccess)
+      return fail(LNSKV_ERR_HIP, "hipMemset of the workspace header failed");
+  }
   return LNSKV_OK;
 }
 

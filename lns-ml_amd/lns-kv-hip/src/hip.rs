@@ -19,6 +19,7 @@ extern "C" {
     pub fn hipMalloc(ptr: *mut *mut c_void, size: usize) -> HipError;
     pub fn hipFree(ptr: *mut c_void) -> HipError;
     pub fn hipMemcpy(dst: *mut c_void, src: *const c_void, size: usize, kind: c_int) -> HipError;
+    pub fn hipMemset(dst: *mut c_void, value: c_int, size: usize) -> HipError;
     pub fn hipStreamSynchronize(stream: HipStream) -> HipError;
     pub fn hipGetErrorString(err: HipError) -> *const c_char;
 }
@@ -48,6 +49,16 @@ impl<T: Copy> DeviceBuffer<T> {
             hip(unsafe { hipMalloc(&mut p, len * size_of::<T>()) }, "hipMalloc")?;
         }
         Ok(Self { ptr: p as *mut T, len, _t: PhantomData })
+    }
+
+    /// Device memory for `len` elements, every byte zero (decode workspaces
+    /// must start so).
+    pub fn zeroed(len: usize) -> Result<Self, String> {
+        let b = Self::new(len)?;
+        if len > 0 {
+            hip(unsafe { hipMemset(b.ptr as *mut c_void, 0, len * size_of::<T>()) }, "hipMemset")?;
+        }
+        Ok(b)
     }
 
     pub fn from_slice(host: &[T]) -> Result<Self, String> {

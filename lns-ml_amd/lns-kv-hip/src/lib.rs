@@ -231,8 +231,10 @@ impl KvLayer {
 
     /// Every sequence's new token appended and attended in one call
     /// (`lnskv_append_decode`).  `workspace`: a device buffer of at least
-    /// `decode_workspace_size` bytes (per stream), or `None` for the
-    /// library's per-device buffer (calls must then not overlap).
+    /// `decode_workspace_size` bytes (per stream) made by
+    /// [`DeviceBuffer::zeroed`] (its first `LNSKV_WORKSPACE_HEADER_BYTES`
+    /// must be zero; every call leaves them so), or `None` for the library's
+    /// per-device buffer (calls must then not overlap).
     pub fn append_decode(
         &self,
         b: &DecodeBatch,

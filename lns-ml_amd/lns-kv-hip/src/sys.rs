@@ -13,6 +13,9 @@ use std::os::raw::{c_char, c_int, c_void};
 pub const LNSKV_PAGE_SIZE: u32 = 16;
 /// `LNSKV_NO_PAGE`: an unallocated block-table entry (engine.rs:65 `u32::MAX`).
 pub const LNSKV_NO_PAGE: u32 = 0xFFFF_FFFF;
+/// `LNSKV_WORKSPACE_HEADER_BYTES`: the leading bytes of a decode workspace
+/// that must be zero before its first use.
+pub const LNSKV_WORKSPACE_HEADER_BYTES: usize = 4096;
 /// `LNSKV_NOALLOC_SCRATCH_BYTES`: the static scratch of `lnskv_append_decode_noalloc`.
 pub const LNSKV_NOALLOC_SCRATCH_BYTES: usize = 24 << 20;
 /// `LNSKV_Q4L_DISK_BYTES` / `LNSKV_Q4L_DEVICE_BYTES`: one Q4_L super-block on disk / on the device.

@@ -26,6 +26,10 @@ ERR_HIP = -4
 ERR_UNSUPPORTED = -5
 ERR_WORKSPACE = -6
 
+# leading bytes of a decode workspace that must be zero before its first use
+# (the workgroup schedule's counters; every call leaves them zero)
+WORKSPACE_HEADER_BYTES = 4096
+
 
 class LnskvError(RuntimeError):
     """A non-zero lnskv_status with the library's message (the reference's

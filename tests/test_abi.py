@@ -79,12 +79,19 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert rc == _lib.ERR_INVALID
 
 
+def test_workspace_header_constant_matches_the_header():
+    text = open(os.path.join(ROOT, "include", "lnskv.h")).read()
+    m = re.search(r"#define LNSKV_WORKSPACE_HEADER_BYTES (\d+)", text)
+    assert m and int(m.group(1)) == _lib.WORKSPACE_HEADER_BYTES
+
+
 def test_workspace_size_formula():
     lib = _lib.lib()
     p = Pages(None, None, None, None, 16384, 8, 128, _lib.DTYPE_F16)
     out = C.c_size_t()
     assert lib.lnskv_decode_workspace_size(C.byref(p), 32, 32, 4097, 256, C.byref(out)) == 0
-    assert out.value == 32 * 32 * 17 * (128 + 2) * 4  # partial numerators + (max, sum)
+    # the counter header, then partial numerators + (max, sum)
+    assert out.value == _lib.WORKSPACE_HEADER_BYTES + 32 * 32 * 17 * (128 + 2) * 4
     assert lib.lnskv_decode_workspace_size(C.byref(p), 4, 32, 200, 256, C.byref(out)) == 0
     assert out.value == 0  # one partition: no partials
 

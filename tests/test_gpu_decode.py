@@ -11,7 +11,7 @@ import torch
 import oracle as O
 from gpu_util import TOL, dev_f32, dev_i32, fill_pages, host_pages, rel_err, say
 from lnskv import DTYPE_F16, DTYPE_F32, DTYPE_Q8A, DTYPE_NAMES, NO_PAGE
-from lnskv._lib import ERR_WORKSPACE, LnskvError
+from lnskv._lib import ERR_WORKSPACE, WORKSPACE_HEADER_BYTES as HEADER_BYTES, LnskvError
 from lnskv.device import PagedKV, sync
 
 pytestmark = pytest.mark.gpu
@@ -261,15 +261,23 @@ def _sk_lens(n, seed):
     return tuple(int(x) for x in lens[:n])
 
 
+SCHEDULES = ["stream-k", "workgroup"]
+
+
+@pytest.mark.parametrize("schedule", SCHEDULES)
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_Q8A])
 @pytest.mark.parametrize("rep", [1, 2, 4, 8])
-def test_stream_k_schedule(gpu, rep, dtype):
-    """split_tokens = 0 on the MFMA path runs the stream-K schedule (every
-    wave an equal share of all pages; pieces merged by combine_sk_kernel).
-    64 sequences (one group) with empty, short and long lengths, windows,
-    a missing page; unfused and fused, against the f64 oracle and against
-    the split-K schedule; f16 and Q8A pages (pages and scales bit-exact)."""
-    say("stream-K rep", rep, DTYPE_NAMES[dtype])
+def test_stream_k_schedule(gpu, monkeypatch, rep, dtype, schedule):
+    """split_tokens = 0 on the MFMA path runs one of two schedules, forced
+    here through LNSKV_DECODE_SCHEDULE: stream-K (every wave an equal share
+    of all pages; pieces merged by combine_sk_kernel) or the workgroup
+    schedule (every workgroup an equal share; pieces merged in LDS and, across
+    workgroups, by the last workgroup to finish).  64 sequences (one group)
+    with empty, short and long lengths, windows, a missing page; unfused and
+    fused, against the f64 oracle and against the split-K schedule; f16 and
+    Q8A pages (pages and scales bit-exact)."""
+    monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", schedule)
+    say(schedule, "rep", rep, DTYPE_NAMES[dtype])
     n_kv, d = 8, 128
     lens = _sk_lens(64, seed=rep)
     pk, tables, kv_len, q = _case(gpu, dtype, d, rep, n_kv, lens, seed=90 + rep)
@@ -306,12 +314,15 @@ def test_stream_k_schedule(gpu, rep, dtype):
     assert rel_err(out1, ref1).max() < TOL[dtype]
 
 
-def test_stream_k_caller_workspace_and_fallback(gpu):
-    """A caller-provided workspace of exactly the queried size serves the
-    stream-K schedule (its size does not depend on the batch up to 4096
-    sequences; 4097 fall back to split-K); 65 sequences take two groups of
-    64; one short sequence leaves most waves idle."""
-    say("stream-K workspace / fallback")
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_stream_k_caller_workspace_and_fallback(gpu, monkeypatch, schedule):
+    """A caller-provided workspace of exactly the queried size serves each
+    schedule (its size does not depend on the batch up to 4096 sequences;
+    4097 fall back to split-K); 65 sequences take two groups of 64; one short
+    sequence leaves most waves idle.  The workspace is zeroed once and
+    reused: every call leaves its counter header zero."""
+    monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", schedule)
+    say(schedule, "workspace / fallback")
     n_kv, d, rep = 8, 128, 4
     pk0 = PagedKV(16, n_kv, d, DTYPE_F16, gpu)
     sizes = [pk0.workspace_size(n, n_kv * rep, 4096, 0) for n in (1, 64, 4096, 4097)]
@@ -322,31 +333,37 @@ def test_stream_k_caller_workspace_and_fallback(gpu):
         ref = O.decode_f64(hp, q, tables, kv_len, None, 0.0883883)
         mkv = int(kv_len.max())
         nbytes = pk.workspace_size(len(lens), n_kv * rep, mkv, 0)
-        ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=gpu)
-        out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
-                        max_kv_len=mkv, scale=0.0883883, split=0, workspace=ws)
-        sync()
-        assert rel_err(out, ref).max() < TOL[DTYPE_F16], len(lens)
+        # the workgroup schedule (up to 4096 sequences) has its counter header
+        assert nbytes > HEADER_BYTES or len(lens) > 4096
+        ws = torch.zeros(max(nbytes, HEADER_BYTES), dtype=torch.uint8, device=gpu)
+        for _ in range(2):
+            out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                            max_kv_len=mkv, scale=0.0883883, split=0, workspace=ws)
+            sync()
+            assert rel_err(out, ref).max() < TOL[DTYPE_F16], len(lens)
+            assert int(ws[:HEADER_BYTES].count_nonzero()) == 0, len(lens)
     # a workspace that is large enough but not 16-byte aligned is refused
     pk, tables, kv_len, q = _case(gpu, DTYPE_F16, d, rep, n_kv, _sk_lens(64, 3), seed=64)
     mkv = int(kv_len.max())
     nbytes = pk.workspace_size(64, n_kv * rep, mkv, 0)
-    ws = torch.empty(nbytes + 64, dtype=torch.uint8, device=gpu)[4:]
+    ws = torch.zeros(nbytes + 64, dtype=torch.uint8, device=gpu)[4:]
     with pytest.raises(LnskvError) as e:
         pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
                   max_kv_len=mkv, scale=0.0883883, split=0, workspace=ws)
     assert e.value.status == ERR_WORKSPACE
 
 
+@pytest.mark.parametrize("schedule", SCHEDULES)
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_Q8A])
 @pytest.mark.parametrize("n_seq", [130, 4096])
-def test_stream_k_many_sequences(gpu, n_seq, dtype):
-    """More than 64 sequences on the stream-K schedule (groups of 64, one
-    lane per sequence): a whole group of empty sequences, ragged lengths and
-    windows, unfused and fused, against the f64 oracle; f16 and Q8A pages
-    (the Q8A fused call quantizes each new token in the wave that holds it;
-    pages and scales bit-exact)."""
-    say("stream-K n_seq", n_seq, DTYPE_NAMES[dtype])
+def test_stream_k_many_sequences(gpu, monkeypatch, n_seq, dtype, schedule):
+    """More than 64 sequences on both schedules (groups of 64, one lane per
+    sequence): a whole group of empty sequences, ragged lengths and windows,
+    unfused and fused, against the f64 oracle; f16 and Q8A pages (the Q8A
+    fused call quantizes each new token in the wave that holds it; pages and
+    scales bit-exact)."""
+    monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", schedule)
+    say(schedule, "n_seq", n_seq, DTYPE_NAMES[dtype])
     n_kv, d, rep = 8, 128, 4
     rng = np.random.default_rng(n_seq)
     hi = 700 if n_seq < 1000 else 48
@@ -378,6 +395,28 @@ def test_stream_k_many_sequences(gpu, n_seq, dtype):
         assert np.array_equal(got.ks.view(np.uint32), hp.ks.view(np.uint32))
         assert np.array_equal(got.vs.view(np.uint32), hp.vs.view(np.uint32))
     assert rel_err(out1, ref1).max() < TOL[dtype]
+
+
+def test_schedule_chosen_by_batch_size(gpu, monkeypatch):
+    """Without LNSKV_DECODE_SCHEDULE the library runs the workgroup schedule
+    for a batch of at most 16 pages per compute unit (the reference's
+    one-sequence call: 4096 tokens, 8 kv heads) and stream-K for a larger one
+    (64 such sequences): the workspace sizes match the forced settings'."""
+    n_kv, d, rep = 8, 128, 4
+    pk = PagedKV(16, n_kv, d, DTYPE_Q8A, gpu)
+
+    def size(n, setting):
+        if setting is None:
+            monkeypatch.delenv("LNSKV_DECODE_SCHEDULE", raising=False)
+        else:
+            monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", setting)
+        return pk.workspace_size(n, n_kv * rep, 4096, 0)
+
+    wg, sk = size(1, "workgroup"), size(1, "stream-k")
+    assert wg != sk
+    assert size(1, None) == wg
+    assert size(64, None) == sk
+    assert size(64, "bogus") == sk
 
 
 @pytest.mark.parametrize("force_valu", ["0", "1"])

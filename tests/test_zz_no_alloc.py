@@ -82,7 +82,7 @@ def test_noalloc_matches_append_decode_twice(gpu, dtype):
         dt, dl = dev_i32(tables, gpu), dev_i32(kv_len, gpu)
         max_len = int(kv_len.max())
         scale = float(1.0 / np.sqrt(128))
-        ws = torch.empty(max(pk.workspace_size(n_seq, n_heads, max_len, 0), 16), dtype=torch.uint8, device=gpu)
+        ws = torch.zeros(max(pk.workspace_size(n_seq, n_heads, max_len, 0), 16), dtype=torch.uint8, device=gpu)
         ref_out = pk.append_decode(dq, dk, dv, dt, dl, n_heads=n_heads, max_kv_len=max_len, scale=scale,
                                    workspace=ws)
         out = torch.full((n_seq, n_heads, 128), float("nan"), dtype=torch.float32, device=gpu)
