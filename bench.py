@@ -531,7 +531,23 @@ def cpu_baseline(w, runner, seconds: float, threads: int):
 
     dt, n = timed(threads, seconds)
     dt1, n1 = timed(1, 0.0) if threads > 1 else (dt, n)  # one whole step on one thread
+    # the checker's use of the oracle: the GPU's output of this step against
+    # the f64 oracle over the same stored pages (the step rewrites the same
+    # token to the same slot, so the pages the oracle holds are the step's)
+    import torch
+
+    o = runner.run(0)
+    torch.cuda.synchronize()
+    o = o.cpu().numpy()
+    ref = O.decode_f64(hp, q, tables, kv_len, None, w.scale)
+    row, ele = O.rel_err_rows(o, ref), O.rel_err_elements(o, ref)
+    parity = {"vs": "f64 oracle over the step's stored pages (layer 0)",
+              "max_row_rel_err": float(row.max()),
+              "row_tolerance": {0: 1e-5, 1: 1e-3, 2: 1e-5}[w.dtype],
+              "max_elem_rel_err_floor_1e-6": float(ele.max()),
+              "median_elem_rel_err_floor_1e-6": float(np.median(ele))}
     return {"value": round(dt * 1e6, 1), "unit": "µs/step", "cores": threads, "kind": "port",
+            "parity": parity,
             "sample": f"{n} whole {w.name} steps (append + reference-order f32 scan of all "
                       f"{len(rows)} decoding sequences), {threads} OpenMP threads, "
                       f"{dt * n:.1f} s; nproc={os.cpu_count()}",

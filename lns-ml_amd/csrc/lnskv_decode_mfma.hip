@@ -1638,11 +1638,19 @@ int launch_decode_mfma_wg(const DecodeArgs& a, int rep, int n_seq, int n_wg, boo
   if (n_seq > kSkMaxSeqs)
     return fail(LNSKV_ERR_INVALID, "the workgroup schedule serves at most %d sequences", kSkMaxSeqs);
   if (n_wg <= 0 || n_wg > kWgMaxGroups) return fail(LNSKV_ERR_INVALID, "%d workgroups", n_wg);
+  // Launch only the workgroups the batch can fill: with at most `bound`
+  // units (from max_kv_len), groups of NW * kWgMinPages units each cover
+  // them, so the kernel's chunk C = max(NW * kWgMinPages, ceil(T / G)) stays
+  // at its minimum and [0, G * C) still holds every unit.
+  const int nw = q8 ? kWgWavesQ8 : kWgWaves;
+  const int64_t bound = (int64_t)n_seq * a.n_kv * ((int64_t)a.max_kv_len / kPage + 1);
+  const int64_t per = (int64_t)nw * kWgMinPages;
+  const int groups = (int)std::max<int64_t>(1, std::min<int64_t>(n_wg, (bound + per - 1) / per));
   switch (rep) {
-    case 1: launch_wg_rep<1, FUSED>(a, n_seq, n_wg, q8, st); break;
-    case 2: launch_wg_rep<2, FUSED>(a, n_seq, n_wg, q8, st); break;
-    case 4: launch_wg_rep<4, FUSED>(a, n_seq, n_wg, q8, st); break;
-    case 8: launch_wg_rep<8, FUSED>(a, n_seq, n_wg, q8, st); break;
+    case 1: launch_wg_rep<1, FUSED>(a, n_seq, groups, q8, st); break;
+    case 2: launch_wg_rep<2, FUSED>(a, n_seq, groups, q8, st); break;
+    case 4: launch_wg_rep<4, FUSED>(a, n_seq, groups, q8, st); break;
+    case 8: launch_wg_rep<8, FUSED>(a, n_seq, groups, q8, st); break;
     default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
   }
   return hip_check("workgroup decode kernel launch");

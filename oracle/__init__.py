@@ -247,6 +247,13 @@ def stored_values(pages: HostPages, which_v: bool) -> np.ndarray:
     return a.reshape(-1, pages.n_kv, pages.head_dim).astype(np.float64) * sc[:, :, None].astype(np.float64)
 
 
+def rel_err_elements(out, ref, floor: float = 1e-6) -> np.ndarray:
+    """Element-wise relative error |o_i - r_i| / max(|r_i|, floor)."""
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return np.abs(out - ref) / np.maximum(np.abs(ref), floor)
+
+
 def rel_err_rows(out, ref) -> np.ndarray:
     """Per (sequence, query head) row: max_i |o_i - r_i| / max(max_i |r_i|, 1e-30)."""
     out = np.asarray(out, np.float64)

@@ -5,9 +5,12 @@ on the GPU; the oracle replays it on a host copy of every page the step can
 touch.  Pages must match bit for bit; attention outputs must be within the
 row-normwise tolerance (1e-3 f16, 1e-5 f32 and Q8A) of the f64 oracle over the exact
 stored values, and within the same tolerance of the reference-order f32 scan
-(the reference CPU path)."""
+(the reference CPU path); the element-wise relative error (floor 1e-6) is
+reported.  Every page outside the step's footprint is compared with its
+contents before the step."""
 import numpy as np
 import pytest
+import torch
 
 import oracle as O
 from gpu_util import TOL, host_pages, rel_err, remap_tables, say
@@ -47,9 +50,20 @@ def test_config_step(gpu, name):
     assert O.append(hp, r.k_new.cpu().numpy(), r.v_new.cpu().numpy(), np.arange(len(rows), dtype=np.int32),
                     kv_len - 1, dec_tables) == 0
 
+    # the whole pools before the step: pages outside its footprint must come
+    # out untouched
+    before = {t: getattr(pk, t).clone() for t in ("k", "v", "ks", "vs") if getattr(pk, t) is not None}
     say("config", name, "step on gpu")
     out = r.run(0)
     sync()
+    outside = np.setdiff1d(np.arange(w.num_pages, dtype=np.int64), pages.astype(np.int64))
+    if len(outside):
+        idx = torch.from_numpy(outside).to(gpu)
+        sidx = (idx[:, None] * 16 + torch.arange(16, device=gpu)[None, :]).reshape(-1)
+        for t, b in before.items():
+            i = sidx if t in ("ks", "vs") else idx
+            assert torch.equal(getattr(pk, t).index_select(0, i), b.index_select(0, i)), f"{t} outside the footprint"
+    del before
     got, _ = host_pages(pk, pages)
     assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8)), "K pages differ"
     assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8)), "V pages differ"
@@ -61,8 +75,11 @@ def test_config_step(gpu, name):
     assert np.isfinite(o).all()
     ref = O.decode_f64(hp, q, dec_tables, kv_len, None, w.scale)
     err = rel_err(o, ref)
-    say("config", name, "max rel err vs f64", float(err.max()))
+    ele = O.rel_err_elements(o, ref)
+    say("config", name, "max rel err vs f64: row-normwise", float(err.max()), "element-wise (floor 1e-6)",
+        float(ele.max()), "median element", float(np.median(ele)))
     assert err.max() < TOL[w.dtype]
+    assert np.isfinite(ele).all()
     if name in ("c1", "c2", "c2-q8a"):
         scan = O.decode_refscan(hp, q, dec_tables, kv_len, None, w.scale)
         assert rel_err(o, scan.astype(np.float64)).max() < TOL[w.dtype]

@@ -364,3 +364,14 @@ def test_append_decode_refscan_is_append_then_scan():
     O.append(b_pages, k_new, v_new, np.arange(4, dtype=np.int32), kv_len - 1, tables)
     b = O.decode_refscan(b_pages, q, tables, kv_len, None, 0.125)
     assert np.array_equal(a_pages.k, b_pages.k) and np.array_equal(a, b)
+
+
+def test_error_measures_by_hand():
+    """The two error measures of the tolerance definition on values worked
+    by hand: row-normwise max|o-r| / max|r| (floor 1e-30) and element-wise
+    |o-r| / max(|r|, 1e-6)."""
+    ref = np.array([[1.5, 1e-7, 0.0, -2.0]])
+    out = np.array([[1.0, 0.0, 2e-7, -2.0]])
+    assert np.allclose(O.rel_err_rows(out, ref), [0.5 / 2.0])
+    assert np.allclose(O.rel_err_elements(out, ref)[0], [0.5 / 1.5, 1e-7 / 1e-6, 2e-7 / 1e-6, 0.0])
+    assert O.rel_err_rows(np.zeros((1, 3)), np.zeros((1, 3)))[0] == 0.0
