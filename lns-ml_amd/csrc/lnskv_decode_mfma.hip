@@ -1724,13 +1724,20 @@ struct PfShape {
 __device__ __forceinline__ void pf_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Per-lane constants of the pair DMA and the LDS operand reads.
+// The K and V read offsets of operand j / nb are rebuilt from two registers
+// each (a constant XOR and an add) instead of being held per operand: with
+// two waves per SIMD the kernel has 256 VGPRs, and twelve held offsets
+// spilled.  K operand j reads chunk (4j + g) ^ n of row n, at
+// krow + ((64 j) ^ kx) with kx = 64 (n >> 2) and krow = 256 n + 16 (g ^ (n & 3));
+// V operand nb (dims 16 nb ..) reads chunk (2 nb + sub) ^ sw(Rv) of row
+// Rv = 4 (n >> 2) + g, at vrow + ((32 nb) ^ vx) with vx = 16 sw(Rv) (sw is
+// even) and vrow = 256 Rv + 8 (n & 1) + 16 sub, sub = (n & 3) >> 1.
 struct PfLanes {
   uint32_t koff;    // K DMA: token 4w+g, chunk n ^ (4w+g)
   uint32_t voff;    // V DMA: token 4g+w, chunk n ^ sw(4w+g)
   uint32_t lds_q;   // 1024 w: this wave's quarter of a page region
-  uint32_t krow;    // K reads: row n
-  uint32_t kchunk[4];  // 16 * ((4j + g) ^ n)
-  uint32_t vrd[8];   // transposed V reads of dims 16 nb ..: row, half and swizzled chunk, as Stream
+  uint32_t krow, kx;
+  uint32_t vrow, vx;
 };
 
 // DMA of this wave's share of pages ph0 and ph1 into `slot`: quarter w % 4
@@ -1779,17 +1786,22 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
   // are inline asm because the compiler cannot tell which slot a DMA writes
   // and would wait for every DMA in flight before a plain LDS read.  This
   // slot's DMAs have completed (vmcnt wait and barrier before the call).
+  // the XOR bases pass through an empty asm so that the compiler rebuilds
+  // the offsets here instead of hoisting all twelve out of the pair loop
+  uint32_t kx = pl.kx, vx = pl.vx;
+  asm volatile("" : "+v"(kx), "+v"(vx));
   const uint32_t kb = (uint32_t)(size_t)slot + pl.krow;
   half8 k[2][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    asm volatile("ds_read_b128 %0, %1" : "=v"(k[0][j]) : "v"(kb + pl.kchunk[j]) : "memory");
-    asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(k[1][j]) : "v"(kb + pl.kchunk[j]) : "memory");
+    const uint32_t ka = kb + ((64u * (uint32_t)j) ^ kx);
+    asm volatile("ds_read_b128 %0, %1" : "=v"(k[0][j]) : "v"(ka) : "memory");
+    asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(k[1][j]) : "v"(ka) : "memory");
   }
-  const uint32_t vb = (uint32_t)(size_t)slot + 2 * kVSlot;
+  const uint32_t vb = (uint32_t)(size_t)slot + 2 * kVSlot + pl.vrow;
   short4v bv[2][8];
   auto read_v = [&](int nb) {
-    const uint32_t a0 = vb + pl.vrd[nb];
+    const uint32_t a0 = vb + ((32u * (uint32_t)nb) ^ vx);
     asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[0][nb]) : "v"(a0) : "memory");
     asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(bv[1][nb]) : "v"(a0) : "memory");
   };
@@ -2007,13 +2019,11 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     pl.koff = R * rs + 16u * ((uint32_t)n ^ R);
     pl.voff = (uint32_t)(4 * g + j) * rs + 16u * ((uint32_t)n ^ v_swz((int)R));
     pl.lds_q = 1024u * (uint32_t)j;
-    pl.krow = (uint32_t)n * kRowBytes;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pl.kchunk[j] = 16u * ((uint32_t)(4 * j + g) ^ (uint32_t)n);
+    pl.krow = (uint32_t)n * kRowBytes + 16u * ((uint32_t)g ^ ((uint32_t)n & 3u));
+    pl.kx = 64u * ((uint32_t)n >> 2);
     const int Rv = 4 * (n >> 2) + g;
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb)
-      pl.vrd[nb] = (uint32_t)Rv * kRowBytes + 8u * (n & 1) + 16u * (((uint32_t)(2 * nb) + ((n & 3) >> 1)) ^ v_swz(Rv));
+    pl.vrow = (uint32_t)Rv * kRowBytes + 8u * (n & 1) + 16u * (uint32_t)((n & 3) >> 1);
+    pl.vx = 16u * v_swz(Rv);
   }
   lds_u8* ring = (lds_u8*)ring_;
 
