@@ -15,9 +15,15 @@ from lnskv.step import StepRunner
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c5"])
-def test_graph_replay_matches_eager(gpu, name):
+@pytest.mark.parametrize("name", ["c1", "c2", "c5", "c2-workgroup"])
+def test_graph_replay_matches_eager(gpu, monkeypatch, name):
+    """c2-workgroup: c2 forced onto the workgroup schedule, whose
+    cross-workgroup counts in the workspace header must be back at zero
+    after every replay."""
     say("graph replay", name)
+    if name.endswith("-workgroup"):
+        monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", "workgroup")
+        name = name.split("-")[0]
     w = make(name)
     r = StepRunner(w, gpu, n_layers=2, seed=3)
     eager = [r.run(layer).clone() for layer in (0, 1)]
@@ -35,6 +41,8 @@ def test_graph_replay_matches_eager(gpu, name):
             assert torch.equal(got, eager[layer]), (name, rep, layer)
             assert torch.equal(r.layers[layer].k, pages[layer][0])
             assert torch.equal(r.layers[layer].v, pages[layer][1])
+    if r.workspace is not None and r.workspace.numel() >= 4096:
+        assert int(r.workspace[:4096].count_nonzero()) == 0
 
 
 def test_library_workspace_under_capture(gpu):
