@@ -136,7 +136,9 @@ __global__ __launch_bounds__(kQ4lWaves * kWave) void q4l_gemv_acc_kernel(const u
   constexpr int kPerThread = (T * 8 * kQ4lRows + kQ4lWaves * kWave - 1) / (kQ4lWaves * kWave);
   __shared__ float red[kQ4lWaves][T][8][kQ4lRows];
   __shared__ __attribute__((aligned(16))) uint8_t wtile[kQ4lWaves][kQ4lBatch][kWTile];
-  const int lane = (int)(threadIdx.x & (kWave - 1)), q = (int)(threadIdx.x / kWave);
+  // q: the wave index, made visibly uniform so that block and sub-block
+  // offsets derived from it stay in scalar registers
+  const int lane = (int)(threadIdx.x & (kWave - 1)), q = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
   const int g = lane >> 4, n = lane & 15;
   const int row0 = (int)blockIdx.x * kQ4lRows;
   const int row = row0 + n;
@@ -168,6 +170,13 @@ __global__ __launch_bounds__(kQ4lWaves * kWave) void q4l_gemv_acc_kernel(const u
       __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)((int64_t)rows * bpr * kQ4lBlockBytes),
                                         kQ4lBufferFormat);
   lds_u8* wl = (lds_u8*)&wtile[q][0][0];
+  // The x operands of this launch's tiles through a buffer resource: the
+  // offset of (tile, sub-block) is wave-uniform (a scalar register) and the
+  // lane's 16 bytes a constant vector offset, so the loads need no 64-bit
+  // address arithmetic per lane.  The host keeps T * nsb * 1024 below 2^31.
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      INLINE_X ? (void*)x : (void*)(xa + (int64_t)tile0 * nsb * kWave), (short)0,
+      INLINE_X ? 0 : T * nsb * kWave * (int)sizeof(half8), kQ4lBufferFormat);
   for (int b0 = q; b0 < bpr; b0 += kQ4lWaves * kQ4lBatch) {
     int bb[kQ4lBatch];
     bool bok[kQ4lBatch];
@@ -207,7 +216,9 @@ __global__ __launch_bounds__(kQ4lWaves * kWave) void q4l_gemv_acc_kernel(const u
             const int64_t base = (int64_t)(vec < n_vec ? vec : 0) * x_stride + 32 * sb + 8 * g + 4 * (n >> 3);
             dst[u][t] = *reinterpret_cast<const float4v*>(x + base);
           } else {
-            dst[u][t] = xa[((int64_t)(tile0 + t) * nsb + sb) * kWave + lane];
+            dst[u][t] = __builtin_bit_cast(
+                half8, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, lane * (int)sizeof(half8),
+                                                             (t * nsb + sb) * kWave * (int)sizeof(half8), 0));
           }
         }
       }
@@ -325,6 +336,9 @@ extern "C" int lnskv_q4l_gemv_accumulate(const void* blocks_dev, const float* x_
                 y_stride, rows);
   if ((int64_t)rows * (cols / 256) * LNSKV_Q4L_DEVICE_BYTES > INT32_MAX)
     return fail(LNSKV_ERR_UNSUPPORTED, "a Q4L matrix over 2 GiB of blocks (%d x %d)", rows, cols);
+  // one launch's x operands (up to kQ4lMaxTiles tiles) are addressed with 32-bit offsets
+  if ((int64_t)kQ4lMaxTiles * (cols / 32) * kWave * (int64_t)sizeof(half8) > INT32_MAX)
+    return fail(LNSKV_ERR_UNSUPPORTED, "cols %d: one launch's x operands exceed 2 GiB", cols);
   if (x_stride % 4 != 0 || (reinterpret_cast<uintptr_t>(x_dev) & 15) != 0 ||
       (reinterpret_cast<uintptr_t>(blocks_dev) & 15) != 0)
     return fail(LNSKV_ERR_INVALID, "x and the blocks must be 16-byte aligned and x_stride a multiple of 4");
