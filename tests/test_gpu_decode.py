@@ -492,3 +492,53 @@ def test_out_of_range_kv_len_stores_nothing(gpu, dtype):
         assert np.array_equal(hp_now.k, hp.k) and np.array_equal(hp_now.v, hp.v), split
         if hp.ks is not None:
             assert np.array_equal(hp_now.ks, hp.ks) and np.array_equal(hp_now.vs, hp.vs)
+
+
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_schedules_random_batches(gpu, monkeypatch, schedule):
+    """Seeded random small batches on each schedule against the f64 oracle:
+    1-70 sequences of 0-900 tokens, rep 1/2/4/8, f16 or Q8A pages, random
+    window starts, a missing page now and then, unfused and fused (pages and
+    Q8A scales bit-exact after the fused call)."""
+    monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", schedule)
+    rng = np.random.default_rng(2024 if schedule == "stream-k" else 2025)
+    for case in range(12):
+        dtype = DTYPE_F16 if case % 2 == 0 else DTYPE_Q8A
+        rep = int(rng.choice([1, 2, 4, 8]))
+        n_kv = int(rng.choice([1, 2, 4]))
+        n_seq = int(rng.integers(1, 71))
+        lens = tuple(int(x) for x in rng.integers(0, 901, n_seq))
+        say(schedule, "random case", case, DTYPE_NAMES[dtype], "rep", rep, "n_kv", n_kv, "n_seq", n_seq)
+        pk, tables, kv_len, q = _case(gpu, dtype, 128, rep, n_kv, lens, seed=1000 + case)
+        if case % 3 == 0 and kv_len.max() > 40:
+            s_miss = int(np.argmax(kv_len))
+            tables[s_miss, 1] = NO_PAGE
+        p_start = np.array([int(rng.integers(0, L + 1)) if rng.random() < 0.4 else 0 for L in kv_len], np.int32)
+        hp, _ = host_pages(pk)
+        scale = 1.0 / np.sqrt(128)
+        ref = O.decode_f64(hp, q, tables, kv_len, p_start, scale)
+        mkv = max(int(kv_len.max()), 1)
+        out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                        max_kv_len=mkv, scale=float(scale), p_start=dev_i32(p_start, gpu), split=0)
+        sync()
+        assert rel_err(out, ref).max() < TOL[dtype], (schedule, case)
+        # fused: one more token per sequence (every table row has a spare
+        # entry; a new token on a page the row lacks is stored nowhere and
+        # skipped, by the oracle as by the library)
+        kv1 = (kv_len + 1).astype(np.int32)
+        assert (kv1 <= tables.shape[1] * 16).all()
+        k_new = rng.standard_normal((n_seq, n_kv, 128)).astype(np.float32)
+        v_new = rng.standard_normal((n_seq, n_kv, 128)).astype(np.float32)
+        O.append(hp, k_new, v_new, np.arange(n_seq, dtype=np.int32), kv1 - 1, tables)
+        ref1 = O.decode_f64(hp, q, tables, kv1, np.minimum(p_start, kv1), scale)
+        out1 = pk.append_decode(dev_f32(q, gpu), dev_f32(k_new, gpu), dev_f32(v_new, gpu), dev_i32(tables, gpu),
+                                dev_i32(kv1, gpu), n_heads=n_kv * rep, max_kv_len=max(int(kv1.max()), 1),
+                                scale=float(scale), p_start=dev_i32(np.minimum(p_start, kv1), gpu), split=0)
+        sync()
+        got, _ = host_pages(pk)
+        assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8)), (schedule, case)
+        assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8)), (schedule, case)
+        if dtype == DTYPE_Q8A:
+            assert np.array_equal(got.ks.view(np.uint32), hp.ks.view(np.uint32)), (schedule, case)
+            assert np.array_equal(got.vs.view(np.uint32), hp.vs.view(np.uint32)), (schedule, case)
+        assert rel_err(out1, ref1).max() < TOL[dtype], (schedule, case)
