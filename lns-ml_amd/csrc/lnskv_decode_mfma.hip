@@ -1156,7 +1156,8 @@ __global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_
 
 
 // ---------------------------------------------------------------------------
-// Workgroup schedule: one workgroup of NW waves per CU.  The units (sequence,
+// Workgroup schedule (small batches): G workgroups of NW waves (two per CU
+// at most; only as many as the batch can fill).  The units (sequence,
 // kv head, page) are ordered as for stream-K; workgroup g of G takes units
 // [A, B) = [g C, g C + C) with C = max(NW kWgMinPages, ceil(T / G)), and its
 // waves split that range equally (wave i: [A + i Cw, A + (i + 1) Cw)).  Each
@@ -1168,10 +1169,13 @@ __global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_
 //  - a segment inside [A, B): the output rows are written;
 //  - a segment that crosses A or B: the merged rows go to the workgroup's
 //    partial slot in the workspace (0: the segment crossing A, 1: the one
-//    crossing B), and wg_cnt[ga] (ga the segment's first workgroup) counts
-//    the workgroups done with it.  The last one merges every workgroup's
-//    rows, in workgroup order, writes the output, and sets the count back to
-//    zero for the next call.
+//    crossing B) as device-scope stores, and wg_cnt[ga] (ga the segment's
+//    first workgroup) counts the workgroups done with it once those stores
+//    have completed.  The last one merges every workgroup's rows with
+//    device-scope loads, in workgroup order, writes the output, and sets the
+//    count back to zero for the next call.  (Device-scope accesses of the
+//    rows themselves instead of agent-scope fences: each such fence writes
+//    back or invalidates the whole L2 of an XCD.)
 // No workgroup waits for another (the last to finish does the merge), and the
 // result does not depend on which one that is: the merge order is fixed.
 // ---------------------------------------------------------------------------
@@ -1614,7 +1618,7 @@ void launch_wg_rep(const DecodeArgs& a, int n_seq, int n_wg, bool q8, hipStream_
 }  // namespace
 
 int mfma_wg_count(int* n_wg) {
-  // one workgroup per CU of the current device
+  // kWgPerCu workgroups per CU of the current device (at most kWgMaxGroups)
   static std::mutex mu;
   static std::map<int, int> cache;
   int dev = 0, cus = 0;

@@ -366,8 +366,8 @@ template <bool FUSED>
 int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, bool q8, hipStream_t st);
 // Waves of the stream-K kernel resident at once on the current device.
 int mfma_sk_waves(int rep, bool fused, bool q8, int* waves);
-// Workgroup schedule of the MFMA kernels (n_seq <= kSkMaxSeqs): n_wg
-// workgroups, one per CU (mfma_wg_count); the workspace holds the header of
+// Workgroup schedule of the MFMA kernels (n_seq <= kSkMaxSeqs): up to n_wg
+// workgroups (mfma_wg_count: two per CU); the workspace holds the header of
 // kWsHeaderBytes (a count per workgroup, zero between calls) and then 2 * rep
 // partial rows per workgroup.
 template <bool FUSED>

@@ -343,7 +343,8 @@ bool mfma_path(int dtype, int d, int rep) {
 }
 
 // Q8A pages with head_dim 128 also run on the matrix cores, on the stream-K
-// schedule only (split_tokens = 0, at most kSkMaxSeqs sequences).
+// and workgroup schedules only (split_tokens = 0, at most kSkMaxSeqs
+// sequences).
 bool mfma_q8_path(int dtype, int d, int rep) {
   return dtype == LNSKV_DTYPE_Q8A && d == 128 && (rep == 1 || rep == 2 || rep == 4 || rep == 8) && !force_valu();
 }
@@ -517,14 +518,16 @@ int library_buffer(int which, size_t need, void** out, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// Static scratch of lnskv_append_decode_noalloc: the decode workspace (partial
-// rows and stream-K segment descriptors) for callers that cannot allocate
-// device memory.  Every GPU the library runs on holds its own copy until the
-// process ends.  The host name `scratch` is only a stand-in for the device
-// array: its device address is looked up once per device and used from then
-// on.  Nothing in it has to start at zero (every word a call reads was written
-// earlier in the same call); calls that overlap in time on one device race on
-// it.
+// Static scratch of lnskv_append_decode_noalloc: the decode workspace (the
+// workgroup schedule's count header, partial rows and stream-K segment
+// descriptors) for callers that cannot allocate device memory.  Every GPU the
+// library runs on holds its own copy until the process ends.  The host name
+// `scratch` is only a stand-in for the device array: its device address is
+// looked up once per device and used from then on.  The count header starts
+// at zero (static device storage is zero-initialised when the code object is
+// loaded) and every call leaves it zero; every other word a call reads was
+// written earlier in the same call.  Calls that overlap in time on one device
+// race on it.
 namespace {
 constexpr size_t kNoAllocScratchBytes = LNSKV_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
