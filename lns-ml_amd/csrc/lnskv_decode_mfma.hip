@@ -58,6 +58,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef int int4v __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 typedef unsigned int uint2v __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) short4v lds_short4v;
@@ -125,7 +126,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 template <int REP>
 struct WaveState {
+  // Q8A pages: int8 products; the B columns are REP heads x 3 limbs
+  static constexpr int kSets = (3 * REP + 15) / 16;
   half8 qb[4];      // B operand of Q.K^T per 32-dim block, column lane%16
+  // Q8A pages: q as three int8 limbs (B operand of the int8 products,
+  // 2 per set): column c = 16*set + lane%16 holds limb c/REP of head c%REP;
+  // qsc takes the limb sums of head lane%16 back to scaled scores
+  u32x4 qi[2 * kSets];
+  float qsc;
   float4v acc[8];   // P.V result: lane (g, n) holds O[row 4g+ii][16*nb + n]
   float m;          // lanes with lane%16 < REP: running max of head lane%16
   float l;          // partial softmax sum over this lane's tokens
@@ -191,16 +199,66 @@ __device__ __forceinline__ bool issue_page(const Stream& sm, uint32_t ph, int sl
   return valid;
 }
 
-// SC (Q8A pages): k and the V slot hold the int8 codes as f16; the scores of
-// tokens 4g+ii are multiplied by their K scale ksc[ii] and the weights that
-// multiply V by the V scale vsc[ii] (the sums l stay unscaled).
+// Scores of tokens 4g+ii of a page of f16 rows (log2 units), lanes n < REP.
+template <int REP>
+__device__ __forceinline__ void page_scores(const WaveState<REP>& st, const half8 (&k)[4], float (&s)[4]) {
+  float4v sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[j], st.qb[j], sacc, 0, 0, 0);
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) s[ii] = (sacc[ii] + dpp_mov<kDppRowShl + REP>(sacc[ii])) * st.qexp;
+}
+
+// The int32 x of lane n + H of this lane's 16-lane row, as a float (exact:
+// the limb sums stay below 2^24).
+template <int H>
+__device__ __forceinline__ float row_up_i32(int x) {
+  if constexpr (H == 0) return (float)x;
+  else return (float)__builtin_amdgcn_update_dpp(0, x, kDppRowShl + H, 0xF, 0xF, false);
+}
+
+// Q8A pages: scores of tokens 4g+ii from the page's int8 K codes as they
+// were loaded (kc[j]: token n, dims 32g + 16j .. +15, the A operand of the
+// int8 product) and the int8 limbs of q.  The products and their sums over
+// the 128 dims are exact integers D_L (|D_L| <= 127*127*128); the score is
+// qsc * ks * (D_0 + D_1/254 + D_2/254^2), lanes n < REP.
+template <int REP>
+__device__ __forceinline__ void page_scores_q8(const WaveState<REP>& st, const u32x4 (&kc)[2], const float4v& ksc,
+                                               float (&s)[4]) {
+  constexpr int NS = WaveState<REP>::kSets;
+  int4v d[NS];
+#pragma unroll
+  for (int S = 0; S < NS; ++S) {
+    d[S] = int4v{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      d[S] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(int4v, kc[j]),
+                                                  __builtin_bit_cast(int4v, st.qi[2 * S + j]), d[S], 0, 0, 0);
+  }
+  // limb L of head h sits in set (L*REP)/16, lane h + (L*REP)%16
+  constexpr int S1 = REP / 16, H1 = REP % 16, S2 = 2 * REP / 16, H2 = 2 * REP % 16;
+  constexpr float kInv254 = 1.0f / 254.0f;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    const float c0 = (float)d[0][ii];
+    const float c1 = row_up_i32<H1>(d[S1][ii]);
+    const float c2 = row_up_i32<H2>(d[S2][ii]);
+    s[ii] = fmaf(fmaf(c2, kInv254, c1), kInv254, c0) * (st.qsc * ksc[ii]);
+  }
+}
+
+// One page's softmax update and P.V product, given its scores s (lanes
+// n < REP, tokens 4g+ii).
+// SC (Q8A pages): the V slot holds int8 codes as f16 (finite, so masked rows
+// need no clearing: their weights are exact zeros); the weights that
+// multiply V are multiplied by the V scale vsc[ii] (the sums l stay
+// unscaled).
 template <int REP, bool FULL, bool SC = false>
-__device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& sm, const half8 (&k)[4], int slot,
-                                             int tok0, bool valid, int ta, int tb, int g, int n,
-                                             float4v ksc = float4v{1.0f, 1.0f, 1.0f, 1.0f},
-                                             float4v vsc = float4v{1.0f, 1.0f, 1.0f, 1.0f}) {
+__device__ __forceinline__ void consume_scores(WaveState<REP>& st, const Stream& sm, float (&s)[4], int slot,
+                                               int tok0, bool valid, int ta, int tb, int g, int n,
+                                               float4v vsc = float4v{1.0f, 1.0f, 1.0f, 1.0f}) {
   lds_u8* vslot = sm.vring + slot * kVSlot;
-  if constexpr (!FULL) {
+  if constexpr (!FULL && !SC) {
     // rows of masked tokens (and of a missing page) must not carry NaN bits
     // into the matrix product: zero them in the slot
 #pragma unroll
@@ -209,17 +267,6 @@ __device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& s
       if (!(valid && t >= ta && t < tb))
         *(lds_u32x4*)(vslot + (4 * j + g) * kRowBytes + 16 * n) = u32x4{0u, 0u, 0u, 0u};
     }
-  }
-
-  float4v sacc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[j], st.qb[j], sacc, 0, 0, 0);
-  float s[4];
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii) s[ii] = (sacc[ii] + dpp_mov<kDppRowShl + REP>(sacc[ii])) * st.qexp;
-  if constexpr (SC) {
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) s[ii] *= ksc[ii];
   }
   if constexpr (!FULL) {
 #pragma unroll
@@ -308,6 +355,15 @@ __device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& s
     st.acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]), st.acc[nb], 0, 0, 0);
 }
 
+// One page of f16 rows: K in registers (k), V in LDS slot `slot`.
+template <int REP, bool FULL>
+__device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& sm, const half8 (&k)[4], int slot,
+                                             int tok0, bool valid, int ta, int tb, int g, int n) {
+  float s[4];
+  page_scores<REP>(st, k, s);
+  consume_scores<REP, FULL>(st, sm, s, slot, tok0, valid, ta, tb, g, n);
+}
+
 // Loads of one piece that do not depend on the sequence's length, issued
 // oldest first in the order they are needed: the table window (64 entries
 // from table index `tbl`), q and, for a fused call, the new token's row.
@@ -319,10 +375,10 @@ struct PieceLoads {
   float2v knew, vnew;
 };
 
-// Q8: the contraction order of the Q8A kernel, where lane (g, n) holds dims
-// 32g + 8j .. 32g + 8j + 7 for product j (a contiguous 32-dim slice per lane,
-// so that a page row's codes come in two 16-byte loads); otherwise dims
-// 32j + 8g .. 32j + 8g + 7.
+// Q8: the order of the Q8A kernel, where lane (g, n) holds dims 32g .. 32g+31
+// of head n % REP (a contiguous 32-dim slice per lane, so that a page row's
+// codes come in two 16-byte loads); otherwise dims 32j + 8g .. 32j + 8g + 7
+// for product j of head n (n < REP) or n - REP (n < 2 REP).
 template <int REP, bool FUSED, bool ROPE, bool Q8 = false>
 __device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh, int tbl, PieceLoads<REP>& pl) {
   const int lane = (int)(threadIdx.x & (kWave - 1));
@@ -331,7 +387,8 @@ __device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh,
   pl.btv = e < a.bt_stride ? a.bt[(size_t)s * a.bt_stride + e] : 0u;
   pl.tbl = tbl;
   const bool qcol = n < 2 * REP;
-  const int hq = qcol ? (n < REP ? n : n - REP) : 0;  // other columns load head 0 and drop it
+  // other columns load some head and drop it
+  const int hq = Q8 ? n % REP : (qcol ? (n < REP ? n : n - REP) : 0);
   const float4v* qh = reinterpret_cast<const float4v*>(a.q + ((size_t)s * a.n_heads + (size_t)kvh * REP + hq) * kD +
                                                       (Q8 ? 32 * g : 8 * g));
 #pragma unroll
@@ -415,6 +472,57 @@ __device__ __forceinline__ void init_wave_state(const DecodeArgs& a, const Piece
     st.vnorm = 0.0f;
     st.vinv = 0.0f;
   }
+}
+
+// Q8A pages: q -> three int8 limbs per element.  y = q*scale*127/amax, amax
+// the head's largest |q*scale| (so |y| <= 127); limb 0 = rint(y), limb 1 =
+// rint(254 r), limb 2 = rint(254 (254 r - limb 1)) with r = y - limb 0, each
+// in [-127, 127]; y = limb0 + limb1/254 + limb2/254^2 to within 0.5/254^2.
+template <int REP>
+__device__ __forceinline__ void init_wave_state_q8(const DecodeArgs& a, const PieceLoads<REP>& pl,
+                                                   WaveState<REP>& st, int n) {
+  constexpr int NS = WaveState<REP>::kSets;
+  float x[32];
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    x[e] = pl.qv[e >> 2][e & 3] * a.scale_log2;
+    amax = fmaxf(amax, fabsf(x[e]));
+  }
+  amax = max_xor16(max_xor32(amax));  // over the head's 128 dims
+  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  st.qsc = amax / 127.0f;
+  uint32_t w[NS][8];
+#pragma unroll
+  for (int S = 0; S < NS; ++S)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[S][i] = 0u;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const float y = x[e] * inv;
+    const float l0 = rintf(y);
+    const float r1 = (y - l0) * 254.0f;
+    const float l1 = rintf(r1);
+    const float l2 = rintf((r1 - l1) * 254.0f);
+#pragma unroll
+    for (int S = 0; S < NS; ++S) {
+      const int c = 16 * S + n;
+      const float v = c < REP ? l0 : (c < 2 * REP ? l1 : (c < 3 * REP ? l2 : 0.0f));
+      w[S][e >> 2] |= ((uint32_t)(int)v & 0xFFu) << (8 * (e & 3));
+    }
+  }
+#pragma unroll
+  for (int S = 0; S < NS; ++S) {
+    st.qi[2 * S] = u32x4{w[S][0], w[S][1], w[S][2], w[S][3]};
+    st.qi[2 * S + 1] = u32x4{w[S][4], w[S][5], w[S][6], w[S][7]};
+  }
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) st.acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  st.m = kMInit;
+  st.l = 0.0f;
+  st.qexp = 1.0f;
+  st.vnorm = 0.0f;
+  st.vinv = 0.0f;
 }
 
 // The end of a piece: sums over the lanes, then the normalised output rows
@@ -707,14 +815,14 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
 // Q8A pages (the reference's paged type: int8 codes, one f32 scale per
 // (slot, kv head), lns_decode.metal:547-593, 611-634) on the same matrix-core
 // pipeline.  A page's K rows (16 x 128 bytes) and V rows come to registers
-// as int8 codes with 16-byte loads, plus the K and V scales of the lane's
-// token; when the page is consumed the codes become f16 exactly (K: the A
-// operand, in a contraction order that gives each lane a contiguous 32-dim
-// slice; V: written to the LDS slot in the layout the transposed reads
-// expect), and consume_page applies the scales per token: scores times the
-// K scale, softmax weights times the V scale in the P.V product (the
-// reference's q.(k8 ks) and (beta vs) v8).  A fused call quantizes the new
-// token in the wave that holds it.
+// as int8 codes with 16-byte buffer loads, plus the K and V scales of the
+// lane's token.  K codes are the A operand of v_mfma_i32_16x16x64_i8 as
+// loaded (each lane a contiguous 32-dim slice), against q split into three
+// int8 limbs: exact integer dot products, scaled back per token
+// (page_scores_q8).  V codes become f16 exactly and go to the LDS slot in the
+// layout the transposed reads expect; the softmax weights are multiplied by
+// the V scale in the P.V product (the reference's q.(k8 ks) and (beta vs)
+// v8).  A fused call quantizes the new token in the wave that holds it.
 // ---------------------------------------------------------------------------
 
 // Exact int8 -> f16 of the four signed bytes of w: the f16 with bits
@@ -735,9 +843,9 @@ __device__ __forceinline__ half8 i8x8_to_f16(uint2v w) {
   return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// One Q8A page in flight: K codes of token n, dims 32g .. 32g+31 (product j
-// takes dims 32g + 8j ..); V codes of token 8h + lane/8, dims 16 (lane%8) ..
-// +15 for load h; the K and V scales of token 4g + n%4.
+// One Q8A page in flight: K codes of token n, dims 32g .. 32g+31 (int8
+// product j takes dims 32g + 16j ..); V codes of token 8h + lane/8, dims
+// 16 (lane%8) .. +15 for load h; the K and V scales of token 4g + n%4.
 struct PageQ8 {
   u32x4 k[2];
   u32x4 v[2];
@@ -810,19 +918,31 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
   };
   asm volatile("" : "+v"(pl.btv) : : "memory");
 
-  // exactly 6 vector-memory loads; a missing page reads page 0 (masked)
+  // exactly 6 vector-memory loads; a missing page reads page 0 (masked).
+  // Buffer resources on the page's rows and scales (scalar bases, 32-bit lane
+  // offsets), each ending where this kv head's last row of the page does.
   auto issue = [&](uint32_t ph, PageQ8& pg) -> bool {
     const bool valid = ph < a.num_pages;
     const size_t pb = (size_t)(valid ? ph : 0u);
-    const uint8_t* kb = a.k_pages + pb * page_bytes + kvh_off;
-    const uint8_t* vb = a.v_pages + pb * page_bytes + kvh_off;
+    const int rows = (int)(page_bytes - kvh_off);
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.k_pages + pb * page_bytes + kvh_off), (short)0, rows, kBufferFormat);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.v_pages + pb * page_bytes + kvh_off), (short)0, rows, kBufferFormat);
+    const size_t sb = pb * kPage * (size_t)a.n_kv;
+    const int sbytes = kPage * a.n_kv * (int)sizeof(float);
+    const __amdgpu_buffer_rsrc_t ksr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.k_scales + sb), (short)0, sbytes, kBufferFormat);
+    const __amdgpu_buffer_rsrc_t vsr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.v_scales + sb), (short)0, sbytes, kBufferFormat);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) pg.k[h] = *reinterpret_cast<const u32x4*>(kb + koff + 16 * h);
+    for (int h = 0; h < 2; ++h)
+      pg.k[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)(koff + 16u * h), 0, 0));
 #pragma unroll
-    for (int h = 0; h < 2; ++h) pg.v[h] = *reinterpret_cast<const u32x4*>(vb + voff[h]);
-    const size_t sb = pb * kPage * (size_t)a.n_kv + soff;
-    pg.ks = a.k_scales[sb];
-    pg.vs = a.v_scales[sb];
+    for (int h = 0; h < 2; ++h)
+      pg.v[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, (int)voff[h], 0, 0));
+    pg.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ksr, (int)(4u * soff), 0, 0));
+    pg.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vsr, (int)(4u * soff), 0, 0));
     return valid;
   };
 
@@ -867,7 +987,7 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
   const bool attend_new = FUSED && append && pos >= ta;
 
   WaveState<REP> st;
-  init_wave_state<REP>(a, pl, st, n);
+  init_wave_state_q8<REP>(a, pl, st, n);
 
   auto step = [&](int i, PageQ8& pg, bool& valid, bool steady) {
     const int ahead = steady ? DEPTH - 1 : min(npg - 1 - i, DEPTH - 1);  // pages issued after page i
@@ -892,9 +1012,6 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
         pg.vs = new_vs;
       }
     }
-    half8 k[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) k[j] = i8x8_to_f16(uint2v{pg.k[j >> 1][2 * (j & 1)], pg.k[j >> 1][2 * (j & 1) + 1]});
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       *(lds_half8*)(vslot + vlds[h][0]) = i8x8_to_f16(uint2v{pg.v[h][0], pg.v[h][1]});
@@ -910,10 +1027,12 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
     vsc[1] = dpp_mov<0x55>(pg.vs);
     vsc[2] = dpp_mov<0xAA>(pg.vs);
     vsc[3] = dpp_mov<0xFF>(pg.vs);
+    float sc[4];
+    page_scores_q8<REP>(st, pg.k, ksc, sc);
     if (steady && valid && tok0 >= ta && tok0 + kPage <= tb)
-      consume_page<REP, true, true>(st, sm, k, 0, tok0, valid, ta, tb, g, n, ksc, vsc);
+      consume_scores<REP, true, true>(st, sm, sc, 0, tok0, valid, ta, tb, g, n, vsc);
     else
-      consume_page<REP, false, true>(st, sm, k, 0, tok0, valid, ta, tb, g, n, ksc, vsc);
+      consume_scores<REP, false, true>(st, sm, sc, 0, tok0, valid, ta, tb, g, n, vsc);
     if (steady || i + DEPTH < npg) valid = issue(phys_of(i + DEPTH), pg);
   };
   int i = 0;
