@@ -490,7 +490,9 @@ __device__ __forceinline__ void init_wave_state_q8(const DecodeArgs& a, const Pi
     amax = fmaxf(amax, fabsf(x[e]));
   }
   amax = max_xor16(max_xor32(amax));  // over the head's 128 dims
-  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  // a head whose largest |q*scale| is below 2^-100 scores zero (127 / amax
+  // could overflow; the products it drops are below 2^-93 |k|)
+  const float inv = amax >= 0x1p-100f ? 127.0f / amax : 0.0f;
   st.qsc = amax / 127.0f;
   uint32_t w[NS][8];
 #pragma unroll

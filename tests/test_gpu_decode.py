@@ -421,10 +421,11 @@ def test_schedule_chosen_by_batch_size(gpu, monkeypatch):
 
 @pytest.mark.parametrize("force_valu", ["0", "1"])
 def test_q8a_d128_both_kernels(gpu, monkeypatch, force_valu):
-    """Q8A pages with head_dim 128 run the MFMA stream-K kernel (int8 codes
-    turned into f16 exactly, K and V scales applied per token; in the fused
-    call the wave that holds the new token quantizes and stores it); LNSKV_FORCE_VALU=1
-    the generic kernel.  Both against the f64 oracle (1e-5), rep 1/2/4/8, with
+    """Q8A pages with head_dim 128 run the MFMA stream-K kernel (q.k as int8
+    products of the K codes and three int8 limbs of q, V codes turned into
+    f16 exactly, K and V scales applied per token; in the fused call the wave
+    that holds the new token quantizes and stores it); LNSKV_FORCE_VALU=1 the
+    generic kernel.  Both against the f64 oracle (1e-5), rep 1/2/4/8, with
     windows, an empty window and a missing page; pages and scales bit-exact."""
     monkeypatch.setenv("LNSKV_FORCE_VALU", force_valu)
     for rep in (1, 2, 4, 8):
@@ -456,6 +457,40 @@ def test_q8a_d128_both_kernels(gpu, monkeypatch, force_valu):
         assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8))
         assert np.array_equal(got.ks, hp.ks) and np.array_equal(got.vs, hp.vs)
         assert rel_err(out1, ref1).max() < TOL[DTYPE_Q8A], rep
+
+
+@pytest.mark.parametrize("schedule", SCHEDULES)
+@pytest.mark.parametrize("rep", [4, 8])
+def test_q8a_query_extremes(gpu, monkeypatch, rep, schedule):
+    """q rows at the edges of the int8-limb q.k of the Q8A matrix-core path
+    (limbs scaled to each head's largest |q*scale|): an all-zero head, a head
+    with one element 10^6 times the rest, a head whose largest element is
+    below 2^-100 (it scores zero), a head of large values (a sharp softmax)
+    and ordinary heads.  Against the f64 oracle (1e-5), both schedules."""
+    monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", schedule)
+    say("q8a q extremes", schedule, "rep", rep)
+    n_kv, d = 2, 128
+    lens = (40, 300, 1000, 2049)
+    pk, tables, kv_len, q = _case(gpu, DTYPE_Q8A, d, rep, n_kv, lens, seed=200 + rep)
+    rng = np.random.default_rng(rep)
+    for s_ in range(len(lens)):
+        for kvh in range(n_kv):
+            h0 = kvh * rep
+            q[s_, h0 + 0] = 0.0
+            q[s_, h0 + 1] = rng.standard_normal(d).astype(np.float32) * 3e-5
+            q[s_, h0 + 1, rng.integers(d)] = 30.0
+            q[s_, h0 + 2] = rng.standard_normal(d).astype(np.float32) * 1e-32
+            q[s_, h0 + 3] = rng.standard_normal(d).astype(np.float32) * 8.0
+    hp, _ = host_pages(pk)
+    scale = 1.0 / np.sqrt(d)
+    ref = O.decode_f64(hp, q, tables, kv_len, None, scale)
+    out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                    max_kv_len=int(kv_len.max()), scale=float(scale), split=0)
+    sync()
+    err = rel_err(out, ref)
+    assert err.max() < TOL[DTYPE_Q8A], err.max()
+    assert np.isfinite(out.cpu().numpy()).all()
+
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_Q8A])
