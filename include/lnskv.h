@@ -467,7 +467,9 @@ int lnskv_fork_sequence(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t pa
                         int32_t child, int32_t n_tok, uint32_t* copy_src, uint32_t* copy_dst,
                         int32_t* n_copy);
 /* upload_block_table (engine.rs:2992-3005): copy rows [0, n_seq) to the device
- * table (same stride), async on stream. */
+ * table (same stride), async on stream.  The runtime stages the host rows
+ * before the call returns (it does not wait for earlier work on the stream),
+ * so the host table may be changed as soon as the call returns. */
 int lnskv_block_tables_upload(const lnskv_block_tables* t, uint32_t* dst_dev,
                               lnskv_stream_t stream);
 

@@ -90,3 +90,26 @@ def test_host_tables_upload(gpu):
     bt.upload(dev.data_ptr(), torch.cuda.current_stream(gpu).cuda_stream)
     sync()
     assert np.array_equal(dev.cpu().numpy().view(np.uint32), bt.array())
+
+
+def test_host_tables_upload_snapshots(gpu):
+    """Each upload carries the table as it was during the call: the host rows
+    change right after every return, with several copies still queued behind a
+    long kernel, and each device buffer holds its own snapshot."""
+    from lnskv import BlockTables, PagePool
+    say("upload snapshots")
+    pool, bt = PagePool(4096), BlockTables(8, 64)
+    stream = torch.cuda.current_stream(gpu)
+    big = torch.ones(1 << 26, device=gpu)
+    devs, want = [], []
+    for it in range(6):
+        big.mul_(1.0001)  # work ahead of the copy on the same stream
+        for s in range(8):
+            bt.ensure_kv_page(pool, s, it * 16 * (s + 1))
+        dev = torch.zeros((8, 64), dtype=torch.int32, device=gpu)
+        bt.upload(dev.data_ptr(), stream.cuda_stream)
+        devs.append(dev)
+        want.append(bt.array().copy())
+    sync()
+    for dev, w in zip(devs, want):
+        assert np.array_equal(dev.cpu().numpy().view(np.uint32), w)
