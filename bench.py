@@ -178,7 +178,7 @@ def oproj_measure(w, runner, dev, reps: int) -> dict | None:
     n_vec = runner.n_dec
     x = torch.randn(n_vec, dim, device=dev)
     y = torch.zeros(n_vec, dim, device=dev)
-    ws = torch.empty(max(mats[0].workspace_size(n_vec), 16), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(max(mats[0].workspace_size(n_vec), 16), dtype=torch.uint8, device=dev)  # counts start at zero
     for i in range(len(mats)):
         mats[i].gemv_accumulate(x, y, ws)
     torch.cuda.synchronize()

@@ -324,9 +324,12 @@ int lnskv_q4l_prepare(const void* disk_blocks, size_t disk_bytes, int32_t rows, 
  * |x| < 65504.  Products of f16 weight codes and f16 parts of x on the matrix
  * cores, f32 sums in a fixed order: the same bits on every call.
  * workspace_dev/ws_bytes: 16-byte aligned device scratch of at least
- * lnskv_q4l_workspace_size(cols, n_vec) bytes (x split into the matrix-core
- * operands), or NULL/0 to use a buffer the library keeps per device (calls
- * that use it must not overlap in time). */
+ * lnskv_q4l_workspace_size(cols, n_vec) bytes (0 when cols < 2048: no
+ * workspace is read), or NULL/0 to use a buffer the library keeps per device.
+ * It holds the partial sums of a launch that splits each row's blocks over
+ * several workgroups, after LNSKV_WORKSPACE_HEADER_BYTES of arrival counts
+ * that must be zero before the first use (hipMemset once); every call leaves
+ * them zero.  Calls that share a workspace must not overlap in time. */
 int lnskv_q4l_workspace_size(int32_t cols, int32_t n_vec, size_t* bytes);
 int lnskv_q4l_gemv_accumulate(const void* blocks_dev, const float* x_dev, float* y_dev,
                               int32_t rows, int32_t cols, int32_t n_vec, int32_t x_stride,
@@ -383,7 +386,7 @@ int lnskv_sync(lnskv_stream_t stream);
  * The library's own device buffers (no counterpart in the reference, whose
  * Metal calls need none).  Entry points given a NULL workspace use a buffer
  * the library keeps per device: the decode workspace, the rotated RoPE rows,
- * the Q4L GEMV operands.  When one is too small a call allocates a larger one
+ * the Q4L GEMV partial sums.  When one is too small a call allocates a larger one
  * (hipMalloc, no device synchronization) and keeps the old one alive, since
  * work queued earlier may still use it; while the call's stream is being
  * captured into a graph it fails with LNSKV_ERR_WORKSPACE instead.

@@ -454,8 +454,8 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
 
 }  // namespace
 
-// Library-kept buffers per device: 0 decode workspace, 1 RoPE rows, 2 Q4L x
-// operands.  A call that finds its buffer too small allocates a larger one and
+// Library-kept buffers per device: 0 decode workspace, 1 RoPE rows, 2 Q4L
+// GEMV workspace (0 and 2 start with a zeroed count header).  A call that finds its buffer too small allocates a larger one and
 // keeps the old one alive (kernels queued earlier may still read it) until
 // lnskv_workspace_release: no call that enqueues work synchronizes the device
 // or frees memory.  While the call's stream is being captured into a graph it
@@ -470,7 +470,7 @@ std::mutex g_ws_mutex;
 std::vector<DeviceWorkspace> g_ws;       // [device * kLibraryBuffers + which]
 std::vector<std::pair<int, void*>> g_ws_retired;  // (device, pointer) outgrown, freed on release
 
-const char* kBufferName[kLibraryBuffers] = {"decode workspace", "RoPE rows", "Q4L operands"};
+const char* kBufferName[kLibraryBuffers] = {"decode workspace", "RoPE rows", "Q4L workspace"};
 
 // grows buffer `which` of device `dev` to at least `need` bytes (lock held)
 int grow_locked(int dev, int which, size_t need) {
@@ -509,8 +509,8 @@ int library_buffer(int which, size_t need, void** out, hipStream_t stream) {
                   "pass a workspace or call lnskv_workspace_reserve before capturing",
                   kBufferName[which], g_ws.size() > slot ? g_ws[slot].bytes : (size_t)0, need);
     if (int rc = grow_locked(dev, which, need)) return rc;
-    // a decode workspace starts with its counts at zero
-    if (which == 0 && hipMemsetAsync(g_ws[slot].ptr, 0, kWsHeaderBytes, stream) != hipSuccess)
+    // a decode or Q4L workspace starts with its counts at zero
+    if ((which == 0 || which == 2) && hipMemsetAsync(g_ws[slot].ptr, 0, kWsHeaderBytes, stream) != hipSuccess)
       return fail(LNSKV_ERR_HIP, "hipMemsetAsync of the workspace header failed");
   }
   *out = g_ws[slot].ptr;
@@ -893,7 +893,7 @@ int lnskv_workspace_reserve(size_t decode_bytes, size_t rope_bytes, size_t q4l_b
     const size_t slot = (size_t)dev * kLibraryBuffers + (size_t)i;
     const bool grows = g_ws.size() <= slot || g_ws[slot].bytes < want[i];
     if (int rc = grow_locked(dev, i, want[i])) return rc;
-    if (grows && i == 0 && hipMemset(g_ws[slot].ptr, 0, kWsHeaderBytes) != hipSuccess)
+    if (grows && (i == 0 || i == 2) && hipMemset(g_ws[slot].ptr, 0, kWsHeaderBytes) != hipSuccess)
       return fail(LNSKV_ERR_HIP, "hipMemset of the workspace header failed");
   }
   return LNSKV_OK;

@@ -1,9 +1,9 @@
 """GPU o_proj over Q4_L weights (lnskv_q4l_gemv_accumulate) against the
 float64 oracle: y_in + W x for every vector, within 2e-6 of
 sum_c |W[r][c] x[c]| + |y_in| (f32 sums of exact f16 x f16 products: ~cols/32
-f32 roundings of the sub-block partial sums, x split into two f16 parts to
-~2^-22; measured at most 2.4e-7 at 4096 columns.  Dropping the lo part of x
-would give ~2^-12).  Shapes cover one vector, odd counts, row counts that
+f32 roundings of the sub-block partial sums, x split into two f16 parts
+rounded toward zero, to 2^-20; measured at most 2.4e-7 at 4096 columns.
+Dropping the lo part of x would give ~2^-11).  Shapes cover one vector, odd counts, row counts that
 are not multiples of 16, padded strides, more than 64 vectors (two passes)
 and the Llama-3-8B o_proj shape at batch 32; every call gives the same bits,
 and the padding of y is not written."""
@@ -61,3 +61,40 @@ def test_q4l_gemv_accumulate(gpu, rows, cols, n_vec, xpad, ypad):
     W.gemv_accumulate(xd, yd2)
     sync()
     assert torch.equal(yd2, yd)
+
+
+def test_q4l_caller_workspace(gpu):
+    """A caller's workspace (arrival counts zeroed once) gives the bits of the
+    library's buffer, call after call and across shapes that share it (every
+    call leaves the counts zero); one byte too small is refused before any
+    launch, leaving y untouched."""
+    from lnskv import _lib
+    say("q4l caller workspace")
+    rng = np.random.default_rng(11)
+    shapes = [(4096, 4096, 32), (1000, 2048, 5), (4096, 4096, 64)]
+    mats = {}
+    need = 0
+    for rows, cols, n_vec in shapes:
+        mats[(rows, cols)] = Q4LMatrix(_disk(rng, rows, cols), rows, cols, gpu)
+        need = max(need, mats[(rows, cols)].workspace_size(n_vec))
+    assert need > _lib.WORKSPACE_HEADER_BYTES
+    ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
+    for rep in range(2):
+        for rows, cols, n_vec in shapes:
+            W = mats[(rows, cols)]
+            x = torch.from_numpy(rng.standard_normal((n_vec, cols)).astype(np.float32)).to(gpu)
+            y0 = torch.from_numpy(rng.standard_normal((n_vec, rows)).astype(np.float32)).to(gpu)
+            ya, yb = y0.clone(), y0.clone()
+            W.gemv_accumulate(x, ya, ws)
+            W.gemv_accumulate(x, yb)
+            sync()
+            assert torch.equal(ya, yb), (rep, rows, cols, n_vec)
+    assert int(ws[:_lib.WORKSPACE_HEADER_BYTES].count_nonzero()) == 0
+    W = mats[(4096, 4096)]
+    small = torch.zeros(W.workspace_size(32) - 1, dtype=torch.uint8, device=gpu)
+    x = torch.ones((32, 4096), device=gpu)
+    y = torch.zeros((32, 4096), device=gpu)
+    with pytest.raises(RuntimeError, match="workspace"):
+        W.gemv_accumulate(x, y, small)
+    sync()
+    assert int(y.count_nonzero()) == 0
