@@ -22,11 +22,12 @@
 // Per sub-block, row tile and vector tile: two products, then four f32
 // multiply-adds for the scale.
 //
-// Work split.  A workgroup of 4 waves owns 64 weight rows (4 row tiles) and a
-// range of whole blocks; wave q takes blocks q, q + 4, ... of the range.  Per
-// block a wave brings the 4 tiles' weights into its LDS by LDS DMA, then for
-// each sub-block forms the x operands once and multiplies them with all 4 row
-// tiles.  When there are too few row groups to fill the GPU, the blocks of a
+// Work split.  A workgroup of 4 waves owns 16 RT weight rows (RT row tiles:
+// 4, or 2 for up to 16 vectors) and a range of whole blocks; wave q takes
+// blocks q, q + 4, ... of the range.  Per block a wave brings the RT tiles'
+// weights into its LDS by LDS DMA (the next block's while it multiplies this
+// one), then for each sub-block forms the x operands once and multiplies them
+// with all RT row tiles.  When there are too few row groups to fill the GPU, the blocks of a
 // row are split over S workgroups: each stores its partial sums, and the last
 // of the S to finish (an arrival count per row group) adds the S partials in
 // split order to y.  All sums run in a fixed order (sub-blocks, waves, then
@@ -46,7 +47,6 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kQ4lBlockBytes = LNSKV_Q4L_DEVICE_BYTES;
 constexpr int kQ4lTileVecs = 16;   // vectors per product (A rows)
 constexpr int kQ4lMaxTiles = 4;    // vector tiles per launch (64 vectors)
-constexpr int kQ4lRowTiles = 4;    // 16-row tiles per workgroup (and per wave)
 constexpr int kQ4lWaves = 4;       // waves per workgroup (split of a range's blocks)
 constexpr int kQ4lTargetWgs = 256; // workgroups wanted per launch: one per CU
 // Buffer resource word 3 for raw dword access (DATA_FORMAT = 32-bit).
@@ -93,8 +93,12 @@ __device__ __forceinline__ void q4l_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// 16-row tiles per workgroup (and per wave) for T vector tiles: each x
+// operand a wave splits serves this many tiles; with one vector tile, two
+// (measured faster: more row groups and a shorter merge).
+constexpr int q4l_row_tiles(int T) { return T == 1 ? 2 : 4; }
 // Outputs (vector, row) one workgroup produces for T vector tiles.
-constexpr int q4l_wg_outputs(int T) { return T * kQ4lTileVecs * 16 * kQ4lRowTiles; }
+constexpr int q4l_wg_outputs(int T) { return T * kQ4lTileVecs * 16 * q4l_row_tiles(T); }
 
 struct Q4lArgs {
   const uint8_t* W;
@@ -104,7 +108,7 @@ struct Q4lArgs {
   uint32_t* cnt;  // [groups] arrival counts, zero between calls (S > 1)
   int64_t x_stride, y_stride;
   int rows, bpr, n_vec, tile0;
-  int groups;     // row groups of 64 rows
+  int groups;     // row groups of 16 q4l_row_tiles(T) rows
   int split;      // S: workgroups per row group
   int bpw;        // blocks per workgroup (the last may hold fewer)
 };
@@ -112,15 +116,16 @@ struct Q4lArgs {
 // Workgroup (row group rg, split sp) = blockIdx.x (rg fastest).
 template <int T>
 __global__ __launch_bounds__(kQ4lWaves * kWave) void q4l_gemv_acc_kernel(Q4lArgs a) {
-  constexpr int RT = kQ4lRowTiles;
+  constexpr int RT = q4l_row_tiles(T);
   constexpr int RW = 16 * RT;                                // rows per workgroup
   constexpr int E = q4l_wg_outputs(T);                       // outputs per workgroup
   constexpr int kPer = E / (kQ4lWaves * kWave);              // outputs per thread
   constexpr int kChunks = RW * 9;                            // 16-byte chunks of a weight tile
   constexpr int kDma = (kChunks + kWave - 1) / kWave;        // LDS DMA instructions per tile
-  constexpr int kTileStride = kDma * kWave * 16;             // LDS bytes per wave (padding included)
+  constexpr int kTileStride = kDma * kWave * 16;             // LDS bytes per tile slot (padding included)
   constexpr int kRedBytes = kQ4lWaves * E * 4;
-  constexpr int kLds = kQ4lWaves * kTileStride > kRedBytes ? kQ4lWaves * kTileStride : kRedBytes;
+  constexpr int kTileBytes = kQ4lWaves * 2 * kTileStride;   // two slots per wave
+  constexpr int kLds = kTileBytes > kRedBytes ? kTileBytes : kRedBytes;
   static_assert(E % (kQ4lWaves * kWave) == 0, "outputs per thread");
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
   __shared__ int merge;
@@ -154,7 +159,7 @@ __global__ __launch_bounds__(kQ4lWaves * kWave) void q4l_gemv_acc_kernel(Q4lArgs
 
   const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)a.W, (short)0, (int)((int64_t)a.rows * a.bpr * kQ4lBlockBytes), kQ4lBufferFormat);
-  lds_u8* wl = (lds_u8*)&lds[q * kTileStride];
+  lds_u8* const wslot = (lds_u8*)&lds[q * 2 * kTileStride];
   // this lane's x row for each tile (vectors past n_vec read vector 0; their
   // outputs are never stored), at its 8 columns of a sub-block
   const float* xrow[T];
@@ -166,19 +171,29 @@ __global__ __launch_bounds__(kQ4lWaves * kWave) void q4l_gemv_acc_kernel(Q4lArgs
 
   float m1;
   asm volatile("v_mov_b32 %0, -1.0" : "=v"(m1));
-  for (int b = sp * a.bpw + q; b < b_end; b += kQ4lWaves) {  // wave-uniform
-    // The RT tiles of block b (RW rows x 144 bytes, chunk 9 r + c) into LDS;
-    // lanes past the tile load its first chunk into the padding.  Rows past
-    // the matrix read row 0 of the group (their outputs are never stored).
+  // The RT tiles of block b (RW rows x 144 bytes, chunk 9 r + c) into LDS by
+  // LDS DMA; lanes past the tile load its first chunk into the padding.  Rows
+  // past the matrix read row 0 of the group (their outputs are never stored).
+  auto weight_dma = [&](int b, lds_u8* dst) {
 #pragma unroll
     for (int k = 0; k < kDma; ++k) {
       const int idx = kWave * k + lane;
       const int r = idx < kChunks ? idx / 9 : 0, c = idx < kChunks ? idx % 9 : 0;
       const int rr = row0 + r < a.rows ? row0 + r : row0;
       const int off = (int)(((int64_t)rr * a.bpr + b) * kQ4lBlockBytes + 16 * c);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, (__attribute__((address_space(3))) void*)(wl + 1024 * k), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, (__attribute__((address_space(3))) void*)(dst + 1024 * k), 16,
                                                off, 0, 0, 0);
     }
+  };
+  // Two tile slots per wave: the next block's tiles are on their way while
+  // this block is multiplied (its slot's LDS reads are all consumed by then).
+  int b = sp * a.bpw + q;
+  if (b < b_end) weight_dma(b, wslot);
+  for (int i = 0; b < b_end; b += kQ4lWaves, ++i) {  // wave-uniform
+    lds_u8* const wl = wslot + (i & 1) * kTileStride;
+    const bool more = b + kQ4lWaves < b_end;
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) weight_dma(b + kQ4lWaves, wslot + ((i + 1) & 1) * kTileStride);
     // x of sub-block j + 1 is loaded while sub-block j is multiplied
     float4v xb[2][T][2];
     auto load_x = [&](int j, float4v (&dst)[T][2]) {
@@ -190,11 +205,15 @@ __global__ __launch_bounds__(kQ4lWaves * kWave) void q4l_gemv_acc_kernel(Q4lArgs
     };
     __builtin_amdgcn_sched_barrier(0);
     load_x(0, xb[0]);
-    // The compiler does not order LDS reads after an LDS DMA: the DMAs were
-    // issued before sub-block 0's x loads and loads complete in order, so
-    // once no more than those are outstanding the tiles are in LDS.
+    // The compiler does not order LDS reads after an LDS DMA: this block's
+    // DMAs were issued before the next block's and sub-block 0's x loads, and
+    // loads complete in order, so once no more than those are outstanding the
+    // tiles are in LDS.
     __builtin_amdgcn_sched_barrier(0);
-    q4l_wait_vmcnt<T * 2>();
+    if (more)
+      q4l_wait_vmcnt<kDma + T * 2>();
+    else
+      q4l_wait_vmcnt<T * 2>();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -290,9 +309,9 @@ __global__ __launch_bounds__(kQ4lWaves * kWave) void q4l_gemv_acc_kernel(Q4lArgs
   }
 }
 
-// The launch plan: row groups, split and blocks per workgroup.
-void q4l_plan(int rows, int bpr, int* groups, int* split, int* bpw) {
-  constexpr int rw = 16 * kQ4lRowTiles;
+// The launch plan for rw rows per workgroup: row groups, split and blocks per
+// workgroup.
+void q4l_plan(int rows, int bpr, int rw, int* groups, int* split, int* bpw) {
   const int G = (rows + rw - 1) / rw;
   int S = 1;
   if (G < kQ4lTargetWgs) S = std::max(1, std::min((kQ4lTargetWgs + G - 1) / G, bpr / kQ4lWaves));
@@ -304,13 +323,14 @@ void q4l_plan(int rows, int bpr, int* groups, int* split, int* bpw) {
 
 template <int T>
 void launch_q4l(Q4lArgs a, hipStream_t st) {
-  q4l_plan(a.rows, a.bpr, &a.groups, &a.split, &a.bpw);
+  q4l_plan(a.rows, a.bpr, 16 * q4l_row_tiles(T), &a.groups, &a.split, &a.bpw);
   q4l_gemv_acc_kernel<T><<<(unsigned)(a.groups * a.split), kQ4lWaves * kWave, 0, st>>>(a);
 }
 
 // Workspace: the arrival counts (LNSKV_WORKSPACE_HEADER_BYTES, zero between
 // calls) and the partial sums of a split launch.  A split needs fewer than
-// kQ4lTargetWgs row groups, so S * groups < 2 kQ4lTargetWgs whatever the rows;
+// kQ4lTargetWgs row groups, so S * groups < 2 kQ4lTargetWgs whatever the rows
+// (q4l_wg_outputs grows with T, so the launch with the most tiles is largest);
 // with fewer than 2 kQ4lWaves blocks a row there is no split and no workspace.
 size_t q4l_ws_bytes(int cols, int n_vec) {
   const int bpr = cols / 256;

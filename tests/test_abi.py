@@ -99,11 +99,12 @@ def test_workspace_size_formula():
 def test_q4l_workspace_size_formula():
     """The Q4L GEMV workspace: none below 8 blocks a row (no split); else the
     arrival counts, then partial sums for fewer than 2 x 256 workgroups of
-    64 rows x 16 vectors per tile (up to 4 tiles a launch)."""
+    64 rows (32 rows with one tile) x 16 vectors per tile (up to 4 tiles a
+    launch)."""
     lib = _lib.lib()
     out = C.c_size_t()
     for cols, n_vec, want in [(256, 1, 0), (1792, 64, 0),
-                              (2048, 1, 1 * 1024), (4096, 16, 1 * 1024), (4096, 17, 2 * 1024),
+                              (2048, 1, 512), (4096, 16, 512), (4096, 17, 2 * 1024),
                               (4096, 32, 2 * 1024), (4096, 64, 4 * 1024), (4096, 300, 4 * 1024)]:
         assert lib.lnskv_q4l_workspace_size(cols, n_vec, C.byref(out)) == 0
         assert out.value == (0 if want == 0 else _lib.WORKSPACE_HEADER_BYTES + 2 * 256 * want * 4), (cols, n_vec)
