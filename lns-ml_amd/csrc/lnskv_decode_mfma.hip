@@ -1498,11 +1498,12 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
   // (workgroup ga's from its slot 1, the others' from slot 0) in workgroup
   // order, with device-scope loads.  Wave v takes query head v % REP and the
   // rows j with j % HP == v / REP (HP = NW / REP parts per head), every load
-  // of up to 16 rows in flight before any is used; wave h < REP then merges
+  // of up to 32 rows in flight before any is used (one round of loads for the
+  // 32 workgroups that share a 256-page segment); wave h < REP then merges
   // the HP parts of head h through LDS, in part order.
   constexpr int HP = NW >= REP ? NW / REP : 1;  // parts per head
   constexpr int HW = NW >= REP ? 1 : REP / NW;  // heads per wave
-  constexpr int kChunk = 16;
+  constexpr int kChunk = 32;
   lds_f32* prow = (lds_f32*)part_;  // free again: row v of wave v, acc then m, l
 #pragma unroll
   for (int side = 0; side < 2; ++side) {
