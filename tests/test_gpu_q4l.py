@@ -98,3 +98,36 @@ def test_q4l_caller_workspace(gpu):
         W.gemv_accumulate(x, y, small)
     sync()
     assert int(y.count_nonzero()) == 0
+
+
+def test_q4l_graph_replay_library_buffer(gpu):
+    """lnskv_workspace_reserve grows the library's Q4L buffer (its arrival
+    counts zeroed) before a capture; the captured y = y0; y += W x (a split
+    launch, 4096 x 4096 with 32 vectors) then replays with unrelated eager
+    work between the replays, each replay equal to the eager call bit for
+    bit, so the counts are back at zero after every replay."""
+    from lnskv._lib import check, lib
+    say("q4l graph replay")
+    rng = np.random.default_rng(21)
+    rows, cols, n_vec = 4096, 4096, 32
+    W = Q4LMatrix(_disk(rng, rows, cols), rows, cols, gpu)
+    check(lib().lnskv_workspace_reserve(0, 0, W.workspace_size(n_vec)))
+    x = torch.from_numpy(rng.standard_normal((n_vec, cols)).astype(np.float32)).to(gpu)
+    y0 = torch.from_numpy(rng.standard_normal((n_vec, rows)).astype(np.float32)).to(gpu)
+    want = y0.clone()
+    W.gemv_accumulate(x, want)
+    y = torch.empty_like(y0)
+    sync()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y.copy_(y0)
+        W.gemv_accumulate(x, y)
+    torch.cuda.synchronize()
+    scratch = torch.randn(1 << 20, device=gpu)
+    for rep in range(4):
+        y.zero_()
+        g.replay()
+        got = y.clone()
+        scratch.mul_(1.0001)  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), rep
