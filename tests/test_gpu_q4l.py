@@ -4,9 +4,10 @@ sum_c |W[r][c] x[c]| + |y_in| (f32 sums of exact f16 x f16 products: ~cols/32
 f32 roundings of the sub-block partial sums, x split into two f16 parts
 rounded toward zero, to 2^-20; measured at most 2.4e-7 at 4096 columns.
 Dropping the lo part of x would give ~2^-11).  Shapes cover one vector, odd counts, row counts that
-are not multiples of 16, padded strides, more than 64 vectors (two passes)
-and the Llama-3-8B o_proj shape at batch 32; every call gives the same bits,
-and the padding of y is not written."""
+are not multiples of 16, padded strides, more than 64 vectors (two passes),
+the Llama-3-8B o_proj shape at batch 32 and wider rows whose waves take two
+blocks each (the next block's weights arriving during the products); every
+call gives the same bits, and the padding of y is not written."""
 import numpy as np
 import pytest
 import torch
@@ -34,6 +35,8 @@ def _disk(rng, rows, cols):
     (100, 2048, 13, 8, 5),
     (48, 512, 70, 0, 0),
     (4096, 4096, 32, 0, 0),
+    (2048, 8192, 3, 0, 0),    # split launch, two blocks per wave (one vector tile)
+    (4096, 8192, 24, 4, 0),   # split launch, two blocks per wave (two vector tiles)
 ])
 def test_q4l_gemv_accumulate(gpu, rows, cols, n_vec, xpad, ypad):
     say("q4l gemv", rows, cols, n_vec, xpad, ypad)
