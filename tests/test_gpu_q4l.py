@@ -37,6 +37,7 @@ def _disk(rng, rows, cols):
     (4096, 4096, 32, 0, 0),
     (2048, 8192, 3, 0, 0),    # split launch, two blocks per wave (one vector tile)
     (4096, 8192, 24, 4, 0),   # split launch, two blocks per wave (two vector tiles)
+    (512, 4096, 70, 0, 3),    # two split launches (4 tiles, then 1) sharing the arrival counts
 ])
 def test_q4l_gemv_accumulate(gpu, rows, cols, n_vec, xpad, ypad):
     say("q4l gemv", rows, cols, n_vec, xpad, ypad)
