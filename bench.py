@@ -561,7 +561,7 @@ def main():
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
               f"(asked for --gpus {args.gpus}); the paged KV path shards by sequence "
-              f"or kv head with no exchange, see DESIGN.md", file=sys.stderr)
+              f"or kv head, one process per GPU with no exchange between them", file=sys.stderr)
         sys.exit(2)
     import torch
 
