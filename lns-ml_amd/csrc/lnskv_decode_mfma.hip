@@ -1829,7 +1829,7 @@ namespace {
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 constexpr int kPfSlot = 4 * kVSlot;  // K and V of two pages
-constexpr int kPfDepth = 3;          // ring slots: one pair consumed, two in flight
+constexpr int kPfDepth = 6;          // ring slots: two pairs consumed per barrier, two in flight
 
 // Two query heads per wave and eight waves per workgroup (two per SIMD, 256
 // VGPRs each): measured against four heads with four waves (one per SIMD,
@@ -2153,7 +2153,7 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
   }
   lds_u8* ring = (lds_u8*)ring_;
 
-  // pair i -> ring slot i % 3; validity bits of the slot's two pages
+  // pair i -> ring slot i % kPfDepth; validity bits of the slot's two pages
   uint32_t vbits = 0;
   auto issue = [&](int i) {
     const int sl = i % kPfDepth;
@@ -2163,8 +2163,9 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     vbits = (vbits & ~(3u << (2 * sl))) | (bits << (2 * sl));
     pf_issue<RPW>(a, pl, page_bytes, kvh_off, ring + sl * kPfSlot, ph0, ph1, w);
   };
-  if (npairs > 0) issue(0);
-  if (npairs > 1) issue(1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (i < npairs) issue(i);
 
   // q -> B operands: per query and head, scale by 2^-E (E from max |q *
   // scale|) so that hi and lo stay in f16 range; scores are scaled back by 2^E
@@ -2202,13 +2203,21 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     for (int nb = 0; nb < 8; ++nb) acc[hh][nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  for (int i = 0; i < npairs; ++i) {
-    if (i + 1 < npairs)
-      wait_vmcnt<RPW>();  // pair i landed; pair i + 1 stays in flight
+  // Two pairs per barrier: pairs i and i + 1 are consumed while i + 2 and
+  // i + 3 are in flight and i + 4, i + 5 are issued into the slots of
+  // i - 2, i - 1 (every wave consumed those before this barrier).
+  for (int i0 = 0; i0 < npairs; i0 += 2) {
+    const int later = min(npairs - (i0 + 2), 2);  // pairs issued after i0 + 1, still in flight
+    if (later == 2)
+      wait_vmcnt<2 * RPW>();  // pairs i0, i0 + 1 landed
+    else if (later == 1)
+      wait_vmcnt<RPW>();
     else
       wait_vmcnt<0>();
-    pf_barrier();  // every wave's quarter of pair i landed; pair i - 1 is consumed
-    if (i + 2 < npairs) issue(i + 2);  // into pair i - 1's slot
+    pf_barrier();  // every wave's quarters of pairs i0, i0 + 1 landed; i0 - 2, i0 - 1 are consumed
+    if (i0 + 4 < npairs) issue(i0 + 4);
+    if (i0 + 5 < npairs) issue(i0 + 5);
+    for (int i = i0; i < min(i0 + 2, npairs); ++i) {
     if (active) {
       const int sl = i % kPfDepth;
       lds_u8* sp = ring + sl * kPfSlot;
@@ -2221,6 +2230,7 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
         pf_consume<HW, 1>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n);
       else
         pf_consume<HW, 2>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n);
+    }
     }
   }
   if (!active) return;
