@@ -1829,7 +1829,8 @@ namespace {
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 constexpr int kPfSlot = 4 * kVSlot;  // K and V of two pages
-constexpr int kPfDepth = 6;          // ring slots: two pairs consumed per barrier, two in flight
+constexpr int kPfBatch = 2;                 // pairs consumed per barrier (1 to 3)
+constexpr int kPfDepth = 3 * kPfBatch;      // ring slots: a batch consumed, a batch in flight, a batch issued
 
 // Two query heads per wave and eight waves per workgroup (two per SIMD, 256
 // VGPRs each): measured against four heads with four waves (one per SIMD,
@@ -2164,7 +2165,7 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     pf_issue<RPW>(a, pl, page_bytes, kvh_off, ring + sl * kPfSlot, ph0, ph1, w);
   };
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2 * kPfBatch; ++i)
     if (i < npairs) issue(i);
 
   // q -> B operands: per query and head, scale by 2^-E (E from max |q *
@@ -2203,21 +2204,26 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     for (int nb = 0; nb < 8; ++nb) acc[hh][nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  // Two pairs per barrier: pairs i and i + 1 are consumed while i + 2 and
-  // i + 3 are in flight and i + 4, i + 5 are issued into the slots of
-  // i - 2, i - 1 (every wave consumed those before this barrier).
-  for (int i0 = 0; i0 < npairs; i0 += 2) {
-    const int later = min(npairs - (i0 + 2), 2);  // pairs issued after i0 + 1, still in flight
+  // kPfBatch pairs per barrier: pairs [i0, i0 + B) are consumed while the
+  // next B are in flight and the B after those are issued into the slots of
+  // [i0 - B, i0) (every wave consumed those before this barrier).
+  for (int i0 = 0; i0 < npairs; i0 += kPfBatch) {
+    // the pairs issued after this batch, which may stay in flight
+    const int later = min(max(npairs - (i0 + kPfBatch), 0), kPfBatch);
+    if constexpr (kPfBatch >= 3) {
+      if (later == 3) wait_vmcnt<3 * RPW>();
+    }
     if (later == 2)
-      wait_vmcnt<2 * RPW>();  // pairs i0, i0 + 1 landed
+      wait_vmcnt<2 * RPW>();
     else if (later == 1)
       wait_vmcnt<RPW>();
-    else
+    else if (later == 0)
       wait_vmcnt<0>();
-    pf_barrier();  // every wave's quarters of pairs i0, i0 + 1 landed; i0 - 2, i0 - 1 are consumed
-    if (i0 + 4 < npairs) issue(i0 + 4);
-    if (i0 + 5 < npairs) issue(i0 + 5);
-    for (int i = i0; i < min(i0 + 2, npairs); ++i) {
+    pf_barrier();  // every wave's quarters of this batch landed; the previous batch is consumed
+#pragma unroll
+    for (int k = 0; k < kPfBatch; ++k)
+      if (i0 + 2 * kPfBatch + k < npairs) issue(i0 + 2 * kPfBatch + k);
+    for (int i = i0; i < min(i0 + kPfBatch, npairs); ++i) {
     if (active) {
       const int sl = i % kPfDepth;
       lds_u8* sp = ring + sl * kPfSlot;
