@@ -109,12 +109,31 @@ def test_library_prepare_matches_oracle():
     assert rc == _lib.ERR_INVALID
 
 
-@pytest.mark.parametrize("bad", ["cols", "null"])
+@pytest.mark.parametrize("bad", ["cols", "null", "x_stride", "y_stride", "x_align", "ws_small", "ws_align"])
 def test_gemv_rejects_bad_arguments(bad):
+    """Every check runs before anything touches the GPU (the pointers here
+    are never dereferenced): the call returns the status and leaves nothing
+    queued."""
     lib = _lib.lib()
+    f = lib.lnskv_q4l_gemv_accumulate
+    # blocks, x, y, rows, cols, n_vec, x_stride, y_stride, ws, ws_bytes, stream
     if bad == "cols":
-        rc = lib.lnskv_q4l_gemv_accumulate(16, 16, 16, 4, 300, 1, 300, 4, None, 0, None)
-        assert rc == _lib.ERR_UNSUPPORTED and "256" in _lib.last_error()
+        assert f(16, 16, 16, 4, 300, 1, 300, 4, None, 0, None) == _lib.ERR_UNSUPPORTED
+        assert "256" in _lib.last_error()
+    elif bad == "null":
+        assert f(None, 16, 16, 4, 256, 1, 256, 4, None, 0, None) == _lib.ERR_INVALID
+    elif bad == "x_stride":
+        assert f(16, 16, 16, 4, 512, 1, 256, 4, None, 0, None) == _lib.ERR_INVALID
+    elif bad == "y_stride":
+        assert f(16, 16, 16, 64, 256, 1, 256, 32, None, 0, None) == _lib.ERR_INVALID
+    elif bad == "x_align":
+        assert f(16, 20, 16, 4, 256, 1, 256, 4, None, 0, None) == _lib.ERR_INVALID
     else:
-        rc = lib.lnskv_q4l_gemv_accumulate(None, 16, 16, 4, 256, 1, 256, 4, None, 0, None)
-        assert rc == _lib.ERR_INVALID
+        # 4096 columns split a row's blocks over workgroups: a workspace is read
+        need = C.c_size_t()
+        assert lib.lnskv_q4l_workspace_size(4096, 32, C.byref(need)) == 0 and need.value > 0
+        if bad == "ws_small":
+            assert f(16, 16, 16, 64, 4096, 32, 4096, 64, 32, need.value - 1, None) == _lib.ERR_WORKSPACE
+        else:
+            assert f(16, 16, 16, 64, 4096, 32, 4096, 64, 24, need.value, None) == _lib.ERR_WORKSPACE
+        assert "workspace" in _lib.last_error()
