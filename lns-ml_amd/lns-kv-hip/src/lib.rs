@@ -13,7 +13,11 @@
 //!   (`engine.rs:20-44, 65-66, 2958-3013`), host code in Rust
 //!   ([`paging`]), with the sliding-window exhaustion fixed;
 //! - [`KvLayer::append_decode`] is the batched serving form (one call per
-//!   layer for every decoding sequence).
+//!   layer for every decoding sequence);
+//! - [`Q4lMatrix`] is a Q4_L weight matrix on the device (`prepare_tensor`,
+//!   `lns-metal/src/lib.rs:1255-1320`) and [`Q4lMatrix::gemv_accumulate`] the
+//!   o_proj after the attention (`gemv_accumulate_multirow_enc`,
+//!   `engine.rs:3433-3446`) for every decoding sequence in one call.
 //!
 //! Errors are the reference's `Result<(), String>`; library failures carry
 //! liblnskv's message (for pool exhaustion, the engine's own text).  Device
@@ -358,5 +362,77 @@ impl KvPaging {
     pub fn reset(&mut self) {
         self.pool.reset();
         self.table = BlockTable::new(self.table.max_pages());
+    }
+}
+
+/// One Q4_L weight matrix on the device: the disk super-blocks
+/// (`LNSKV_Q4L_DISK_BYTES` per 256 weights, row-major) repacked by
+/// `lnskv_q4l_prepare` into device blocks and uploaded once, as
+/// `prepare_tensor(.., QuantType::Q4L)` does (`lns-metal/src/lib.rs:1255-1320`),
+/// plus the GEMV's workspace.
+pub struct Q4lMatrix {
+    pub rows: usize,
+    pub cols: usize,
+    blocks: DeviceBuffer<u8>,
+    workspace: DeviceBuffer<u8>,
+    ws_vectors: usize,
+}
+
+impl Q4lMatrix {
+    pub fn prepare(disk: &[u8], rows: usize, cols: usize) -> Result<Self, String> {
+        let n_blocks = rows * ((cols + 255) / 256);
+        let mut host = vec![0u8; n_blocks * sys::LNSKV_Q4L_DEVICE_BYTES];
+        check(unsafe {
+            sys::lnskv_q4l_prepare(
+                disk.as_ptr() as *const c_void,
+                disk.len(),
+                rows as i32,
+                cols as i32,
+                host.as_mut_ptr() as *mut c_void,
+            )
+        })?;
+        Ok(Self {
+            rows,
+            cols,
+            blocks: DeviceBuffer::from_slice(&host)?,
+            workspace: DeviceBuffer::new(0)?,
+            ws_vectors: 0,
+        })
+    }
+
+    /// `gemv_accumulate_multirow_enc(enc, o_proj, attn_out, x, dim, attn_dim)`
+    /// (`engine.rs:3433-3446`) for `n_vec` sequences at once: x[v] += W
+    /// attn_out[v], with attn_out `[n_vec][cols]` and x `[n_vec][rows]` f32 on
+    /// the device.  The workspace grows to the largest `n_vec` seen; its
+    /// arrival counts start at zero and every call leaves them zero, so calls
+    /// on one matrix must not overlap in time.
+    pub fn gemv_accumulate(
+        &mut self,
+        attn_out_dev: *const f32,
+        x_dev: *mut f32,
+        n_vec: usize,
+        stream: HipStream,
+    ) -> Result<(), String> {
+        if n_vec > self.ws_vectors {
+            let mut bytes: usize = 0;
+            check(unsafe { sys::lnskv_q4l_workspace_size(self.cols as i32, n_vec as i32, &mut bytes) })?;
+            self.workspace = DeviceBuffer::zeroed(bytes.max(16))?;
+            self.ws_vectors = n_vec;
+        }
+        check(unsafe {
+            sys::lnskv_q4l_gemv_accumulate(
+                self.blocks.as_ptr() as *const c_void,
+                attn_out_dev,
+                x_dev,
+                self.rows as i32,
+                self.cols as i32,
+                n_vec as i32,
+                self.cols as i32,
+                self.rows as i32,
+                self.workspace.as_mut_ptr() as *mut c_void,
+                self.workspace.len(),
+                stream,
+            )
+        })
     }
 }

@@ -143,6 +143,20 @@ def test_safe_layer_calls_only_declared_functions():
                          "n_kv_heads", "p_start", "stream"], fn
 
 
+def test_q4l_wrapper_follows_the_engine_call():
+    """Q4lMatrix::gemv_accumulate takes gemv_accumulate_multirow_enc's
+    operands in its order (attn_out, then the x it adds to, engine.rs:
+    3433-3446) and passes the header's dense strides; its workspace is zeroed
+    before first use (the arrival counts)."""
+    lib_rs = open(os.path.join(CRATE, "src", "lib.rs")).read()
+    sig = re.search(r"pub fn gemv_accumulate\(\s*&mut self,(.*?)\)\s*->", lib_rs, flags=re.S).group(1)
+    names = [a.split(":")[0].strip() for a in sig.split(",") if a.strip()]
+    assert names == ["attn_out_dev", "x_dev", "n_vec", "stream"]
+    body = lib_rs.split("pub fn gemv_accumulate(", 1)[1]
+    assert "DeviceBuffer::zeroed" in body and "sys::lnskv_q4l_workspace_size" in body
+    assert "sys::lnskv_q4l_prepare" in lib_rs.split("pub fn prepare(", 1)[1]
+
+
 def test_crate_builds_offline_and_links_the_library():
     toml = open(os.path.join(CRATE, "Cargo.toml")).read()
     deps = toml.split("[dependencies]", 1)[1]
