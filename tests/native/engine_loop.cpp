@@ -7,12 +7,20 @@
 //   2960-2990 with the exhaustion fixed), lnskv_block_tables_upload
 //   (upload_block_table, engine.rs:2992-3005), lnskv_dispatch_attention_paged
 //   (dispatch_attention_paged_q8a, lns-metal/src/lib.rs:1046-1094) with
-//   p_start = lnskv_kv_p_start(pos, 40) (engine.rs:3007-3013).
+//   p_start = lnskv_kv_p_start(pos, 40) (engine.rs:3007-3013), then the
+//   o_proj: lnskv_q4l_gemv_accumulate adds W_o attn_out to the residual x
+//   (gemv_accumulate_multirow_enc, engine.rs:3433-3446) over a 4096 x 4096
+//   Q4_L matrix repacked once by lnskv_q4l_prepare (prepare_tensor,
+//   lns-metal/src/lib.rs:1255-1320), its workspace zeroed once.
 // Checked against a host restatement: the stored codes and scales bit for bit
 // (lns_decode.metal:547-593: absmax / 127, round half away from zero, clamp
-// 127; read back with lnskv_gather) and every output row within 1e-5 of an
-// f64 softmax over the dequantized window.  Prints one line and exits 0 when
-// every check holds, 1 otherwise.
+// 127; read back with lnskv_gather), every output row within 1e-5 of an f64
+// softmax over the dequantized window, and at every tenth position W_o times
+// that position's output within 2e-6 of sum |w x| of an f64 product over the
+// decoded weights (the weight of nibble i of a device block: sign bit 3,
+// magnitude m = bits 0-2, zero for m = 0, else the sub-block's f16 scale times
+// 2^(m - 5)).  Prints one line and exits 0 when every check holds, 1
+// otherwise.
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
@@ -26,6 +34,9 @@
 namespace {
 
 constexpr int kHq = 32, kHkv = 8, kD = 128, kWindow = 40, kPositions = 150;
+constexpr int kDim = kHq * kD;         // W_o: kDim x kDim (model dim = Hq * head_dim)
+constexpr int kBpr = kDim / 256;       // Q4_L blocks per row
+constexpr int kOprojCheckEvery = 10;
 
 // SplitMix64 -> values in [-2, 2)
 struct Rng {
@@ -50,6 +61,31 @@ void quantize(const float* x, int8_t* codes, float* scale) {
     codes[i] = (int8_t)std::max(-127.0f, std::min(127.0f, r));
   }
   *scale = sc;
+}
+
+// f16 bits -> float (normal numbers, subnormals, zero)
+float half_to_float(uint16_t h) {
+  const int e = (h >> 10) & 31, m = h & 1023;
+  const float v = e == 0 ? std::ldexp((float)m, -24) : std::ldexp((float)(m | 1024), e - 25);
+  return (h >> 15) ? -v : v;
+}
+
+// The weights of a rows x cols device-block matrix, [row][col].
+std::vector<float> decode_q4l(const std::vector<uint8_t>& blocks, int rows, int cols) {
+  const int bpr = cols / 256;
+  std::vector<float> w((size_t)rows * cols);
+  for (int r = 0; r < rows; ++r)
+    for (int b = 0; b < bpr; ++b) {
+      const uint8_t* blk = &blocks[((size_t)r * bpr + b) * LNSKV_Q4L_DEVICE_BYTES];
+      for (int i = 0; i < 256; ++i) {
+        const uint8_t byte = blk[16 + i / 2];
+        const int nib = (i & 1) ? byte >> 4 : byte & 15, m = nib & 7;
+        const float sc = half_to_float((uint16_t)(blk[2 * (i / 32)] | (blk[2 * (i / 32) + 1] << 8)));
+        const float mag = m == 0 ? 0.0f : sc * std::ldexp(1.0f, m - 5);
+        w[(size_t)r * cols + b * 256 + i] = (nib & 8) ? -mag : mag;
+      }
+    }
+  return w;
 }
 
 bool ok(int rc, const char* what) {
@@ -96,6 +132,37 @@ int run() {
     std::printf("engine_loop FAILED: hipMalloc\n");
     return 1;
   }
+
+  // o_proj weights: random disk super-blocks (scale_global a positive f16 in
+  // [2^-12, 2^-2), 8 local-scale nibbles, 256 weight nibbles), repacked once
+  Rng wrng{11};
+  std::vector<uint8_t> disk((size_t)kDim * kBpr * LNSKV_Q4L_DISK_BYTES);
+  for (size_t blk = 0; blk < (size_t)kDim * kBpr; ++blk) {
+    uint8_t* d = &disk[blk * LNSKV_Q4L_DISK_BYTES];
+    for (int i = 0; i < LNSKV_Q4L_DISK_BYTES; ++i) d[i] = (uint8_t)((wrng.next() + 2.0f) * 64.0f);
+    const uint16_t g = (uint16_t)(((3 + (int)((wrng.next() + 2.0f) * 2.5f)) << 10) | (d[1] & 3) << 8 | d[0]);
+    d[0] = (uint8_t)(g & 255);
+    d[1] = (uint8_t)(g >> 8);
+  }
+  std::vector<uint8_t> wblocks((size_t)kDim * kBpr * LNSKV_Q4L_DEVICE_BYTES);
+  if (!ok(lnskv_q4l_prepare(disk.data(), disk.size(), kDim, kDim, wblocks.data()), "lnskv_q4l_prepare")) return 1;
+  const std::vector<float> W = decode_q4l(wblocks, kDim, kDim);
+  size_t ws_bytes = 0;
+  if (!ok(lnskv_q4l_workspace_size(kDim, 1, &ws_bytes), "lnskv_q4l_workspace_size")) return 1;
+  uint8_t* w_dev = dev_alloc<uint8_t>(wblocks.size());
+  uint8_t* ws_dev = dev_alloc<uint8_t>(std::max<size_t>(ws_bytes, 16));
+  float* x_dev = dev_alloc<float>(kDim);
+  float* y_dev = dev_alloc<float>(kDim);
+  if (!w_dev || !ws_dev || !x_dev || !y_dev) {
+    std::printf("engine_loop FAILED: hipMalloc\n");
+    return 1;
+  }
+  if (!hip_ok(hipMemcpy(w_dev, wblocks.data(), wblocks.size(), hipMemcpyHostToDevice), "W_o upload") ||
+      !hip_ok(hipMemset(ws_dev, 0, std::max<size_t>(ws_bytes, 16)), "workspace zero") ||
+      !hip_ok(hipMemset(x_dev, 0, kDim * 4), "x zero"))
+    return 1;
+  std::vector<float> y(kDim);
+  double worst_oproj = 0.0;
 
   // every position's dequantized K and V, [pos][kvh][d]
   std::vector<double> kq((size_t)kPositions * kHkv * kD), vq((size_t)kPositions * kHkv * kD);
@@ -172,6 +239,34 @@ int run() {
         return 1;
       }
     }
+    // o_proj: the residual x += W_o out, as the engine's step does; every
+    // tenth position also W_o out alone, checked on the host
+    if (!ok(lnskv_q4l_gemv_accumulate(w_dev, out_dev, x_dev, kDim, kDim, 1, kDim, kDim, ws_dev, ws_bytes, nullptr),
+            "lnskv_q4l_gemv_accumulate"))
+      return 1;
+    if (pos % kOprojCheckEvery == 0) {
+      if (!hip_ok(hipMemset(y_dev, 0, kDim * 4), "y zero") ||
+          !ok(lnskv_q4l_gemv_accumulate(w_dev, out_dev, y_dev, kDim, kDim, 1, kDim, kDim, ws_dev, ws_bytes,
+                                        nullptr),
+              "lnskv_q4l_gemv_accumulate") ||
+          !ok(lnskv_sync(nullptr), "lnskv_sync") ||
+          !hip_ok(hipMemcpy(y.data(), y_dev, kDim * 4, hipMemcpyDeviceToHost), "y"))
+        return 1;
+      for (int r = 0; r < kDim; ++r) {
+        double ref = 0.0, mag = 0.0;
+        for (int c2 = 0; c2 < kDim; ++c2) {
+          const double p = (double)W[(size_t)r * kDim + c2] * out[c2];
+          ref += p;
+          mag += std::fabs(p);
+        }
+        const double err = std::fabs((double)y[r] - ref) / (mag + 1e-30);
+        worst_oproj = std::max(worst_oproj, err);
+        if (err > 2e-6) {
+          std::printf("engine_loop FAILED: o_proj at pos %d row %d: error %.3e of sum |w x|\n", pos, r, err);
+          return 1;
+        }
+      }
+    }
     // the window's pages only, never more than lnskv_window_pages(window)
     const uint32_t* row = lnskv_block_tables_host(bt);
     const int live = (int)std::count_if(row, row + max_pages, [](uint32_t p) { return p != LNSKV_NO_PAGE; });
@@ -180,12 +275,14 @@ int run() {
       return 1;
     }
   }
-  std::printf("engine_loop ok: %d positions, window %d on a %u-page pool, max row error %.3e\n", kPositions,
-              kWindow, c.num_pages, worst);
+  if (!ok(lnskv_sync(nullptr), "lnskv_sync")) return 1;
+  std::printf("engine_loop ok: %d positions, window %d on a %u-page pool, max row error %.3e, o_proj max error "
+              "%.3e of sum |w x|\n", kPositions, kWindow, c.num_pages, worst, worst_oproj);
   lnskv_block_tables_destroy(bt);
   lnskv_page_pool_destroy(pool);
   for (void* p : {(void*)table_dev, (void*)q_dev, (void*)k_dev, (void*)v_dev, (void*)out_dev, (void*)kc_dev,
-                  (void*)vc_dev, (void*)ks_dev, (void*)vs_dev})
+                  (void*)vc_dev, (void*)ks_dev, (void*)vs_dev, (void*)w_dev, (void*)ws_dev, (void*)x_dev,
+                  (void*)y_dev})
     (void)hipFree(p);
   return ok(lnskv_pages_free(&c), "lnskv_pages_free") ? 0 : 1;
 }
