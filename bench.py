@@ -94,6 +94,43 @@ def copy_ceiling(dev, mb: int, reps: int = 20) -> dict:
     return {"bytes_per_copy": 2 * n * 4, "gb_per_s": round(2 * n * 4 / dt / 1e9, 1)}
 
 
+def read_ceiling(dev, mib: int = 1024, reps: int = 10) -> dict:
+    """Same-run plain read ceiling: lnskv_read_stream over one buffer of `mib`
+    MiB (1 GiB by default, four times the 256 MB last-level cache, so every
+    launch reads from HBM), front to back with 16-byte loads; the best of a
+    sweep of loads in flight per thread (4, 8, 16) and workgroups per CU
+    (2, 4, 8), each timed with HIP events over `reps` launches."""
+    import ctypes as C
+
+    import torch
+
+    from lnskv._lib import check, lib
+
+    nbytes = mib << 20
+    buf = torch.empty(nbytes // 4, dtype=torch.int32, device=dev).random_()
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    sweep = {}
+    for u in (4, 8, 16):
+        for bpc in (2, 4, 8):
+            def launch():
+                check(lib().lnskv_read_stream(buf.data_ptr(), nbytes, u, bpc, sink.data_ptr(), stream))
+            for _ in range(2):
+                launch()
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps):
+                launch()
+            e.record()
+            torch.cuda.synchronize()
+            dt = s.elapsed_time(e) / 1e3 / reps
+            sweep[f"{u}x{bpc}"] = round(nbytes / dt / 1e9, 1)
+    best = max(sweep, key=sweep.get)
+    return {"bytes_per_launch": nbytes, "gb_per_s": sweep[best], "best": best,
+            "sweep_gbs": sweep, "note": "loads in flight per thread x workgroups of 256 threads per CU"}
+
+
 def pattern_ceiling(w, runner, dev, reps: int) -> dict | None:
     """Load ceiling of the step's decode page pattern, timed live with HIP
     events: lnskv_read_units over the same (page, kv head) units as the
@@ -369,6 +406,48 @@ def config_measure(name: str, dev, steps: int, layers: int = 2, kv_dtype: int | 
     return res
 
 
+def c5_churn_measure(dev, steps: int, n_plan: int = 20, layers: int = 2) -> dict:
+    """c5 with churn in every timed step: each step frees the previous step's
+    forks and 32 sequences, refills their rows with new sequences on the freed
+    pages, forks 8 survivors (copy-on-write: tail pages copied) and appends +
+    attends over all 136 live sequences.  The host bookkeeping (PagePool and
+    BlockTables through the C ABI) is done for n_plan steps ahead of the timed
+    loop (its time per step is reported); inside each timed step the changed
+    tables, kv_len and copy lists go to the device (one host-to-device copy
+    from pinned memory), then the page copies and the fused append + decode
+    run.  Event mean over `steps` steps cycling the plan and the layers."""
+    import time
+
+    import torch
+
+    from lnskv.configs import churn_plan, make_c5
+    from lnskv.step import ChurnRunner, StepRunner
+
+    w = make_c5(spare=4096, extra_pages=2)
+    runner = StepRunner(w, dev, n_layers=layers, seed=1)
+    t0 = time.perf_counter()
+    plan = churn_plan(w, n_plan)
+    host_s = (time.perf_counter() - t0) / n_plan
+    cr = ChurnRunner(runner, plan, max_kv_len=w.tables.shape[1] * 16)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    step = lambda i: cr.run(i, i % layers)  # noqa: E731
+    ev, wall = timed_steps(step, stream, steps, 10)
+    nb = sum(cr.step_bytes(i) for i in range(steps)) / steps
+    res = {"us_per_step_events": round(ev * 1e6, 2), "us_per_step_wall": round(wall * 1e6, 2),
+           "algorithmic_bytes_mean": int(nb), "gb_per_s": round(nb / ev / 1e9, 1),
+           "frac_of_hbm_peak": round(nb / ev / 1e9 / HBM_PEAK_GBS, 4),
+           "upload_bytes_per_step": int(cr.host.shape[1] * 4),
+           "page_copies_per_step_mean": round(sum(len(p["copies"]) for p in plan) / n_plan, 2),
+           "host_bookkeeping_ms_per_step": round(host_s * 1e3, 2),
+           "note": "timed step = upload of the step's tables/kv_len/copy lists + tail-page copies + fused "
+                   "append/decode of 136 sequences; host bookkeeping (free 40, allocate 32, fork 8) done "
+                   "ahead, from Python through the C ABI, one call per page"}
+    del cr, runner
+    torch.cuda.empty_cache()
+    return res
+
+
 def full_copy_fork(w, runner, dev, reps: int = 20) -> dict:
     """c5's fork with every page of the 8 children copied (no sharing): one
     lnskv_page_copy of all their pages, K and V, read and written."""
@@ -626,6 +705,7 @@ def main():
     gbs_wall = nb["total"] / wall / 1e9
     gbs_ev = nb["total"] / ev_mean / 1e9
     copy = copy_ceiling(dev, args.copy_mb) if args.copy_mb > 0 else None
+    readc = read_ceiling(dev) if args.copy_mb > 0 else None
     pattern = pattern_ceiling(w, runner, dev, args.pattern_reps)
     oproj = oproj_measure(w, runner, dev, args.oproj_reps)
     prefill = prefill_measure(w, runner, dev, args.prefill_reps)
@@ -637,6 +717,7 @@ def main():
                   "block_table_upload": table_upload_measure(w, dev)}
         for name in ("c1", "c3", "c4", "c5"):
             extras[name] = config_measure(name, dev, min(args.steps, 100))
+        extras["c5_churn_every_step"] = c5_churn_measure(dev, min(args.steps, 100))
     cpu = None
     if args.cpu_seconds > 0:
         threads = args.cpu_threads or len(os.sched_getaffinity(0))
@@ -690,6 +771,9 @@ def main():
                        "of one lnskv_append_decode call), mean HIP-event duration per step"),
             "copy_ceiling_gbs": copy["gb_per_s"] if copy else None,
             "frac_of_copy_ceiling": round(gbs_ev / copy["gb_per_s"], 4) if copy else None,
+            "read_ceiling_gbs": readc["gb_per_s"] if readc else None,
+            "frac_of_read_ceiling": round(gbs_ev / readc["gb_per_s"], 4) if readc else None,
+            "read_ceiling": readc,
             "pattern_ceiling": pattern,
             "frac_of_pattern_ceiling": round(gbs_ev / pattern["gb_per_s"], 4) if pattern else None,
         },

@@ -326,6 +326,9 @@ int lnskv_q4l_prepare(const void* disk_blocks, size_t disk_bytes, int32_t rows, 
  * workspace_dev/ws_bytes: 16-byte aligned device scratch of at least
  * lnskv_q4l_workspace_size(cols, n_vec) bytes (0 when cols < 2048: no
  * workspace is read), or NULL/0 to use a buffer the library keeps per device.
+ * A call none of whose launches splits its rows' blocks (enough row groups to
+ * fill the GPU, e.g. rows >= 8192 for up to 16 vectors) reads no workspace and
+ * may pass NULL without the library buffer being grown, under capture too.
  * It holds the partial sums of a launch that splits each row's blocks over
  * several workgroups, after LNSKV_WORKSPACE_HEADER_BYTES of arrival counts
  * that must be zero before the first use (hipMemset once); every call leaves
@@ -379,7 +382,14 @@ int lnskv_gather(const lnskv_pages* c, const uint32_t* block_table_dev, int32_t 
                  float* vs_out_dev, lnskv_stream_t stream);
 
 /* Wait for all work queued on stream (the commit + wait_until_completed of
- * dispatch_*, lib.rs:1091-1092). */
+ * dispatch_*, lib.rs:1091-1092).  Also returns LNSKV_ERR_WORKSPACE when a
+ * decode or Q4L GEMV call since the last lnskv_sync (on any stream of the
+ * process) met an arrival count in its workspace header above what one call
+ * can reach: that workspace's first LNSKV_WORKSPACE_HEADER_BYTES bytes were
+ * not zeroed before its first use, and the cut segments' (decode) or split
+ * rows' (Q4L) results of calls on it are wrong.  Such a count is left in
+ * place, so every later call on that workspace is reported again.  A garbage
+ * count that happens to lie within what a call can reach is not detected. */
 int lnskv_sync(lnskv_stream_t stream);
 
 /* ---------------------------------------------------------------------------
@@ -497,6 +507,16 @@ int lnskv_block_tables_upload(const lnskv_block_tables* t, uint32_t* dst_dev,
 int lnskv_read_units(const lnskv_pages* c, const uint32_t* unit_page, const int32_t* unit_kvh,
                      const int32_t* wave_start, int32_t n_waves, uint32_t* sink,
                      lnskv_stream_t stream);
+/* lnskv_read_stream: the plain read ceiling.  Reads bytes (a positive multiple
+ * of 16) of buf_dev (16-byte aligned) front to back with 16-byte loads,
+ * loads_in_flight (1, 2, 4, 8 or 16) per thread issued before any is used,
+ * blocks_per_cu (1..8) workgroups of 256 threads per compute unit, thread t of
+ * T reading chunks t, t + T, ... (each wave instruction 1 KiB contiguous).
+ * Nothing is written except by a thread whose XOR of the 32-bit words it read
+ * is 0x9E3779B9: it stores 1 to sink_dev[0] (this keeps the loads from being
+ * elided). */
+int lnskv_read_stream(const void* buf_dev, size_t bytes, int32_t loads_in_flight, int32_t blocks_per_cu,
+                      uint32_t* sink_dev, lnskv_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1484,6 +1484,11 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
       uint32_t old = 0;
       if (lane == 0) old = __hip_atomic_fetch_add(a.wg_cnt + ga, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       old = __builtin_amdgcn_readfirstlane(old);
+      // a count above gz - ga cannot happen on a header that was zero: flag it
+      // for the host (lnskv_sync reports it); the count is left as it is, so
+      // every later call on this header is flagged too
+      if (old > (uint32_t)(gz - ga) && lane == 0 && a.ws_err)
+        __hip_atomic_store(a.ws_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       if (old == (uint32_t)(gz - ga)) {  // every other workgroup is done: this one merges
         if (lane == 0) {
           __hip_atomic_store(a.wg_cnt + ga, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -152,6 +152,8 @@ struct DecodeArgs {
   int4* sk_desc;        // stream-K: per wave, the segment its first piece closes
   uint32_t* wg_cnt;     // workgroup schedule: per workgroup, a count of the workgroups done
                         // with the segment that starts in it (zero between calls)
+  uint32_t* ws_err;     // host word set to 1 when a count exceeds what a call can reach
+                        // (a header that was not zero); nullptr: not checked
   const float* gate;      // gated attention: out *= gate ([n_seq][n_heads][D]); nullptr: none
   const float* rope_inv;  // fused RoPE in the MFMA kernels: inverse frequencies
   int32_t rope_half;      // fused RoPE: rotary_dim / 2, 32 or 64; 0: none (the kernels without RoPE run)

@@ -22,6 +22,15 @@ int check_geometry(const lnskv_pages* c);
 // Checks geometry and that the pools (and Q8A scales) are non-null.
 int check_pages(const lnskv_pages* c);
 uint16_t f32_to_f16_bits(float f);
+
+// The process's workspace error word: pinned host memory that a decode or Q4L
+// kernel sets to 1 when an arrival count in a workspace header exceeds the
+// number of workgroups that share it (a header that was not zero before its
+// first use).  Allocated on first use outside stream capture; nullptr while it
+// does not exist (a capturing stream, or allocate == false).
+uint32_t* ws_error_word(void* stream, bool allocate);
+// Reads and clears the word (after a stream synchronization): 1 if set.
+int take_ws_error();
 float f16_bits_to_f32(uint16_t h);
 
 }  // namespace lnskv

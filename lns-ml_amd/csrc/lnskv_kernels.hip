@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -27,6 +28,40 @@ int hip_check(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(LNSKV_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
   return LNSKV_OK;
+}
+
+namespace {
+std::mutex g_err_mutex;
+std::atomic<uint32_t*> g_ws_err{nullptr};  // pinned, coherent host word; never freed
+}  // namespace
+
+uint32_t* ws_error_word(void* stream, bool allocate) {
+  uint32_t* w = g_ws_err.load(std::memory_order_acquire);
+  if (w || !allocate) return w;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (cs != hipStreamCaptureStatusNone) return nullptr;
+  std::lock_guard<std::mutex> lock(g_err_mutex);
+  w = g_ws_err.load(std::memory_order_acquire);
+  if (!w) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, sizeof(uint32_t), hipHostMallocCoherent) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    w = static_cast<uint32_t*>(p);
+    __atomic_store_n(w, 0u, __ATOMIC_RELAXED);
+    g_ws_err.store(w, std::memory_order_release);
+  }
+  return w;
+}
+
+int take_ws_error() {
+  uint32_t* w = g_ws_err.load(std::memory_order_acquire);
+  return w ? (int)__atomic_exchange_n(w, 0u, __ATOMIC_ACQ_REL) : 0;
 }
 
 namespace {
@@ -585,7 +620,7 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
                  int32_t kv_len_scalar, const int32_t* p_start, int32_t p_start_scalar,
                  int32_t n_seq, int32_t n_heads, int32_t max_kv_len, float scale, int32_t split,
                  void* ws, size_t ws_bytes, lnskv_stream_t stream, const lnskv_rope* rope = nullptr,
-                 const float* gate = nullptr) {
+                 const float* gate = nullptr, bool noalloc = false) {
   clear_error();
   if (int rc = check_pages(c)) return rc;
   if (!q || !out || !bt) return fail(LNSKV_ERR_INVALID, "q, out and block tables must be non-null");
@@ -673,6 +708,7 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
   a.rope_half = rope_half;
   a.rope_inv = rope_half > 0 ? rope->inv_freqs_dev : nullptr;
   a.gate = gate;
+  a.ws_err = ws_error_word(stream, !noalloc);
   if (plan.wg > 0) {
     a.wg_cnt = static_cast<uint32_t*>(ws);
     a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeaderBytes);
@@ -951,7 +987,8 @@ int lnskv_append_decode_noalloc(const lnskv_pages* c, const float* q, const floa
   void* ws = nullptr;
   if (int rc = noalloc_scratch(&ws)) return rc;
   return decode_entry<true>(c, q, k_new, v_new, out, bt, bt_stride, kv_len, 0, p_start, 0, n_seq, n_heads,
-                            max_kv_len, scale, split_tokens, ws, kNoAllocScratchBytes, stream);
+                            max_kv_len, scale, split_tokens, ws, kNoAllocScratchBytes, stream, nullptr, nullptr,
+                            true);
 }
 
 int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const float* q, const float* k_new,
@@ -1130,6 +1167,11 @@ int lnskv_sync(lnskv_stream_t stream) {
   clear_error();
   const hipError_t e = hipStreamSynchronize((hipStream_t)stream);
   if (e != hipSuccess) return fail(LNSKV_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+  if (take_ws_error())
+    return fail(LNSKV_ERR_WORKSPACE,
+                "a decode or Q4L GEMV call found an arrival count in its workspace header above what the call "
+                "can reach: that header was not zero before its first use, and the results of calls on it are "
+                "wrong (zero the first LNSKV_WORKSPACE_HEADER_BYTES bytes once)");
   return LNSKV_OK;
 }
 

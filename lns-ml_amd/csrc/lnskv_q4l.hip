@@ -106,6 +106,7 @@ struct Q4lArgs {
   float* y;
   float* part;    // [S][groups][q4l_wg_outputs(T)] partial sums (S > 1)
   uint32_t* cnt;  // [groups] arrival counts, zero between calls (S > 1)
+  uint32_t* err;  // host word set to 1 on a count above S - 1 (a header that was not zero)
   int64_t x_stride, y_stride;
   int rows, bpr, n_vec, tile0;
   int groups;     // row groups of 16 q4l_row_tiles(T) rows
@@ -284,6 +285,8 @@ __global__ __launch_bounds__(kQ4lWaves * kWave) void q4l_gemv_acc_kernel(Q4lArgs
     if (tid == 0) {
       const uint32_t old = __hip_atomic_fetch_add(a.cnt + rg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const bool last = old == (uint32_t)(a.split - 1);
+      if (old > (uint32_t)(a.split - 1) && a.err)  // not a zeroed header: flagged for lnskv_sync
+        __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       if (last) __hip_atomic_store(a.cnt + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       merge = last;
     }
@@ -339,6 +342,21 @@ size_t q4l_ws_bytes(int cols, int n_vec) {
   return kWsHeaderBytes + (size_t)2 * kQ4lTargetWgs * (size_t)q4l_wg_outputs(T) * sizeof(float);
 }
 
+// What the launches of one call use: 0 when none of them splits (then the
+// call needs no workspace at all), else at most q4l_ws_bytes(cols, n_vec).
+size_t q4l_call_ws_bytes(int rows, int cols, int n_vec) {
+  const int bpr = cols / 256;
+  const int n_tiles = (n_vec + kQ4lTileVecs - 1) / kQ4lTileVecs;
+  size_t most = 0;
+  for (int t0 = 0; t0 < n_tiles; t0 += kQ4lMaxTiles) {
+    const int T = std::min(n_tiles - t0, kQ4lMaxTiles);
+    int groups = 0, split = 0, bpw = 0;
+    q4l_plan(rows, bpr, 16 * q4l_row_tiles(T), &groups, &split, &bpw);
+    if (split > 1) most = std::max(most, (size_t)split * groups * (size_t)q4l_wg_outputs(T) * sizeof(float));
+  }
+  return most > 0 ? kWsHeaderBytes + most : 0;
+}
+
 }  // namespace
 }  // namespace lnskv
 
@@ -370,7 +388,7 @@ extern "C" int lnskv_q4l_gemv_accumulate(const void* blocks_dev, const float* x_
       (reinterpret_cast<uintptr_t>(blocks_dev) & 15) != 0)
     return fail(LNSKV_ERR_INVALID, "x and the blocks must be 16-byte aligned and x_stride a multiple of 4");
   const hipStream_t st = (hipStream_t)stream;
-  const size_t need = q4l_ws_bytes(cols, n_vec);
+  const size_t need = q4l_call_ws_bytes(rows, cols, n_vec);
   if (need > 0) {
     if (ws == nullptr) {
       if (int rc = library_buffer(2, need, &ws, st)) return rc;
@@ -386,6 +404,7 @@ extern "C" int lnskv_q4l_gemv_accumulate(const void* blocks_dev, const float* x_
   a.y = y_dev;
   a.cnt = need > 0 ? static_cast<uint32_t*>(ws) : nullptr;
   a.part = need > 0 ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeaderBytes) : nullptr;
+  a.err = need > 0 ? ws_error_word(stream, true) : nullptr;
   a.x_stride = x_stride;
   a.y_stride = y_stride;
   a.rows = rows;

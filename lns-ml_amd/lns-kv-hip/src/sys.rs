@@ -398,4 +398,12 @@ extern "C" {
         sink: *mut u32,
         stream: HipStream,
     ) -> c_int;
+    pub fn lnskv_read_stream(
+        buf_dev: *const c_void,
+        bytes: usize,
+        loads_in_flight: i32,
+        blocks_per_cu: i32,
+        sink_dev: *mut u32,
+        stream: HipStream,
+    ) -> c_int;
 }

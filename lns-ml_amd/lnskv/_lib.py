@@ -127,6 +127,7 @@ SIGNATURES = {
         C.c_int, [_P, _R, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _vp, _sz,
                   _vp]),
     "lnskv_read_units": (C.c_int, [_P, _vp, _vp, _vp, _i32, _vp, _vp]),
+    "lnskv_read_stream": (C.c_int, [_vp, _sz, _i32, _i32, _vp, _vp]),
     "lnskv_q4l_prepare": (C.c_int, [_vp, _sz, _i32, _i32, _vp]),
     "lnskv_q4l_workspace_size": (C.c_int, [_i32, _i32, C.POINTER(_sz)]),
     "lnskv_q4l_gemv_accumulate": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),

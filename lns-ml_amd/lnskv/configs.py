@@ -222,7 +222,7 @@ def make_c4(seed: int = 0, n_chunk: int = 16, chunk: int = 256, n_dec: int = 48,
 
 
 def make_c5(seed: int = 0, n_seq: int = 128, lo: int = 256, hi: int = 8192, n_free: int = 32,
-            n_fork: int = 8) -> Workload:
+            n_fork: int = 8, spare: int = 64, extra_pages: int = 0) -> Workload:
     """State after one churn step.  Rows 0..n_seq-1 hold the original batch; the
     n_free freed rows are refilled by new sequences (seeded lengths); rows
     n_seq..n_seq+n_fork-1 are copy-on-write children of n_fork surviving
@@ -230,7 +230,7 @@ def make_c5(seed: int = 0, n_seq: int = 128, lo: int = 256, hi: int = 8192, n_fr
     rl = SplitMix64(seed, S_LEN)
     ctx0 = [rl.randint(lo, hi) for _ in range(n_seq)]
     total = n_seq + n_fork
-    stride = (hi + 1 + PAGE_SIZE - 1) // PAGE_SIZE
+    stride = (hi + 1 + PAGE_SIZE - 1) // PAGE_SIZE + extra_pages  # extra: room for later churn steps
     # Draw every choice first so the pool can be sized tightly: the new
     # sequences then take the freed pages once the few spare ones run out.
     freed = sorted(SplitMix64(seed, S_CHURN).shuffle(list(range(n_seq)))[:n_free])
@@ -242,7 +242,7 @@ def make_c5(seed: int = 0, n_seq: int = 128, lo: int = 256, hi: int = 8192, n_fr
     need0 = sum(pages(c) for c in ctx0)
     final = [new_len.get(s, ctx0[s]) for s in range(n_seq)] + [ctx0[p] for p in parents]
     need1 = sum(pages(c + 1) for c in final)
-    num_pages = max(need0, need1) + 64
+    num_pages = max(need0, need1) + spare
     pool, _ = _shuffled_pool(num_pages, SplitMix64(seed, S_PERM))
     bt = BlockTables(total, stride)
     _alloc_rows(bt, pool, range(n_seq), ctx0)
@@ -271,6 +271,54 @@ def make_c5(seed: int = 0, n_seq: int = 128, lo: int = 256, hi: int = 8192, n_fr
                  pool=pool, bt=bt, info={"freed_rows": freed, "freed_pages": freed_pages,
                                          "parents": parents})
     return _finish(w)
+
+
+def churn_plan(w: Workload, n_steps: int, seed: int = 1, n_free: int = 32, lo: int = 256,
+               hi: int = 8192) -> list[dict]:
+    """c5's churn continued for n_steps more steps from the state of make_c5,
+    on its PagePool and BlockTables.  Step i: the previous step's copy-on-write
+    children are freed; n_free seeded sequences of the base batch are freed
+    and their rows refilled by new sequences of seeded lengths (ensure_kv_page
+    over their pages, which come from the FIFO free list, the freed pages
+    among them); as many children are forked from seeded survivors (full
+    pages shared by refcount, the tail page copied); every live sequence gets
+    the page of its appended token.  Each step records what its device step
+    needs: the block tables, kv_len (the appended token included) and the
+    (src, dst) page copies.  Lengths grow by one per step."""
+    n_fork = len(w.info["parents"])
+    n_seq = w.n_seq - n_fork
+    pool, bt = w.pool, w.bt
+    L = [int(x) for x in w.kv_len]  # after make_c5's step
+    if max(L) + n_steps > bt.max_pages * PAGE_SIZE:
+        raise ValueError(f"{n_steps} churn steps need rows of {max(L) + n_steps} positions; the table holds "
+                         f"{bt.max_pages * PAGE_SIZE} (make_c5 extra_pages)")
+    plan = []
+    for i in range(n_steps):
+        rs = SplitMix64(seed + 97 * i, S_CHURN)
+        for c in range(n_seq, n_seq + n_fork):
+            bt.free_sequence(pool, c)
+        freed = sorted(rs.shuffle(list(range(n_seq)))[:n_free])
+        rn = SplitMix64(seed + 97 * i, S_NEWLEN)
+        for s in freed:
+            bt.free_sequence(pool, s)
+        for s in freed:
+            L[s] = rn.randint(lo, hi)
+        _alloc_rows(bt, pool, freed, [L[s] for s in freed])
+        keep = set(freed)
+        survivors = [s for s in range(n_seq) if s not in keep]
+        parents = SplitMix64(seed + 97 * i, S_FORK).shuffle(survivors)[:n_fork]
+        copies = []
+        for j, par in enumerate(parents):
+            child = n_seq + j
+            cp = bt.fork_sequence(pool, par, child, L[par])
+            if cp is not None:
+                copies.append(cp)
+            L[child] = L[par]
+        _alloc_rows(bt, pool, range(n_seq + n_fork), [x + 1 for x in L])
+        plan.append({"tables": bt.array(), "kv_len": np.array([x + 1 for x in L], np.int32),
+                     "copies": copies, "freed": freed, "parents": parents})
+        L = [x + 1 for x in L]
+    return plan
 
 
 MAKERS = {"c1": make_c1, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5}

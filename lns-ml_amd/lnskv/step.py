@@ -122,3 +122,62 @@ class StepRunner:
             self.run(layer)
         torch.cuda.synchronize(self.dev)
         return g
+
+
+class ChurnRunner:
+    """c5's eviction churn step by step (configs.churn_plan): each step's
+    block tables, kv_len and copy-on-write page copies differ, so every step
+    uploads them (one packed host-to-device copy from pinned memory: tables,
+    kv_len, copy sources, copy destinations), then runs the tail-page copies
+    and the fused append + decode of every live sequence.  The pools,
+    q/k_new/v_new and the layers come from a StepRunner of the c5 workload."""
+
+    def __init__(self, runner: StepRunner, plan: list[dict], max_kv_len: int):
+        self.r = runner
+        self.plan = plan
+        w = runner.w
+        self.n, self.stride = w.tables.shape
+        self.max_copies = max(1, max(len(st["copies"]) for st in plan))
+        self.max_kv_len = max_kv_len
+        n, sd, mc = self.n, self.stride, self.max_copies
+        words = n * sd + n + 2 * mc
+        self.host = torch.empty((len(plan), words), dtype=torch.int32, pin_memory=True)
+        for i, st in enumerate(plan):
+            row = np.zeros(words, np.int32)
+            row[:n * sd] = st["tables"].astype(np.uint32).view(np.int32).ravel()
+            row[n * sd:n * sd + n] = st["kv_len"]
+            cps = np.array(st["copies"], np.uint32).reshape(-1, 2)
+            row[n * sd + n:n * sd + n + len(cps)] = cps[:, 0].view(np.int32)
+            row[n * sd + n + mc:n * sd + n + mc + len(cps)] = cps[:, 1].view(np.int32)
+            self.host[i].copy_(torch.from_numpy(row))
+        self.dev_buf = torch.empty(words, dtype=torch.int32, device=runner.dev)
+        self.tables = self.dev_buf[:n * sd].view(n, sd)
+        self.kv_len = self.dev_buf[n * sd:n * sd + n]
+        self.src = self.dev_buf[n * sd + n:n * sd + n + mc]
+        self.dst = self.dev_buf[n * sd + n + mc:]
+        ws = runner.layers[0].workspace_size(n, w.n_heads, max_kv_len, w.split)
+        self.workspace = torch.zeros(max(ws, 16), dtype=torch.uint8, device=runner.dev)
+
+    def run(self, i: int, layer: int = 0) -> torch.Tensor:
+        r, w = self.r, self.r.w
+        st = self.plan[i % len(self.plan)]
+        pk = r.layers[layer]
+        self.dev_buf.copy_(self.host[i % len(self.plan)], non_blocking=True)
+        nc = len(st["copies"])
+        if nc:
+            pk.page_copy(self.src[:nc], self.dst[:nc])
+        return pk.append_decode(r.q, r.k_new, r.v_new, self.tables, self.kv_len, n_heads=w.n_heads,
+                                max_kv_len=self.max_kv_len, scale=w.scale, split=w.split,
+                                workspace=self.workspace, out=r.out)
+
+    def step_bytes(self, i: int) -> int:
+        """Algorithmic HBM bytes of churn step i (as Workload.algorithmic_bytes:
+        K+V windows, append, q/out, table entries, page copies)."""
+        w = self.r.w
+        st = self.plan[i % len(self.plan)]
+        d, nkv, hq, e = w.head_dim, w.n_kv, w.n_heads, w.elem_bytes
+        L = st["kv_len"].astype(np.int64)
+        per_tok = 2 * nkv * d * e
+        page = 16 * nkv * d * e
+        return int(L.sum() * per_tok + len(L) * (2 * nkv * d * 4 + per_tok) + len(L) * hq * d * 8 +
+                   np.ceil(L / 16).sum() * 4 + len(st["copies"]) * 2 * 2 * page)

@@ -72,6 +72,15 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert rc == _lib.ERR_UNSUPPORTED and "256" in msg
     rc, _ = _status(lib.lnskv_read_units, C.byref(good), 1, 1, 1, 0, 1, None)
     assert rc == _lib.ERR_INVALID
+    # the read ceiling: size, alignment, depth and occupancy are checked before any launch
+    rc, msg = _status(lib.lnskv_read_stream, 16, 24, 4, 4, 16, None)
+    assert rc == _lib.ERR_INVALID and "multiple of 16" in msg
+    rc, msg = _status(lib.lnskv_read_stream, 8, 32, 4, 4, 16, None)
+    assert rc == _lib.ERR_INVALID and "aligned" in msg
+    rc, msg = _status(lib.lnskv_read_stream, 16, 32, 4, 9, 16, None)
+    assert rc == _lib.ERR_INVALID and "blocks_per_cu" in msg
+    rc, _ = _status(lib.lnskv_read_stream, None, 32, 4, 4, 16, None)
+    assert rc == _lib.ERR_INVALID
     rc, msg = _status(lib.lnskv_gated_append_decode, C.byref(good), None, None, 1, 1, 1, 1, 1, 4, 1, None, 1,
                       32, 16, 0.1, 0, None, 0, None)
     assert rc == _lib.ERR_INVALID and "gate" in msg

@@ -88,3 +88,37 @@ def test_config_step(gpu, name):
     out2 = r.run(0).cpu().numpy()
     assert np.array_equal(out2, o)
 
+
+
+def test_c5_churn_steps(gpu):
+    """c5's churn continued step by step (a smaller batch): every step frees
+    the previous children and a quarter of the batch, refills those rows with
+    new sequences on the freed pages, forks children (tail pages copied) and
+    uploads the changed tables inside the step.  After each step the pages
+    the step touched are bit-exact with the oracle's replay and every output
+    row is within tolerance of the f64 oracle."""
+    from lnskv.configs import churn_plan, make_c5
+    from lnskv.step import ChurnRunner
+
+    w = make_c5(n_seq=24, lo=40, hi=700, n_free=6, n_fork=3, spare=256)
+    r = StepRunner(w, gpu, n_layers=1, seed=5)
+    plan = churn_plan(w, 3, seed=2, n_free=6, lo=40, hi=700)
+    cr = ChurnRunner(r, plan, max_kv_len=700 + 8)
+    pk = r.layers[0]
+    for i, st in enumerate(plan):
+        say("c5 churn step", i, "copies", len(st["copies"]), "freed", st["freed"])
+        hp, _ = host_pages(pk)
+        tables = st["tables"]
+        if st["copies"]:
+            cps = np.array(st["copies"], np.uint32)
+            O.page_copy(hp, cps[:, 0], cps[:, 1])
+        kv_len = st["kv_len"]
+        assert O.append(hp, r.k_new.cpu().numpy(), r.v_new.cpu().numpy(), np.arange(len(kv_len), dtype=np.int32),
+                        kv_len - 1, tables) == 0
+        out = cr.run(i).cpu().numpy()
+        sync()
+        got, _ = host_pages(pk)
+        assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8)), i
+        assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8)), i
+        ref = O.decode_f64(hp, r.q.cpu().numpy(), tables, kv_len, None, w.scale)
+        assert rel_err(out, ref).max() < TOL[w.dtype], i

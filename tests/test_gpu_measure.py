@@ -90,3 +90,29 @@ def test_read_units_checksum(gpu, dtype, d):
         exp = _expected(k32, v32, pages, kvhs, start, num_pages, n_kv)
     got = sink.cpu().numpy().view(np.uint32)
     assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("where", ["first", "middle", "last"])
+def test_read_stream_reads_every_chunk(gpu, where):
+    """lnskv_read_stream (the plain read ceiling) reads every 16-byte chunk: a
+    buffer of zeros with one word set to the marker makes the thread that
+    reads that chunk store 1; an all-zero buffer stores nothing.  Sizes that
+    do and do not fill whole rounds of loads."""
+    import ctypes as C
+
+    from lnskv._lib import check, lib
+
+    say("read stream", where)
+    stream = C.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+    for n16 in (1 << 16, (1 << 16) + 37):
+        for u, bpc in ((4, 2), (16, 8), (1, 1)):
+            buf = torch.zeros(n16 * 4, dtype=torch.int32, device=gpu)
+            sink = torch.zeros(1, dtype=torch.int32, device=gpu)
+            check(lib().lnskv_read_stream(buf.data_ptr(), n16 * 16, u, bpc, sink.data_ptr(), stream))
+            torch.cuda.synchronize()
+            assert int(sink.item()) == 0
+            chunk = {"first": 0, "middle": n16 // 2 + 3, "last": n16 - 1}[where]
+            buf[4 * chunk + 2] = np.int32(np.uint32(0x9E3779B9).view(np.int32))
+            check(lib().lnskv_read_stream(buf.data_ptr(), n16 * 16, u, bpc, sink.data_ptr(), stream))
+            torch.cuda.synchronize()
+            assert int(sink.item()) == 1, (n16, u, bpc)

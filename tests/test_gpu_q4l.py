@@ -70,7 +70,7 @@ def test_q4l_gemv_accumulate(gpu, rows, cols, n_vec, xpad, ypad):
 def test_q4l_caller_workspace(gpu):
     """A caller's workspace (arrival counts zeroed once) gives the bits of the
     library's buffer, call after call and across shapes that share it (every
-    call leaves the counts zero); one byte too small is refused before any
+    call leaves the counts zero); one too small is refused before any
     launch, leaving y untouched."""
     from lnskv import _lib
     say("q4l caller workspace")
@@ -95,7 +95,9 @@ def test_q4l_caller_workspace(gpu):
             assert torch.equal(ya, yb), (rep, rows, cols, n_vec)
     assert int(ws[:_lib.WORKSPACE_HEADER_BYTES].count_nonzero()) == 0
     W = mats[(4096, 4096)]
-    small = torch.zeros(W.workspace_size(32) - 1, dtype=torch.uint8, device=gpu)
+    # the call's own need (its launch plan) is at most the query's bound; the
+    # count header alone holds none of its partial sums
+    small = torch.zeros(_lib.WORKSPACE_HEADER_BYTES + 16, dtype=torch.uint8, device=gpu)
     x = torch.ones((32, 4096), device=gpu)
     y = torch.zeros((32, 4096), device=gpu)
     with pytest.raises(RuntimeError, match="workspace"):

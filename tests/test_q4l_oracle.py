@@ -133,7 +133,10 @@ def test_gemv_rejects_bad_arguments(bad):
         need = C.c_size_t()
         assert lib.lnskv_q4l_workspace_size(4096, 32, C.byref(need)) == 0 and need.value > 0
         if bad == "ws_small":
-            assert f(16, 16, 16, 64, 4096, 32, 4096, 64, 32, need.value - 1, None) == _lib.ERR_WORKSPACE
+            # the call's own need (its launch plan) is at most the query's bound;
+            # a workspace of the count header alone holds no partial sums
+            assert f(16, 16, 16, 64, 4096, 32, 4096, 64, 32, _lib.WORKSPACE_HEADER_BYTES, None) == \
+                _lib.ERR_WORKSPACE
         else:
             assert f(16, 16, 16, 64, 4096, 32, 4096, 64, 24, need.value, None) == _lib.ERR_WORKSPACE
         assert "workspace" in _lib.last_error()

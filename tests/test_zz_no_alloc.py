@@ -118,3 +118,46 @@ def test_noalloc_refuses_a_schedule_larger_than_the_scratch(gpu):
     sync()
     assert bool((out == 7.0).all())          # nothing ran
     assert _pools_equal(pk, twin)
+
+
+def test_noalloc_allocates_nothing_and_replays_under_capture(gpu):
+    """After one warm-up call (the scratch address lookup and the schedule
+    caches), the library's own buffers are released: an eager call then takes
+    no device memory, and the call captured into a HIP graph replays with the
+    eager call's bits (the append rewrites the same slot with the same values)."""
+    say("noalloc: no device memory taken, graph capture and replay")
+    lens = [700, 1500, 3000, 64]
+    pk, tables, kv_len, q, k_new, v_new = _batch(gpu, DTYPE_Q8A, lens, seed=21)
+    n_seq, n_heads = len(lens), 32
+    dq, dk, dv = dev_f32(q, gpu), dev_f32(k_new, gpu), dev_f32(v_new, gpu)
+    dt, dl = dev_i32(tables, gpu), dev_i32(kv_len, gpu)
+    max_len = int(kv_len.max())
+    scale = float(1.0 / np.sqrt(128))
+    out = torch.zeros((n_seq, n_heads, 128), dtype=torch.float32, device=gpu)
+
+    def call():
+        rc = lib().lnskv_append_decode_noalloc(C.byref(pk.desc), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                               out.data_ptr(), dt.data_ptr(), int(tables.shape[1]), dl.data_ptr(),
+                                               None, n_seq, n_heads, max_len, scale, 0, _stream(gpu))
+        assert rc == 0, lib().lnskv_last_error()
+
+    call()
+    sync()
+    assert lib().lnskv_workspace_release() == 0
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info(gpu)[0]
+    call()
+    sync()
+    assert torch.cuda.mem_get_info(gpu)[0] == free0
+    eager = out.clone()
+    s = torch.cuda.Stream(device=gpu)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call()
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), eager.view(torch.int32)), i
