@@ -67,9 +67,13 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) half8 lds_half8;
 
-constexpr int kD = 128;
-constexpr int kRowBytes = kD * 2;         // one (token, kv head) row of f16
-constexpr int kVSlot = kPage * kRowBytes;  // one page of V in LDS (swizzled rows)
+// Heads of 128 dims (Llama-3 / Mixtral) and of 256 (lns-ml's Qwen3.5
+// full-attention layers, model_config.rs:563-593): a 256-wide head is two
+// 128-dim halves (NH = 2) that share one softmax; every per-half layout below
+// (K operand lanes, V slot, transposed reads, output lanes) is the 128-dim one.
+constexpr int kD = 128;                    // dims of one half
+constexpr int kRowBytes = kD * 2;         // one half-row of f16
+constexpr int kVSlot = kPage * kRowBytes;  // one half-page of V in LDS (swizzled rows)
 constexpr float kRescaleSlack = 8.0f;     // log2 units the running max may lag
 constexpr int kSkMinPages = 4;            // stream-K: fewest pages per wave
 // Buffer resource word 3 for raw dword access on gfx9-family parts
@@ -124,17 +128,18 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <int REP>
+template <int REP, int NH = 1>
 struct WaveState {
   // Q8A pages: int8 products; the B columns are REP heads x 3 limbs
   static constexpr int kSets = (3 * REP + 15) / 16;
-  half8 qb[4];      // B operand of Q.K^T per 32-dim block, column lane%16
-  // Q8A pages: q as three int8 limbs (B operand of the int8 products,
-  // 2 per set): column c = 16*set + lane%16 holds limb c/REP of head c%REP;
-  // qsc takes the limb sums of head lane%16 back to scaled scores
-  u32x4 qi[2 * kSets];
+  half8 qb[4 * NH];  // B operand of Q.K^T per 32-dim block, column lane%16
+  // Q8A pages: q as three int8 limbs (B operand of the int8 products, 2 per
+  // set and half: qi[2 kSets h + 2 set + j]): column c = 16*set + lane%16
+  // holds limb c/REP of head c%REP; qsc takes the limb sums of head lane%16
+  // back to scaled scores
+  u32x4 qi[2 * kSets * NH];
   float qsc;
-  float4v acc[8];   // P.V result: lane (g, n) holds O[row 4g+ii][16*nb + n]
+  float4v acc[8 * NH];  // P.V result: lane (g, n) holds O[row 4g+ii][16*nb + n]
   float m;          // lanes with lane%16 < REP: running max of head lane%16
   float l;          // partial softmax sum over this lane's tokens
   float qexp;       // 2^E undoing the per-head normalisation of q
@@ -147,14 +152,14 @@ struct WaveState {
 // Multiplies the result rows 4g+ii of this lane by their head's alpha: row r
 // belongs to head r % REP, whose alpha sits in lane (r % REP) of every
 // 16-lane row (all rows agree).
-template <int REP, int II = 0>
-__device__ __forceinline__ void scale_rows(WaveState<REP>& st, float alpha, int g) {
+template <int REP, int NH, int II = 0>
+__device__ __forceinline__ void scale_rows(WaveState<REP, NH>& st, float alpha, int g) {
   if constexpr (II < 4) {
     float f = row_value<II % REP>(alpha);
     if constexpr (REP == 8) f = (g & 1) ? row_value<4 + II>(alpha) : f;
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) st.acc[nb][II] *= f;
-    scale_rows<REP, II + 1>(st, alpha, g);
+    for (int nb = 0; nb < 8 * NH; ++nb) st.acc[nb][II] *= f;
+    scale_rows<REP, NH, II + 1>(st, alpha, g);
   }
 }
 
@@ -170,41 +175,44 @@ struct Stream {
   uint32_t vr_half;    // 8 * (n & 1)
   uint32_t vr_sub;     // (n & 3) >> 1: chunk within the 2-chunk pair
   uint32_t num_pages;
-  uint32_t kvh_off;    // kvh * kRowBytes
-  uint32_t page_bytes; // 16 * n_kv * kRowBytes
+  uint32_t kvh_off;    // kvh * NH * kRowBytes
+  uint32_t page_bytes; // 16 * n_kv * NH * kRowBytes
 };
 
 // Issues the loads of page `ph` (physical id, wave-uniform): K into
-// registers, V by DMA into slot `slot`.  Returns the page validity.  Exactly
-// 8 vector-memory instructions.
-__device__ __forceinline__ bool issue_page(const Stream& sm, uint32_t ph, int slot, half8 (&k)[4]) {
+// registers, V by DMA into slot `slot` (NH half-slots of kVSlot bytes).
+// Returns the page validity.  Exactly 8 NH vector-memory instructions.
+template <int NH>
+__device__ __forceinline__ bool issue_page(const Stream& sm, uint32_t ph, int slot, half8 (&k)[4 * NH]) {
   const bool valid = ph < sm.num_pages;
   // a missing page reads page 0 (in bounds) and all its tokens are masked
   const size_t base = (size_t)(valid ? ph : 0u) * sm.page_bytes + sm.kvh_off;
   const uint8_t* kb = sm.k_pages + base;
   const uint8_t* vb = sm.v_pages + base;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) k[j] = *reinterpret_cast<const half8*>(kb + sm.koff + 64 * j);
+  for (int j = 0; j < 4 * NH; ++j) k[j] = *reinterpret_cast<const half8*>(kb + sm.koff + 64 * j);
   // V goes through a buffer-resource DMA (MUBUF `lds` form) whose base is this
   // page's row block (wave-uniform).  The FLAT form (global_load_lds) would
   // make the compiler drain all vector loads before any dependent use, since
   // it counts it as a flat access to both global memory and LDS.
   const __amdgpu_buffer_rsrc_t rsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, (int)sm.page_bytes, kBufferFormat);
-  lds_u8* dst = sm.vring + slot * kVSlot;
+  lds_u8* dst = sm.vring + slot * (NH * kVSlot);
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(dst + 1024 * j), 16,
-                                             (int)sm.voff[j], 0, 0, 0);
+  for (int h = 0; h < NH; ++h)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(dst + h * kVSlot + 1024 * j),
+                                               16, (int)(sm.voff[j] + h * kRowBytes), 0, 0, 0);
   return valid;
 }
 
 // Scores of tokens 4g+ii of a page of f16 rows (log2 units), lanes n < REP.
-template <int REP>
-__device__ __forceinline__ void page_scores(const WaveState<REP>& st, const half8 (&k)[4], float (&s)[4]) {
+template <int REP, int NH>
+__device__ __forceinline__ void page_scores(const WaveState<REP, NH>& st, const half8 (&k)[4 * NH], float (&s)[4]) {
   float4v sacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[j], st.qb[j], sacc, 0, 0, 0);
+  for (int j = 0; j < 4 * NH; ++j) sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[j], st.qb[j], sacc, 0, 0, 0);
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) s[ii] = (sacc[ii] + dpp_mov<kDppRowShl + REP>(sacc[ii])) * st.qexp;
 }
@@ -222,18 +230,21 @@ __device__ __forceinline__ float row_up_i32(int x) {
 // int8 product) and the int8 limbs of q.  The products and their sums over
 // the 128 dims are exact integers D_L (|D_L| <= 127*127*128); the score is
 // qsc * ks * (D_0 + D_1/254 + D_2/254^2), lanes n < REP.
-template <int REP>
-__device__ __forceinline__ void page_scores_q8(const WaveState<REP>& st, const u32x4 (&kc)[2], const float4v& ksc,
-                                               float (&s)[4]) {
-  constexpr int NS = WaveState<REP>::kSets;
+template <int REP, int NH>
+__device__ __forceinline__ void page_scores_q8(const WaveState<REP, NH>& st, const u32x4 (&kc)[2 * NH],
+                                               const float4v& ksc, float (&s)[4]) {
+  constexpr int NS = WaveState<REP, NH>::kSets;
   int4v d[NS];
 #pragma unroll
   for (int S = 0; S < NS; ++S) {
     d[S] = int4v{0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      d[S] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(int4v, kc[j]),
-                                                  __builtin_bit_cast(int4v, st.qi[2 * S + j]), d[S], 0, 0, 0);
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        d[S] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(int4v, kc[2 * h + j]),
+                                                    __builtin_bit_cast(int4v, st.qi[2 * NS * h + 2 * S + j]), d[S], 0,
+                                                    0, 0);
   }
   // limb L of head h sits in set (L*REP)/16, lane h + (L*REP)%16
   constexpr int S1 = REP / 16, H1 = REP % 16, S2 = 2 * REP / 16, H2 = 2 * REP % 16;
@@ -253,11 +264,11 @@ __device__ __forceinline__ void page_scores_q8(const WaveState<REP>& st, const u
 // need no clearing: their weights are exact zeros); the weights that
 // multiply V are multiplied by the V scale vsc[ii] (the sums l stay
 // unscaled).
-template <int REP, bool FULL, bool SC = false>
-__device__ __forceinline__ void consume_scores(WaveState<REP>& st, const Stream& sm, float (&s)[4], int slot,
+template <int REP, bool FULL, bool SC = false, int NH = 1>
+__device__ __forceinline__ void consume_scores(WaveState<REP, NH>& st, const Stream& sm, float (&s)[4], int slot,
                                                int tok0, bool valid, int ta, int tb, int g, int n,
                                                float4v vsc = float4v{1.0f, 1.0f, 1.0f, 1.0f}) {
-  lds_u8* vslot = sm.vring + slot * kVSlot;
+  lds_u8* vslot = sm.vring + slot * (NH * kVSlot);
   if constexpr (!FULL && !SC) {
     // rows of masked tokens (and of a missing page) must not carry NaN bits
     // into the matrix product: zero them in the slot
@@ -265,7 +276,9 @@ __device__ __forceinline__ void consume_scores(WaveState<REP>& st, const Stream&
     for (int j = 0; j < 4; ++j) {
       const int t = tok0 + 4 * g + j;
       if (!(valid && t >= ta && t < tb))
-        *(lds_u32x4*)(vslot + (4 * j + g) * kRowBytes + 16 * n) = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+          *(lds_u32x4*)(vslot + h * kVSlot + (4 * j + g) * kRowBytes + 16 * n) = u32x4{0u, 0u, 0u, 0u};
     }
   }
   if constexpr (!FULL) {
@@ -283,7 +296,7 @@ __device__ __forceinline__ void consume_scores(WaveState<REP>& st, const Stream&
     const float alpha = fast_exp2(st.m - m_new);
     st.m = m_new;
     st.l *= alpha;
-    scale_rows<REP>(st, alpha, g);
+    scale_rows<REP, NH>(st, alpha, g);
   }
   float pr[4];
 #pragma unroll
@@ -314,7 +327,7 @@ __device__ __forceinline__ void consume_scores(WaveState<REP>& st, const Stream&
       if (st.vnorm > 0.0f) {
         const float r = st.vnorm * ldexpf(1.0f, -e);  // a power of two: exact
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb)
+        for (int nb = 0; nb < 8 * NH; ++nb)
 #pragma unroll
           for (int q = 0; q < 4; ++q) st.acc[nb][q] *= r;
       }
@@ -338,49 +351,55 @@ __device__ __forceinline__ void consume_scores(WaveState<REP>& st, const Stream&
   // complete (the caller's vmcnt wait); the lgkmcnt wait below, tied to the
   // results, completes the reads before any use and before the next DMA
   // into this slot is issued.
-  const uint32_t vbase = (uint32_t)(size_t)(vslot + sm.vr_off + sm.vr_half);
-  short4v bv[8];
+  // (Half h of a 256-wide head: its own half-slot, accumulators 8h .. 8h+7.)
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) {
-    const uint32_t chunk = ((uint32_t)(2 * nb) + sm.vr_sub) ^ sm.vr_swz;
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[nb]) : "v"(vbase + 16u * chunk) : "memory");
+  for (int h = 0; h < NH; ++h) {
+    const uint32_t vbase = (uint32_t)(size_t)(vslot + h * kVSlot + sm.vr_off + sm.vr_half);
+    short4v bv[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const uint32_t chunk = ((uint32_t)(2 * nb) + sm.vr_sub) ^ sm.vr_swz;
+      asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[nb]) : "v"(vbase + 16u * chunk) : "memory");
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]), "+v"(bv[4]), "+v"(bv[5]), "+v"(bv[6]),
+                   "+v"(bv[7])
+                 :
+                 : "memory");
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+      st.acc[8 * h + nb] =
+          __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]), st.acc[8 * h + nb], 0, 0, 0);
   }
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]), "+v"(bv[4]), "+v"(bv[5]), "+v"(bv[6]),
-                 "+v"(bv[7])
-               :
-               : "memory");
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb)
-    st.acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4, bv[nb]), st.acc[nb], 0, 0, 0);
 }
 
 // One page of f16 rows: K in registers (k), V in LDS slot `slot`.
-template <int REP, bool FULL>
-__device__ __forceinline__ void consume_page(WaveState<REP>& st, const Stream& sm, const half8 (&k)[4], int slot,
-                                             int tok0, bool valid, int ta, int tb, int g, int n) {
+template <int REP, bool FULL, int NH>
+__device__ __forceinline__ void consume_page(WaveState<REP, NH>& st, const Stream& sm, const half8 (&k)[4 * NH],
+                                             int slot, int tok0, bool valid, int ta, int tb, int g, int n) {
   float s[4];
-  page_scores<REP>(st, k, s);
-  consume_scores<REP, FULL>(st, sm, s, slot, tok0, valid, ta, tb, g, n);
+  page_scores<REP, NH>(st, k, s);
+  consume_scores<REP, FULL, false, NH>(st, sm, s, slot, tok0, valid, ta, tb, g, n);
 }
 
 // Loads of one piece that do not depend on the sequence's length, issued
 // oldest first in the order they are needed: the table window (64 entries
 // from table index `tbl`), q and, for a fused call, the new token's row.
-template <int REP>
+template <int REP, int NH = 1>
 struct PieceLoads {
   uint32_t btv;  // lane j: block-table entry tbl + j (0 past the row's end)
   int tbl;
-  float4v qv[8];
-  float2v knew, vnew;
+  float4v qv[8 * NH];      // 8 float4 per 128-dim half
+  float2v knew[NH], vnew[NH];  // new token, half h: elements 128h + 2 lane, +1
 };
 
 // Q8: the order of the Q8A kernel, where lane (g, n) holds dims 32g .. 32g+31
 // of head n % REP (a contiguous 32-dim slice per lane, so that a page row's
 // codes come in two 16-byte loads); otherwise dims 32j + 8g .. 32j + 8g + 7
-// for product j of head n (n < REP) or n - REP (n < 2 REP).
-template <int REP, bool FUSED, bool ROPE, bool Q8 = false>
-__device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh, int tbl, PieceLoads<REP>& pl) {
+// for product j of head n (n < REP) or n - REP (n < 2 REP).  Half h of a
+// 256-wide head: the same, 128h further (qv[8h ..]).
+template <int REP, bool FUSED, bool ROPE, bool Q8 = false, int NH = 1>
+__device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh, int tbl, PieceLoads<REP, NH>& pl) {
   const int lane = (int)(threadIdx.x & (kWave - 1));
   const int g = lane >> 4, n = lane & 15;
   const int e = tbl + lane;
@@ -389,22 +408,30 @@ __device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh,
   const bool qcol = n < 2 * REP;
   // other columns load some head and drop it
   const int hq = Q8 ? n % REP : (qcol ? (n < REP ? n : n - REP) : 0);
-  const float4v* qh = reinterpret_cast<const float4v*>(a.q + ((size_t)s * a.n_heads + (size_t)kvh * REP + hq) * kD +
-                                                      (Q8 ? 32 * g : 8 * g));
+  const float4v* qh = reinterpret_cast<const float4v*>(
+      a.q + ((size_t)s * a.n_heads + (size_t)kvh * REP + hq) * (NH * kD) + (Q8 ? 32 * g : 8 * g));
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    pl.qv[2 * j] = qh[Q8 ? 2 * j : 8 * j];
-    pl.qv[2 * j + 1] = qh[Q8 ? 2 * j + 1 : 8 * j + 1];
-  }
+  for (int h = 0; h < NH; ++h)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pl.qv[8 * h + 2 * j] = qh[32 * h + (Q8 ? 2 * j : 8 * j)];
+      pl.qv[8 * h + 2 * j + 1] = qh[32 * h + (Q8 ? 2 * j + 1 : 8 * j + 1)];
+    }
   // Every piece of a fused call loads the new token's row (the same 1 KiB
   // per sequence and kv head, so the repeats hit L2): a load under a branch
   // would make the compiler wait for it right there.
-  pl.knew = float2v{0.0f, 0.0f};
-  pl.vnew = float2v{0.0f, 0.0f};
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    pl.knew[h] = float2v{0.0f, 0.0f};
+    pl.vnew[h] = float2v{0.0f, 0.0f};
+  }
   if constexpr (FUSED) {
-    const size_t src = ((size_t)s * a.n_kv + kvh) * kD + 2 * lane;
-    pl.knew = *reinterpret_cast<const float2v*>(a.k_new + src);
-    pl.vnew = *reinterpret_cast<const float2v*>(a.v_new + src);
+    const size_t src = ((size_t)s * a.n_kv + kvh) * (NH * kD) + 2 * lane;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      pl.knew[h] = *reinterpret_cast<const float2v*>(a.k_new + src + h * kD);
+      pl.vnew[h] = *reinterpret_cast<const float2v*>(a.v_new + src + h * kD);
+    }
   }
 }
 
@@ -427,8 +454,8 @@ struct PieceOut {
   size_t pbase;
   int pstride;
   // in_lds: partial rows go to the LDS array `lds` instead, row r at
-  // lds + r * (kD + 2): acc[kD], then m, then l.  (A flag, not a null test:
-  // an LDS array may sit at address 0.)
+  // lds + r * (D + 2): acc[D], then m, then l (D the head dim).  (A flag, not
+  // a null test: an LDS array may sit at address 0.)
   bool in_lds = false;
   __attribute__((address_space(3))) float* lds = nullptr;
 };
@@ -436,15 +463,15 @@ struct PieceOut {
 // q -> B operand: column n < REP is hi of head n, REP <= n < 2REP lo of head
 // n-REP, others zero.  Each head is first scaled by 2^-E (E from its max
 // |q*scale|) so hi/lo stay in f16 range; the scores are scaled back by 2^E.
-template <int REP>
-__device__ __forceinline__ void init_wave_state(const DecodeArgs& a, const PieceLoads<REP>& pl, WaveState<REP>& st,
-                                                int n) {
+template <int REP, int NH>
+__device__ __forceinline__ void init_wave_state(const DecodeArgs& a, const PieceLoads<REP, NH>& pl,
+                                                WaveState<REP, NH>& st, int n) {
   const bool qcol = n < 2 * REP;
   {
-    float x[4][8];
+    float x[4 * NH][8];
     float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4 * NH; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float qe = pl.qv[2 * j + (e >> 2)][e & 3];
@@ -457,7 +484,7 @@ __device__ __forceinline__ void init_wave_state(const DecodeArgs& a, const Piece
     const float inv = ldexpf(1.0f, -E);
     st.qexp = ldexpf(1.0f, E);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4 * NH; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float y = x[j][e] * inv;
@@ -466,7 +493,7 @@ __device__ __forceinline__ void init_wave_state(const DecodeArgs& a, const Piece
         st.qb[j][e] = n < REP ? hi : (qcol ? lo : (_Float16)0.0f);
       }
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) st.acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int nb = 0; nb < 8 * NH; ++nb) st.acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
     st.m = kMInit;
     st.l = 0.0f;
     st.vnorm = 0.0f;
@@ -478,48 +505,51 @@ __device__ __forceinline__ void init_wave_state(const DecodeArgs& a, const Piece
 // the head's largest |q*scale| (so |y| <= 127); limb 0 = rint(y), limb 1 =
 // rint(254 r), limb 2 = rint(254 (254 r - limb 1)) with r = y - limb 0, each
 // in [-127, 127]; y = limb0 + limb1/254 + limb2/254^2 to within 0.5/254^2.
-template <int REP>
-__device__ __forceinline__ void init_wave_state_q8(const DecodeArgs& a, const PieceLoads<REP>& pl,
-                                                   WaveState<REP>& st, int n) {
-  constexpr int NS = WaveState<REP>::kSets;
-  float x[32];
+template <int REP, int NH>
+__device__ __forceinline__ void init_wave_state_q8(const DecodeArgs& a, const PieceLoads<REP, NH>& pl,
+                                                   WaveState<REP, NH>& st, int n) {
+  constexpr int NS = WaveState<REP, NH>::kSets;
+  float x[32 * NH];
   float amax = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) {
+  for (int e = 0; e < 32 * NH; ++e) {
     x[e] = pl.qv[e >> 2][e & 3] * a.scale_log2;
     amax = fmaxf(amax, fabsf(x[e]));
   }
-  amax = max_xor16(max_xor32(amax));  // over the head's 128 dims
+  amax = max_xor16(max_xor32(amax));  // over the head's dims
   // a head whose largest |q*scale| is below 2^-100 scores zero (127 / amax
   // could overflow; the products it drops are below 2^-93 |k|)
   const float inv = amax >= 0x1p-100f ? 127.0f / amax : 0.0f;
   st.qsc = amax / 127.0f;
-  uint32_t w[NS][8];
 #pragma unroll
-  for (int S = 0; S < NS; ++S)
+  for (int h = 0; h < NH; ++h) {
+    uint32_t w[NS][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w[S][i] = 0u;
+    for (int S = 0; S < NS; ++S)
 #pragma unroll
-  for (int e = 0; e < 32; ++e) {
-    const float y = x[e] * inv;
-    const float l0 = rintf(y);
-    const float r1 = (y - l0) * 254.0f;
-    const float l1 = rintf(r1);
-    const float l2 = rintf((r1 - l1) * 254.0f);
+      for (int i = 0; i < 8; ++i) w[S][i] = 0u;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const float y = x[32 * h + e] * inv;
+      const float l0 = rintf(y);
+      const float r1 = (y - l0) * 254.0f;
+      const float l1 = rintf(r1);
+      const float l2 = rintf((r1 - l1) * 254.0f);
+#pragma unroll
+      for (int S = 0; S < NS; ++S) {
+        const int c = 16 * S + n;
+        const float v = c < REP ? l0 : (c < 2 * REP ? l1 : (c < 3 * REP ? l2 : 0.0f));
+        w[S][e >> 2] |= ((uint32_t)(int)v & 0xFFu) << (8 * (e & 3));
+      }
+    }
 #pragma unroll
     for (int S = 0; S < NS; ++S) {
-      const int c = 16 * S + n;
-      const float v = c < REP ? l0 : (c < 2 * REP ? l1 : (c < 3 * REP ? l2 : 0.0f));
-      w[S][e >> 2] |= ((uint32_t)(int)v & 0xFFu) << (8 * (e & 3));
+      st.qi[2 * NS * h + 2 * S] = u32x4{w[S][0], w[S][1], w[S][2], w[S][3]};
+      st.qi[2 * NS * h + 2 * S + 1] = u32x4{w[S][4], w[S][5], w[S][6], w[S][7]};
     }
   }
 #pragma unroll
-  for (int S = 0; S < NS; ++S) {
-    st.qi[2 * S] = u32x4{w[S][0], w[S][1], w[S][2], w[S][3]};
-    st.qi[2 * S + 1] = u32x4{w[S][4], w[S][5], w[S][6], w[S][7]};
-  }
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) st.acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int nb = 0; nb < 8 * NH; ++nb) st.acc[nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
   st.m = kMInit;
   st.l = 0.0f;
   st.qexp = 1.0f;
@@ -530,18 +560,19 @@ __device__ __forceinline__ void init_wave_state_q8(const DecodeArgs& a, const Pi
 // The end of a piece: sums over the lanes, then the normalised output rows
 // or the partial rows the piece leaves for a merge.
 // SC (Q8A pages): acc is in units of st.vnorm.
-template <int REP, bool SC = false>
-__device__ __forceinline__ void finish_piece(const DecodeArgs& a, WaveState<REP>& st, int s, int kvh,
+template <int REP, bool SC = false, int NH = 1>
+__device__ __forceinline__ void finish_piece(const DecodeArgs& a, WaveState<REP, NH>& st, int s, int kvh,
                                              const PieceOut& po, int g, int n) {
+  constexpr int D = NH * kD;
   // Denominators: sum this head's lanes over the four 16-lane rows.
   st.l = sum_xor16(sum_xor32(st.l));
   // Numerators: result row r (hi) and r + REP (lo) belong to head r.  After
   // the sums, lanes g == 0 hold heads 0..min(REP,4)-1 and, for REP == 8,
   // lanes g == 1 hold heads 4..7, at dims 16*nb + n.
-  constexpr int NH = REP < 4 ? REP : 4;
-  float o[NH][8];
+  constexpr int HL = REP < 4 ? REP : 4;  // heads a lane writes
+  float o[HL][8 * NH];
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) {
+  for (int nb = 0; nb < 8 * NH; ++nb) {
     if constexpr (REP == 1) {
       o[0][nb] = st.acc[nb][0] + st.acc[nb][1];
     } else if constexpr (REP == 2) {
@@ -558,35 +589,37 @@ __device__ __forceinline__ void finish_piece(const DecodeArgs& a, WaveState<REP>
   // l and m of the heads this lane writes (REP == 8: lanes g == 1 hold heads
   // 4..7), broadcast while every lane is active: DPP reads of inactive lanes
   // return nothing useful.
-  float lsel[NH], msel[NH];
-  static_for<NH>([&](auto c) {
+  float lsel[HL], msel[HL];
+  static_for<HL>([&](auto c) {
     constexpr int ii = decltype(c)::value;
     lsel[ii] = (REP == 8 && g == 1) ? row_value<(4 + ii) % REP>(st.l) : row_value<ii>(st.l);
     msel[ii] = (REP == 8 && g == 1) ? row_value<(4 + ii) % REP>(st.m) : row_value<ii>(st.m);
   });
   if (g == 0 || (REP == 8 && g == 1)) {
     const int hb = REP == 8 ? 4 * g : 0;
-    static_for<NH>([&](auto c) {
+    static_for<HL>([&](auto c) {
       constexpr int ii = decltype(c)::value;
       const float lh = lsel[ii], mh = msel[ii];
       if (po.final) {
         const size_t hrow = (size_t)s * a.n_heads + (size_t)kvh * REP + hb + ii;
         const float inv = lh > 0.0f ? (SC ? st.vnorm : 1.0f) / lh : 0.0f;
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) a.out[hrow * kD + 16 * nb + n] = gated(a, hrow * kD + 16 * nb + n, o[ii][nb] * inv);
+        for (int nb = 0; nb < 8 * NH; ++nb)
+          a.out[hrow * D + 16 * nb + n] = gated(a, hrow * D + 16 * nb + n, o[ii][nb] * inv);
       } else {
         const size_t pidx = po.pbase + (size_t)(hb + ii) * po.pstride;
         if (po.in_lds) {
-          __attribute__((address_space(3))) float* row = po.lds + pidx * (kD + 2);
+          __attribute__((address_space(3))) float* row = po.lds + pidx * (D + 2);
 #pragma unroll
-          for (int nb = 0; nb < 8; ++nb) row[16 * nb + n] = SC ? o[ii][nb] * st.vnorm : o[ii][nb];
+          for (int nb = 0; nb < 8 * NH; ++nb) row[16 * nb + n] = SC ? o[ii][nb] * st.vnorm : o[ii][nb];
           if (n == 0) {
-            row[kD] = mh;
-            row[kD + 1] = lh;
+            row[D] = mh;
+            row[D + 1] = lh;
           }
         } else {
 #pragma unroll
-          for (int nb = 0; nb < 8; ++nb) a.ws_acc[pidx * kD + 16 * nb + n] = SC ? o[ii][nb] * st.vnorm : o[ii][nb];
+          for (int nb = 0; nb < 8 * NH; ++nb)
+            a.ws_acc[pidx * D + 16 * nb + n] = SC ? o[ii][nb] * st.vnorm : o[ii][nb];
           if (n == 0) {
             a.ws_ml[pidx * 2 + 0] = mh;
             a.ws_ml[pidx * 2 + 1] = lh;
@@ -605,20 +638,21 @@ __device__ __forceinline__ void finish_piece(const DecodeArgs& a, WaveState<REP>
 // the page data it reads.  `tbl_ok`: pl.btv holds the table window from
 // pl.tbl; the window is reloaded when that is not so or does not cover the
 // piece's first page.
-template <int REP, bool FUSED, int DEPTH, bool ROPE>
-__device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, lds_u8* newtok, PieceLoads<REP>& pl,
-                                          bool tbl_ok, int s, int kvh, int ta, int tb, bool append, int pos,
-                                          const PieceOut& po, lds_u8* rope_table = nullptr) {
+template <int REP, bool FUSED, int DEPTH, bool ROPE, int NH = 1>
+__device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, lds_u8* newtok,
+                                          PieceLoads<REP, NH>& pl, bool tbl_ok, int s, int kvh, int ta, int tb,
+                                          bool append, int pos, const PieceOut& po, lds_u8* rope_table = nullptr) {
   const int lane = (int)(threadIdx.x & (kWave - 1));
   const int g = lane >> 4, n = lane & 15;
+  constexpr int kRow = NH * kRowBytes;  // one (token, kv head) row of f16
 
   Stream sm;
   sm.k_pages = a.k_pages;
   sm.v_pages = a.v_pages;
   sm.vring = vring;
   sm.num_pages = a.num_pages;
-  sm.kvh_off = (uint32_t)kvh * kRowBytes;
-  const uint32_t rs = (uint32_t)a.n_kv * kRowBytes;  // bytes between token rows
+  sm.kvh_off = (uint32_t)kvh * kRow;
+  const uint32_t rs = (uint32_t)a.n_kv * kRow;  // bytes between token rows
   sm.page_bytes = kPage * rs;
   sm.koff = (uint32_t)n * rs + 16u * g;
 #pragma unroll
@@ -666,17 +700,21 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
   // The first DEPTH pages are issued unconditionally, for the same reason: a
   // piece with fewer pages loads pool page 0 as a stand-in (in bounds, never
   // consumed; drained before the epilogue).
-  half8 kbuf[DEPTH][4];
+  half8 kbuf[DEPTH][4 * NH];
   bool vld[DEPTH];
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) vld[d] = issue_page(sm, phys_of(d), d, kbuf[d]) && npg > d;
+  for (int d = 0; d < DEPTH; ++d) vld[d] = issue_page<NH>(sm, phys_of(d), d, kbuf[d]) && npg > d;
   // Uses of q and of the new token start here, with the pages in flight.
-  asm volatile(""
-               : "+v"(pl.qv[0]), "+v"(pl.qv[1]), "+v"(pl.qv[2]), "+v"(pl.qv[3]), "+v"(pl.qv[4]), "+v"(pl.qv[5]),
-                 "+v"(pl.qv[6]), "+v"(pl.qv[7]), "+v"(pl.knew), "+v"(pl.vnew));
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+    asm volatile(""
+                 : "+v"(pl.qv[8 * h + 0]), "+v"(pl.qv[8 * h + 1]), "+v"(pl.qv[8 * h + 2]), "+v"(pl.qv[8 * h + 3]),
+                   "+v"(pl.qv[8 * h + 4]), "+v"(pl.qv[8 * h + 5]), "+v"(pl.qv[8 * h + 6]), "+v"(pl.qv[8 * h + 7]),
+                   "+v"(pl.knew[h]), "+v"(pl.vnew[h]));
 
   // Fused RoPE: turn q (every piece) and the new K (the appending piece) by
-  // the new token's position before they are used.
+  // the new token's position before they are used.  A rotary width of 64 or
+  // 128 lies in the first 128 dims (half 0 of a 256-wide head).
   if constexpr (FUSED && ROPE) {
     {
       const float fpos = (float)max(pos, 0);
@@ -725,8 +763,8 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
         // half/2 lanes away
         const int mlane = a.rope_half / 2;
         const bool first = (lane & mlane) == 0;
-        const float p0 = __shfl_xor(pl.knew.x, mlane, kWave);
-        const float p1 = __shfl_xor(pl.knew.y, mlane, kWave);
+        const float p0 = __shfl_xor(pl.knew[0].x, mlane, kWave);
+        const float p1 = __shfl_xor(pl.knew[0].y, mlane, kWave);
         const bool rotated = a.rope_half == 64 || lane < 32;  // half 32: elements 64.. stay
         if (rotated) {
           // its new-K pair is elements 2*(lane % (half/2)) + {0, 1}
@@ -736,8 +774,8 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
           rope_sincos(fpos * kinv.x, &sn0, &cs0);
           rope_sincos(fpos * kinv.y, &sn1, &cs1);
           // first half: x*cos - partner*sin; second half: partner*sin + x*cos
-          pl.knew.x = first ? pl.knew.x * cs0 - p0 * sn0 : p0 * sn0 + pl.knew.x * cs0;
-          pl.knew.y = first ? pl.knew.y * cs1 - p1 * sn1 : p1 * sn1 + pl.knew.y * cs1;
+          pl.knew[0].x = first ? pl.knew[0].x * cs0 - p0 * sn0 : p0 * sn0 + pl.knew[0].x * cs0;
+          pl.knew[0].y = first ? pl.knew[0].y * cs1 - p1 * sn1 : p1 * sn1 + pl.knew[0].y * cs1;
         }
       }
     }
@@ -747,55 +785,67 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
   // stage it in LDS for substitution.
   if constexpr (FUSED) {
     if (append) {
-      const uint32_t kb = to_f16_bits(pl.knew.x) | (to_f16_bits(pl.knew.y) << 16);
-      const uint32_t vb = to_f16_bits(pl.vnew.x) | (to_f16_bits(pl.vnew.y) << 16);
-      ((__attribute__((address_space(3))) uint32_t*)newtok)[lane] = kb;
-      ((__attribute__((address_space(3))) uint32_t*)(newtok + kRowBytes))[lane] = vb;
+      typedef __attribute__((address_space(3))) uint32_t lds_u32;
+      uint32_t kb[NH], vb[NH];
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        kb[h] = to_f16_bits(pl.knew[h].x) | (to_f16_bits(pl.knew[h].y) << 16);
+        vb[h] = to_f16_bits(pl.vnew[h].x) | (to_f16_bits(pl.vnew[h].y) << 16);
+        ((lds_u32*)newtok)[64 * h + lane] = kb[h];
+        ((lds_u32*)(newtok + kRow))[64 * h + lane] = vb[h];
+      }
       const int ip = pos / kPage - base - win;  // the page is normally in the table window
       const uint32_t ph = ip >= 0 && ip < 64 && pos / kPage - pg_first < npg ? __builtin_amdgcn_readlane(pl.btv, ip)
                                                                               : bt_row[pos / kPage];
       if (ph < a.num_pages) {
         const size_t row = ((size_t)ph * kPage + (size_t)(pos % kPage)) * a.n_kv + kvh;
-        *reinterpret_cast<uint32_t*>(a.k_pages_w + row * kRowBytes + 4 * lane) = kb;
-        *reinterpret_cast<uint32_t*>(a.v_pages_w + row * kRowBytes + 4 * lane) = vb;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+          *reinterpret_cast<uint32_t*>(a.k_pages_w + row * kRow + h * kRowBytes + 4 * lane) = kb[h];
+          *reinterpret_cast<uint32_t*>(a.v_pages_w + row * kRow + h * kRowBytes + 4 * lane) = vb[h];
+        }
       }
     }
   }
   const bool attend_new = append && pos >= ta;
 
-  WaveState<REP> st;
-  init_wave_state<REP>(a, pl, st, n);
+  WaveState<REP, NH> st;
+  init_wave_state<REP, NH>(a, pl, st, n);
 
   // Page i: wait for its loads (those of the pages issued after it may stay
   // in flight), patch in the new token if it lives there, consume, refill the
   // slot with page i + DEPTH.  `steady` asserts pages i+1 .. i+DEPTH exist,
   // which lets the compiler's wait counting see exactly DEPTH pages in
   // flight; the other steps use the masked consume only.
-  auto step = [&](int i, half8(&k)[4], bool& valid, int slot, bool steady) {
+  auto step = [&](int i, half8(&k)[4 * NH], bool& valid, int slot, bool steady) {
     const int ahead = steady ? DEPTH - 1 : min(npg - 1 - i, DEPTH - 1);  // pages issued after page i
-    if (ahead >= 3) wait_vmcnt<24>();
-    else if (ahead == 2) wait_vmcnt<16>();
-    else if (ahead == 1) wait_vmcnt<8>();
+    constexpr int kLoads = 8 * NH;  // vector-memory instructions per page
+    if (ahead >= 3) wait_vmcnt<3 * kLoads>();
+    else if (ahead == 2) wait_vmcnt<2 * kLoads>();
+    else if (ahead == 1) wait_vmcnt<kLoads>();
     else wait_vmcnt<0>();
     const int tok0 = (pg_first + i) * kPage;
     if (attend_new && pos / kPage == pg_first + i) {
       const int t = pos % kPage;
       if (n == t) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) k[j] = *(lds_half8*)(newtok + 64 * j + 16 * g);
+        for (int j = 0; j < 4 * NH; ++j) k[j] = *(lds_half8*)(newtok + 64 * j + 16 * g);
       }
       const int R = 4 * (t & 3) + (t >> 2);
       if (g == (R & 3)) {
-        lds_u8* vslot = vring + slot * kVSlot;
-        *(lds_u32x4*)(vslot + R * kRowBytes + 16 * n) = *(lds_u32x4*)(newtok + kRowBytes + 16 * ((uint32_t)n ^ v_swz(R)));
+        lds_u8* vslot = vring + slot * (NH * kVSlot);
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+          *(lds_u32x4*)(vslot + h * kVSlot + R * kRowBytes + 16 * n) =
+              *(lds_u32x4*)(newtok + kRow + h * kRowBytes + 16 * ((uint32_t)n ^ v_swz(R)));
       }
       __builtin_amdgcn_wave_barrier();
     }
     if (steady && valid && tok0 >= ta && tok0 + kPage <= tb)
-      consume_page<REP, true>(st, sm, k, slot, tok0, valid, ta, tb, g, n);
+      consume_page<REP, true, NH>(st, sm, k, slot, tok0, valid, ta, tb, g, n);
     else
-      consume_page<REP, false>(st, sm, k, slot, tok0, valid, ta, tb, g, n);
-    if (steady || i + DEPTH < npg) valid = issue_page(sm, phys_of(i + DEPTH), slot, k);
+      consume_page<REP, false, NH>(st, sm, k, slot, tok0, valid, ta, tb, g, n);
+    if (steady || i + DEPTH < npg) valid = issue_page<NH>(sm, phys_of(i + DEPTH), slot, k);
   };
   int i = 0;
   for (; i + 2 * DEPTH - 1 < npg; i += DEPTH) {
@@ -810,7 +860,7 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
   // the slots and the staged token are reused by the next piece
   __builtin_amdgcn_wave_barrier();
 
-  finish_piece<REP>(a, st, s, kvh, po, g, n);
+  finish_piece<REP, false, NH>(a, st, s, kvh, po, g, n);
 }
 
 // ---------------------------------------------------------------------------
@@ -847,24 +897,60 @@ __device__ __forceinline__ half8 i8x8_to_f16(uint2v w) {
 
 // One Q8A page in flight: K codes of token n, dims 32g .. 32g+31 (int8
 // product j takes dims 32g + 16j ..); V codes of token 8h + lane/8, dims
-// 16 (lane%8) .. +15 for load h; the K and V scales of token 4g + n%4.
+// 16 (lane%8) .. +15 for load h; the K and V scales of token 4g + n%4.  Half
+// hh of a 256-wide head: the same, 128hh further (k[2hh ..], v[2hh ..]).
+template <int NH>
 struct PageQ8 {
-  u32x4 k[2];
-  u32x4 v[2];
+  u32x4 k[2 * NH];
+  u32x4 v[2 * NH];
   float ks, vs;
 };
+
+// RoPE on the Q8A lane order (lane (g, n): dims 32g .. 32g+31 of half 0):
+// rotary width 2H (H = 32: dims 0..63, H = 64: dims 0..127), dim i < H pairs
+// with i + H, which lives in lane g ^ (H/32) at the same element; the angle of
+// dim i is pos * inv_freq[i % H] (the table in LDS).
+__device__ __forceinline__ void rope_q8_lanes(float4v (&qv)[8], int half, float fpos, const lds_u8* rope_table,
+                                              int g) {
+  typedef __attribute__((address_space(3))) float lds_f32;
+  const lds_f32* tq = (const lds_f32*)rope_table;
+  const bool h64 = half == 64;
+  const bool rotated = h64 || g < 2;
+  const bool first = h64 ? g < 2 : g == 0;
+  const int fb = h64 ? 32 * (g & 1) : 0;  // first table index of this lane's 32 dims
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const float x = qv[e >> 2][e & 3];
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false,
+                                                      false);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false,
+                                                      false);
+    // the value of lane ^ 16 / lane ^ 32 (the swaps return the pair in lane order)
+    const int lane = (int)(threadIdx.x & (kWave - 1));
+    const float p16 = __builtin_bit_cast(float, (int)((lane & 16) ? r16[0] : r16[1]));
+    const float p32 = __builtin_bit_cast(float, (int)((lane & 32) ? r32[0] : r32[1]));
+    const float p = h64 ? p32 : p16;
+    float sn, cs;
+    rope_sincos(fpos * tq[fb + e], &sn, &cs);
+    const float y = first ? x * cs - p * sn : p * sn + x * cs;
+    qv[e >> 2][e & 3] = rotated ? y : x;
+  }
+}
 
 // FUSED: when `append`, this piece holds position pos = L-1; the wave
 // quantizes the new token (the quantizer of append_kernel: absmax / 127,
 // IEEE divide, round half away from zero, clamp 127), stores its codes and
 // scales to the slot, and substitutes them into the page data it loaded.
-template <int REP, int DEPTH, bool FUSED>
-__device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot, lds_u8* newtok, PieceLoads<REP>& pl,
-                                             bool tbl_ok, int s, int kvh, int ta, int tb, bool append, int pos,
-                                             const PieceOut& po) {
+// ROPE (fused calls): q and the new K are turned by pos first, so the codes
+// stored are those of the rotated K (the engine's rotate, then attend).
+template <int REP, int DEPTH, bool FUSED, int NH = 1, bool ROPE = false>
+__device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot, lds_u8* newtok,
+                                             PieceLoads<REP, NH>& pl, bool tbl_ok, int s, int kvh, int ta, int tb,
+                                             bool append, int pos, const PieceOut& po,
+                                             lds_u8* rope_table = nullptr) {
   const int lane = (int)(threadIdx.x & (kWave - 1));
   const int g = lane >> 4, n = lane & 15;
-  constexpr int kRowQ8 = kD;  // one (token, kv head) row of int8 codes
+  constexpr int kRowQ8 = NH * kD;  // one (token, kv head) row of int8 codes
 
   Stream sm{};
   sm.vring = vslot;
@@ -920,10 +1006,11 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
   };
   asm volatile("" : "+v"(pl.btv) : : "memory");
 
-  // exactly 6 vector-memory loads; a missing page reads page 0 (masked).
-  // Buffer resources on the page's rows and scales (scalar bases, 32-bit lane
-  // offsets), each ending where this kv head's last row of the page does.
-  auto issue = [&](uint32_t ph, PageQ8& pg) -> bool {
+  // exactly 4 NH + 2 vector-memory loads; a missing page reads page 0
+  // (masked).  Buffer resources on the page's rows and scales (scalar bases,
+  // 32-bit lane offsets), each ending where this kv head's last row of the
+  // page does.
+  auto issue = [&](uint32_t ph, PageQ8<NH>& pg) -> bool {
     const bool valid = ph < a.num_pages;
     const size_t pb = (size_t)(valid ? ph : 0u);
     const int rows = (int)(page_bytes - kvh_off);
@@ -938,46 +1025,96 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
     const __amdgpu_buffer_rsrc_t vsr =
         __builtin_amdgcn_make_buffer_rsrc((void*)(a.v_scales + sb), (short)0, sbytes, kBufferFormat);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      pg.k[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)(koff + 16u * h), 0, 0));
+    for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      pg.v[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, (int)voff[h], 0, 0));
+      for (int h = 0; h < 2; ++h)
+        pg.k[2 * hh + h] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)(koff + kD * hh + 16u * h), 0, 0));
+#pragma unroll
+    for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        pg.v[2 * hh + h] =
+            __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, (int)(voff[h] + kD * hh), 0, 0));
     pg.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ksr, (int)(4u * soff), 0, 0));
     pg.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vsr, (int)(4u * soff), 0, 0));
     return valid;
   };
 
-  PageQ8 pbuf[DEPTH];
+  PageQ8<NH> pbuf[DEPTH];
   bool vld[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) vld[d] = issue(phys_of(d), pbuf[d]) && npg > d;
-  asm volatile(""
-               : "+v"(pl.qv[0]), "+v"(pl.qv[1]), "+v"(pl.qv[2]), "+v"(pl.qv[3]), "+v"(pl.qv[4]), "+v"(pl.qv[5]),
-                 "+v"(pl.qv[6]), "+v"(pl.qv[7]), "+v"(pl.knew), "+v"(pl.vnew));
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+    asm volatile(""
+                 : "+v"(pl.qv[8 * h + 0]), "+v"(pl.qv[8 * h + 1]), "+v"(pl.qv[8 * h + 2]), "+v"(pl.qv[8 * h + 3]),
+                   "+v"(pl.qv[8 * h + 4]), "+v"(pl.qv[8 * h + 5]), "+v"(pl.qv[8 * h + 6]), "+v"(pl.qv[8 * h + 7]),
+                   "+v"(pl.knew[h]), "+v"(pl.vnew[h]));
 
-  // Fused append: quantize the new token (lane: elements 2*lane, 2*lane+1),
-  // store codes and scales to its slot, stage the codes in LDS.
+  // Fused RoPE: turn q and, in the appending piece, the new K (the f16
+  // kernels' lane order for it: elements 2 lane, 2 lane + 1 of half 0) by the
+  // new token's position.
+  if constexpr (FUSED && ROPE) {
+    const float fpos = (float)max(pos, 0);
+    float4v q0[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q0[j] = pl.qv[j];
+    rope_q8_lanes(q0, a.rope_half, fpos, rope_table, g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pl.qv[j] = q0[j];
+    if (append) {
+      const int mlane = a.rope_half / 2;
+      const bool first = (lane & mlane) == 0;
+      const float p0 = __shfl_xor(pl.knew[0].x, mlane, kWave);
+      const float p1 = __shfl_xor(pl.knew[0].y, mlane, kWave);
+      const bool rotated = a.rope_half == 64 || lane < 32;
+      if (rotated) {
+        typedef __attribute__((address_space(3))) float2v lds_float2v;
+        const float2v kinv = ((const lds_float2v*)rope_table)[lane & (mlane - 1)];
+        float sn0, cs0, sn1, cs1;
+        rope_sincos(fpos * kinv.x, &sn0, &cs0);
+        rope_sincos(fpos * kinv.y, &sn1, &cs1);
+        pl.knew[0].x = first ? pl.knew[0].x * cs0 - p0 * sn0 : p0 * sn0 + pl.knew[0].x * cs0;
+        pl.knew[0].y = first ? pl.knew[0].y * cs1 - p1 * sn1 : p1 * sn1 + pl.knew[0].y * cs1;
+      }
+    }
+  }
+
+  // Fused append: quantize the new token (lane: elements 2*lane, 2*lane+1 of
+  // each half), store codes and scales to its slot, stage the codes in LDS.
   float new_ks = 1.0f, new_vs = 1.0f;
   if constexpr (FUSED) {
     if (append) {
-      auto quant = [&](float2v x, float& sc) -> uint32_t {
-        const float amax = group_max<kWave>(fmaxf(fabsf(x.x), fabsf(x.y)));
+      auto quant = [&](const float2v (&x)[NH], float& sc, uint32_t (&c)[NH]) {
+        float m = 0.0f;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) m = fmaxf(m, fmaxf(fabsf(x[h].x), fabsf(x[h].y)));
+        const float amax = group_max<kWave>(m);
         sc = amax == 0.0f ? 1.0f : amax / 127.0f;
-        return ((uint32_t)to_q8(x.x, sc) & 0xFFu) | (((uint32_t)to_q8(x.y, sc) & 0xFFu) << 8);
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+          c[h] = ((uint32_t)to_q8(x[h].x, sc) & 0xFFu) | (((uint32_t)to_q8(x[h].y, sc) & 0xFFu) << 8);
       };
-      const uint32_t kc = quant(pl.knew, new_ks);
-      const uint32_t vc = quant(pl.vnew, new_vs);
+      uint32_t kc[NH], vcd[NH];
+      quant(pl.knew, new_ks, kc);
+      quant(pl.vnew, new_vs, vcd);
       typedef __attribute__((address_space(3))) uint16_t lds_u16;
-      ((lds_u16*)newtok)[lane] = (uint16_t)kc;
-      ((lds_u16*)(newtok + kRowQ8))[lane] = (uint16_t)vc;
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        ((lds_u16*)newtok)[64 * h + lane] = (uint16_t)kc[h];
+        ((lds_u16*)(newtok + kRowQ8))[64 * h + lane] = (uint16_t)vcd[h];
+      }
       const int ip = pos / kPage - base - win;  // the page is normally in the table window
       const uint32_t ph = ip >= 0 && ip < 64 && pos / kPage - pg_first < npg ? __builtin_amdgcn_readlane(pl.btv, ip)
                                                                               : bt_row[pos / kPage];
       if (ph < a.num_pages) {
         const size_t row = ((size_t)ph * kPage + (size_t)(pos % kPage)) * a.n_kv + kvh;
-        *reinterpret_cast<uint16_t*>(a.k_pages_w + row * kRowQ8 + 2 * lane) = (uint16_t)kc;
-        *reinterpret_cast<uint16_t*>(a.v_pages_w + row * kRowQ8 + 2 * lane) = (uint16_t)vc;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+          *reinterpret_cast<uint16_t*>(a.k_pages_w + row * kRowQ8 + kD * h + 2 * lane) = (uint16_t)kc[h];
+          *reinterpret_cast<uint16_t*>(a.v_pages_w + row * kRowQ8 + kD * h + 2 * lane) = (uint16_t)vcd[h];
+        }
         if (lane == 0) {
           a.k_scales_w[row] = new_ks;
           a.v_scales_w[row] = new_vs;
@@ -988,14 +1125,15 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
   }
   const bool attend_new = FUSED && append && pos >= ta;
 
-  WaveState<REP> st;
-  init_wave_state_q8<REP>(a, pl, st, n);
+  WaveState<REP, NH> st;
+  init_wave_state_q8<REP, NH>(a, pl, st, n);
 
-  auto step = [&](int i, PageQ8& pg, bool& valid, bool steady) {
+  auto step = [&](int i, PageQ8<NH>& pg, bool& valid, bool steady) {
     const int ahead = steady ? DEPTH - 1 : min(npg - 1 - i, DEPTH - 1);  // pages issued after page i
-    if (ahead >= 3) wait_vmcnt<18>();
-    else if (ahead == 2) wait_vmcnt<12>();
-    else if (ahead == 1) wait_vmcnt<6>();
+    constexpr int kLoads = 4 * NH + 2;  // vector-memory loads per page
+    if (ahead >= 3) wait_vmcnt<3 * kLoads>();
+    else if (ahead == 2) wait_vmcnt<2 * kLoads>();
+    else if (ahead == 1) wait_vmcnt<kLoads>();
     else wait_vmcnt<0>();
     const int tok0 = (pg_first + i) * kPage;
     if (attend_new && pos / kPage == pg_first + i) {
@@ -1004,21 +1142,27 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
       const int t = pos % kPage;
       if (n == t) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) pg.k[h] = *(const lds_u32x4*)(newtok + 32 * g + 16 * h);
+        for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) pg.k[2 * hh + h] = *(const lds_u32x4*)(newtok + kD * hh + 32 * g + 16 * h);
       }
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        if (8 * h + (lane >> 3) == t) pg.v[h] = *(const lds_u32x4*)(newtok + kRowQ8 + 16 * vc);
+      for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          if (8 * h + (lane >> 3) == t) pg.v[2 * hh + h] = *(const lds_u32x4*)(newtok + kRowQ8 + kD * hh + 16 * vc);
       if (4 * g + (n & 3) == t) {
         pg.ks = new_ks;
         pg.vs = new_vs;
       }
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      *(lds_half8*)(vslot + vlds[h][0]) = i8x8_to_f16(uint2v{pg.v[h][0], pg.v[h][1]});
-      *(lds_half8*)(vslot + vlds[h][1]) = i8x8_to_f16(uint2v{pg.v[h][2], pg.v[h][3]});
-    }
+    for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        *(lds_half8*)(vslot + hh * kVSlot + vlds[h][0]) = i8x8_to_f16(uint2v{pg.v[2 * hh + h][0], pg.v[2 * hh + h][1]});
+        *(lds_half8*)(vslot + hh * kVSlot + vlds[h][1]) = i8x8_to_f16(uint2v{pg.v[2 * hh + h][2], pg.v[2 * hh + h][3]});
+      }
     // scales of tokens 4g+ii: lane 4*(n/4) + ii of this row holds them
     float4v ksc, vsc;
     ksc[0] = dpp_mov<0x00>(pg.ks);
@@ -1030,11 +1174,11 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
     vsc[2] = dpp_mov<0xAA>(pg.vs);
     vsc[3] = dpp_mov<0xFF>(pg.vs);
     float sc[4];
-    page_scores_q8<REP>(st, pg.k, ksc, sc);
+    page_scores_q8<REP, NH>(st, pg.k, ksc, sc);
     if (steady && valid && tok0 >= ta && tok0 + kPage <= tb)
-      consume_scores<REP, true, true>(st, sm, sc, 0, tok0, valid, ta, tb, g, n, vsc);
+      consume_scores<REP, true, true, NH>(st, sm, sc, 0, tok0, valid, ta, tb, g, n, vsc);
     else
-      consume_scores<REP, false, true>(st, sm, sc, 0, tok0, valid, ta, tb, g, n, vsc);
+      consume_scores<REP, false, true, NH>(st, sm, sc, 0, tok0, valid, ta, tb, g, n, vsc);
     if (steady || i + DEPTH < npg) valid = issue(phys_of(i + DEPTH), pg);
   };
   int i = 0;
@@ -1047,24 +1191,24 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
     if (i + d < npg) step(i + d, pbuf[d % DEPTH], vld[d % DEPTH], false);
   wait_vmcnt<0>();  // stand-in pages of a piece with fewer than DEPTH pages
   __builtin_amdgcn_wave_barrier();
-  finish_piece<REP, true>(a, st, s, kvh, po, g, n);
+  finish_piece<REP, true, NH>(a, st, s, kvh, po, g, n);
 }
 
 // Split-K schedule: block (kv head, partition, sequence) attends one
 // partition of `split` tokens.  Partial rows: [sequence][head][partition].
-template <int REP, bool FUSED, bool ROPE>
+template <int REP, bool FUSED, bool ROPE, int NH = 1>
 __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
-  __shared__ __attribute__((aligned(16))) uint8_t vring_[2 * kVSlot];
-  __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
+  __shared__ __attribute__((aligned(16))) uint8_t vring_[2 * NH * kVSlot];
+  __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * NH * kRowBytes];  // K row, V row (f16)
   const int kvh = blockIdx.x, part = blockIdx.y, s = blockIdx.z;
   // The table window guesses that the partitions start at position 0 (no
   // sliding window), so that every load of the piece is issued before the
   // sequence's length is known; a wrong guess reloads it.
-  PieceLoads<REP> pl;
+  PieceLoads<REP, NH> pl;
   __shared__ __attribute__((aligned(16))) uint8_t rope_table_[ROPE ? 256 : 16];
   stage_rope_table<ROPE>(a, (lds_u8*)rope_table_);
-  piece_loads<REP, FUSED, ROPE>(a, s, kvh, part * (a.split / kPage), pl);
+  piece_loads<REP, FUSED, ROPE, false, NH>(a, s, kvh, part * (a.split / kPage), pl);
   const SeqWindow w = seq_window<FUSED>(a, s);
   if (part >= w.nparts) return;  // wave-uniform
   const int jp = w.jf + part;
@@ -1074,8 +1218,8 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
   po.final = w.nparts == 1;
   po.pbase = ((size_t)s * a.n_heads + (size_t)kvh * REP) * a.max_parts + part;
   po.pstride = a.max_parts;
-  run_piece<REP, FUSED, 2, ROPE>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, w.jf == 0, s, kvh, ta, tb,
-                        FUSED && part == w.nparts - 1 && w.L > 0, w.L - 1, po, (lds_u8*)rope_table_);
+  run_piece<REP, FUSED, 2, ROPE, NH>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, w.jf == 0, s, kvh, ta, tb,
+                                     FUSED && part == w.nparts - 1 && w.L > 0, w.L - 1, po, (lds_u8*)rope_table_);
 }
 
 // ---------------------------------------------------------------------------
@@ -1175,12 +1319,12 @@ __device__ __forceinline__ int sk_chunk(int total, int n_waves) {
   return max(kSkMinPages, (total + n_waves - 1) / n_waves);
 }
 
-template <int REP, bool FUSED, int DEPTH, bool ROPE, bool Q8 = false>
+template <int REP, bool FUSED, int DEPTH, bool ROPE, bool Q8 = false, int NH = 1>
 __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
-  static_assert(!Q8 || !ROPE, "Q8A pages: RoPE runs as a pass before the kernel");
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
-  __shared__ __attribute__((aligned(16))) uint8_t vring_[DEPTH * kVSlot];
-  __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * kRowBytes];  // K row, V row (f16)
+  constexpr int kSlots = Q8 ? 1 : DEPTH;  // Q8A: V is written to its slot when it is used
+  __shared__ __attribute__((aligned(16))) uint8_t vring_[kSlots * NH * kVSlot];
+  __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * NH * kRowBytes];  // K row, V row (f16)
   __shared__ __attribute__((aligned(16))) uint8_t rope_table_[ROPE ? 256 : 16];
   stage_rope_table<ROPE>(a, (lds_u8*)rope_table_);
   const int wv = blockIdx.x;
@@ -1227,21 +1371,20 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
       const int wa = seg0 / chunk;
       desc = make_int4(s, kvh, wa, (wv - wa + 1) * 2 + (seg0 == wa * chunk ? 0 : 1));
     }
-    PieceLoads<REP> pl;
-    piece_loads<REP, FUSED, ROPE, Q8>(a, s, kvh, pg0 + i0, pl);
+    PieceLoads<REP, NH> pl;
+    piece_loads<REP, FUSED, ROPE, Q8, NH>(a, s, kvh, pg0 + i0, pl);
     PieceOut po;
     po.final = i0 == 0 && i1 == np;
     po.pbase = ((size_t)wv * 2 + slot) * REP;
     po.pstride = 1;
     if constexpr (Q8)
-      run_piece_q8<REP, DEPTH, FUSED>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh,
-                                      max(p0, (pg0 + i0) * kPage), min(L, (pg0 + i1) * kPage),
-                                      FUSED && i1 == np && L > 0, L - 1, po);
+      run_piece_q8<REP, DEPTH, FUSED, NH, ROPE>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh,
+                                                max(p0, (pg0 + i0) * kPage), min(L, (pg0 + i1) * kPage),
+                                                FUSED && i1 == np && L > 0, L - 1, po, (lds_u8*)rope_table_);
     else
-      run_piece<REP, FUSED, DEPTH, ROPE>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh,
-                                       max(p0, (pg0 + i0) * kPage),
-                          min(L, (pg0 + i1) * kPage), FUSED && i1 == np && L > 0, L - 1, po,
-                          (lds_u8*)rope_table_);
+      run_piece<REP, FUSED, DEPTH, ROPE, NH>(a, (lds_u8*)vring_, (lds_u8*)newtok_, pl, true, s, kvh,
+                                             max(p0, (pg0 + i0) * kPage), min(L, (pg0 + i1) * kPage),
+                                             FUSED && i1 == np && L > 0, L - 1, po, (lds_u8*)rope_table_);
     cur = pend;
     slot = 1;
   }
@@ -1252,23 +1395,24 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
 // that segment began in an earlier wave (the descriptor the decode kernel
 // left), and writes zeros for the empty windows of sequences w, w + W, ...
 // Wave h of the block merges query heads h, h + 4, ... of the segment.
-template <int REP, bool FUSED>
+template <int REP, bool FUSED, int NH = 1>
 __global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
-  constexpr int C = kD / kWave;
+  constexpr int D = NH * kD;
+  constexpr int C = D / kWave;
   const int w = blockIdx.x, wv = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int4 d = a.sk_desc[w];
   for (int s = w; s < n_seq; s += n_waves) {  // block-uniform
     if (sk_fields<FUSED>(a, s, n_seq).np == 0)
-      for (int i = threadIdx.x; i < a.n_heads * kD; i += kBlock) a.out[(size_t)s * a.n_heads * kD + i] = 0.0f;
+      for (int i = threadIdx.x; i < a.n_heads * D; i += kBlock) a.out[(size_t)s * a.n_heads * D + i] = 0.0f;
   }
   if (d.w == 0) return;
   const int s = d.x, kvh = d.y, wa = d.z, nw = d.w >> 1, first_slot = d.w & 1;
   for (int h = wv; h < REP; h += kWavesPerBlock) {
     float M, Ls, A[C];
-    merge_wave<kD, 1, 8>(reinterpret_cast<const float2*>(a.ws_ml), a.ws_acc, 0, nw,
-                         [=](int j) { return ((size_t)(wa + j) * 2 + (j == 0 ? first_slot : 0)) * REP + h; },
-                         M, Ls, A);
-    const size_t row = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * kD;
+    merge_wave<D, 1, 8>(reinterpret_cast<const float2*>(a.ws_ml), a.ws_acc, 0, nw,
+                        [=](int j) { return ((size_t)(wa + j) * 2 + (j == 0 ? first_slot : 0)) * REP + h; },
+                        M, Ls, A);
+    const size_t row = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * D;
 #pragma unroll
     for (int c = 0; c < C; ++c)
       a.out[row + c * kWave + lane] = gated(a, row + c * kWave + lane, Ls > 0.0f ? A[c] / Ls : 0.0f);
@@ -1334,15 +1478,16 @@ __device__ __forceinline__ WgSeg wg_seg_at(const DecodeArgs& a, int n_seq, int n
   return x;
 }
 
-template <int REP, bool FUSED, int DEPTH, bool ROPE, bool Q8, int NW>
+template <int REP, bool FUSED, int DEPTH, bool ROPE, bool Q8, int NW, int NH = 1>
 __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg) {
-  static_assert(!Q8 || !ROPE, "Q8A pages: RoPE runs as a pass before the kernel");
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
   constexpr int kSlots = Q8 ? 1 : DEPTH;
-  constexpr int kRow = kD + 2;                  // an LDS partial row: acc, m, l
+  constexpr int D = NH * kD;                    // head dim
+  constexpr int CL = D / kWave;                 // elements a lane merges per row
+  constexpr int kRow = D + 2;                   // an LDS partial row: acc, m, l
   typedef __attribute__((address_space(3))) float lds_f32;
-  __shared__ __attribute__((aligned(16))) uint8_t vring_[NW][kSlots * kVSlot];
-  __shared__ __attribute__((aligned(16))) uint8_t newtok_[NW][2 * kRowBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vring_[NW][kSlots * NH * kVSlot];
+  __shared__ __attribute__((aligned(16))) uint8_t newtok_[NW][2 * NH * kRowBytes];
   __shared__ __attribute__((aligned(16))) uint8_t rope_table_[NW][ROPE ? 256 : 16];
   __shared__ __attribute__((aligned(16))) float part_[NW * 2 * REP * kRow];
   __shared__ int split_[NW + 1][4];  // cut segments: s, kv head, x0, x1
@@ -1390,8 +1535,8 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
     const int seg0 = sbase + kvh * np;
     const int pend = min(end, seg0 + np);
     const int i0 = cur - seg0, i1 = pend - seg0;  // pages [i0, i1) of the segment
-    PieceLoads<REP> pl;
-    piece_loads<REP, FUSED, ROPE, Q8>(a, s, kvh, pg0 + i0, pl);
+    PieceLoads<REP, NH> pl;
+    piece_loads<REP, FUSED, ROPE, Q8, NH>(a, s, kvh, pg0 + i0, pl);
     PieceOut po;
     po.final = i0 == 0 && i1 == np;
     po.pbase = ((size_t)wi * 2 + slot) * REP;
@@ -1399,13 +1544,13 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
     po.in_lds = true;
     po.lds = (lds_f32*)part_;
     if constexpr (Q8)
-      run_piece_q8<REP, DEPTH, FUSED>(a, (lds_u8*)vring_[wi], (lds_u8*)newtok_[wi], pl, true, s, kvh,
-                                      max(p0, (pg0 + i0) * kPage), min(L, (pg0 + i1) * kPage),
-                                      FUSED && i1 == np && L > 0, L - 1, po);
+      run_piece_q8<REP, DEPTH, FUSED, NH, ROPE>(a, (lds_u8*)vring_[wi], (lds_u8*)newtok_[wi], pl, true, s, kvh,
+                                                max(p0, (pg0 + i0) * kPage), min(L, (pg0 + i1) * kPage),
+                                                FUSED && i1 == np && L > 0, L - 1, po, (lds_u8*)rope_table_[wi]);
     else
-      run_piece<REP, FUSED, DEPTH, ROPE>(a, (lds_u8*)vring_[wi], (lds_u8*)newtok_[wi], pl, true, s, kvh,
-                                         max(p0, (pg0 + i0) * kPage), min(L, (pg0 + i1) * kPage),
-                                         FUSED && i1 == np && L > 0, L - 1, po, (lds_u8*)rope_table_[wi]);
+      run_piece<REP, FUSED, DEPTH, ROPE, NH>(a, (lds_u8*)vring_[wi], (lds_u8*)newtok_[wi], pl, true, s, kvh,
+                                             max(p0, (pg0 + i0) * kPage), min(L, (pg0 + i1) * kPage),
+                                             FUSED && i1 == np && L > 0, L - 1, po, (lds_u8*)rope_table_[wi]);
     cur = pend;
     slot = 1;
   }
@@ -1437,7 +1582,7 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
   __syncthreads();
 
   // Merge each cut segment's pieces held in LDS (wave e takes segments e,
-  // e + NW, ...), head by head; lane l holds acc elements l and l + 64.
+  // e + NW, ...), head by head; lane l holds acc elements l + 64 c.
   const int n_split = n_split_;
   for (int e = wi; e < n_split; e += NW) {  // wave-uniform
     const int s = split_[e][0], kvh = split_[e][1], x0 = split_[e][2], x1 = split_[e][3];
@@ -1446,28 +1591,31 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
     const bool inside = x0 >= A && x1 <= B;
     const int side = x0 < A ? 0 : 1;
     for (int h = 0; h < REP; ++h) {
-      float M = kMInit, Ls = 0.0f, A0 = 0.0f, A1 = 0.0f;
+      float M = kMInit, Ls = 0.0f, Av[CL];
+#pragma unroll
+      for (int c = 0; c < CL; ++c) Av[c] = 0.0f;
       for (int w = w1; w <= w2; ++w) {
         const int sl = (w == w1 && x0 > A + w1 * Cw) ? 1 : 0;
         const lds_f32* row = (const lds_f32*)part_ + ((size_t)(w * 2 + sl) * REP + h) * kRow;
-        const float m = row[kD], l = row[kD + 1];
+        const float m = row[D], l = row[D + 1];
         const float Mn = fmaxf(M, m);
         const float ra = fast_exp2(M - Mn), rb = fast_exp2(m - Mn);
         Ls = Ls * ra + l * rb;
-        A0 = A0 * ra + row[lane] * rb;
-        A1 = A1 * ra + row[lane + kWave] * rb;
+#pragma unroll
+        for (int c = 0; c < CL; ++c) Av[c] = Av[c] * ra + row[lane + c * kWave] * rb;
         M = Mn;
       }
       if (inside) {
-        const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * kD;
+        const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * D;
         const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-        a.out[orow + lane] = gated(a, orow + lane, A0 * inv);
-        a.out[orow + kWave + lane] = gated(a, orow + kWave + lane, A1 * inv);
+#pragma unroll
+        for (int c = 0; c < CL; ++c) a.out[orow + c * kWave + lane] = gated(a, orow + c * kWave + lane, Av[c] * inv);
       } else {
         // device-scope stores: written through to where every XCD reads
         const size_t r = ((size_t)wg * 2 + side) * REP + h;
-        __hip_atomic_store(a.ws_acc + r * kD + lane, A0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.ws_acc + r * kD + kWave + lane, A1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int c = 0; c < CL; ++c)
+          __hip_atomic_store(a.ws_acc + r * D + c * kWave + lane, Av[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (lane == 0) {
           __hip_atomic_store(a.ws_ml + r * 2 + 0, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_store(a.ws_ml + r * 2 + 1, Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1508,7 +1656,7 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
   // the HP parts of head h through LDS, in part order.
   constexpr int HP = NW >= REP ? NW / REP : 1;  // parts per head
   constexpr int HW = NW >= REP ? 1 : REP / NW;  // heads per wave
-  constexpr int kChunk = 32;
+  constexpr int kChunk = 32 / NH;               // rows in flight (registers: kChunk x (2 + CL))
   lds_f32* prow = (lds_f32*)part_;  // free again: row v of wave v, acc then m, l
 #pragma unroll
   for (int side = 0; side < 2; ++side) {
@@ -1519,20 +1667,26 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
     for (int hh = 0; hh < HW; ++hh) {
       const int h = NW >= REP ? wi % REP : wi + hh * NW;
       const int part = NW >= REP ? wi / REP : 0;
-      float M = kMInit, Ls = 0.0f, A0 = 0.0f, A1 = 0.0f;
+      float M = kMInit, Ls = 0.0f, Av[CL];
+#pragma unroll
+      for (int c = 0; c < CL; ++c) Av[c] = 0.0f;
       for (int j0 = part; j0 < nwg; j0 += kChunk * HP) {  // wave-uniform
-        float m[kChunk], l[kChunk], v0[kChunk], v1[kChunk];
+        float m[kChunk], l[kChunk], v[kChunk][CL];
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) {
           const int j = j0 + u * HP;
           m[u] = kMInit;
-          l[u] = v0[u] = v1[u] = 0.0f;
+          l[u] = 0.0f;
+#pragma unroll
+          for (int c = 0; c < CL; ++c) v[u][c] = 0.0f;
           if (j < nwg) {
             const size_t r = ((size_t)(ga + j) * 2 + (j == 0 ? 1 : 0)) * REP + h;
             m[u] = __hip_atomic_load(a.ws_ml + r * 2 + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             l[u] = __hip_atomic_load(a.ws_ml + r * 2 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            v0[u] = __hip_atomic_load(a.ws_acc + r * kD + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            v1[u] = __hip_atomic_load(a.ws_acc + r * kD + kWave + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int c = 0; c < CL; ++c)
+              v[u][c] = __hip_atomic_load(a.ws_acc + r * D + c * kWave + lane, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
           }
         }
         float Mc = M;
@@ -1540,28 +1694,28 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
         for (int u = 0; u < kChunk; ++u) Mc = fmaxf(Mc, m[u]);
         const float ra = fast_exp2(M - Mc);
         Ls *= ra;
-        A0 *= ra;
-        A1 *= ra;
+#pragma unroll
+        for (int c = 0; c < CL; ++c) Av[c] *= ra;
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) {
           const float wgt = fast_exp2(m[u] - Mc);
           Ls = fmaf(wgt, l[u], Ls);
-          A0 = fmaf(wgt, v0[u], A0);
-          A1 = fmaf(wgt, v1[u], A1);
+#pragma unroll
+          for (int c = 0; c < CL; ++c) Av[c] = fmaf(wgt, v[u][c], Av[c]);
         }
         M = Mc;
       }
-      const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * kD;
+      const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * D;
       if constexpr (HP == 1) {
         const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-        a.out[orow + lane] = gated(a, orow + lane, A0 * inv);
-        a.out[orow + kWave + lane] = gated(a, orow + kWave + lane, A1 * inv);
+#pragma unroll
+        for (int c = 0; c < CL; ++c) a.out[orow + c * kWave + lane] = gated(a, orow + c * kWave + lane, Av[c] * inv);
       } else {
-        prow[wi * kRow + lane] = A0;
-        prow[wi * kRow + kWave + lane] = A1;
+#pragma unroll
+        for (int c = 0; c < CL; ++c) prow[wi * kRow + c * kWave + lane] = Av[c];
         if (lane == 0) {
-          prow[wi * kRow + kD] = M;
-          prow[wi * kRow + kD + 1] = Ls;
+          prow[wi * kRow + D] = M;
+          prow[wi * kRow + D + 1] = Ls;
         }
       }
     }
@@ -1570,20 +1724,22 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
       if (wi < REP) {
         float Mt = kMInit;
 #pragma unroll
-        for (int q = 0; q < HP; ++q) Mt = fmaxf(Mt, prow[(wi + q * REP) * kRow + kD]);
-        float Lt = 0.0f, T0 = 0.0f, T1 = 0.0f;
+        for (int q = 0; q < HP; ++q) Mt = fmaxf(Mt, prow[(wi + q * REP) * kRow + D]);
+        float Lt = 0.0f, T[CL];
+#pragma unroll
+        for (int c = 0; c < CL; ++c) T[c] = 0.0f;
 #pragma unroll
         for (int q = 0; q < HP; ++q) {
           const lds_f32* row = prow + (wi + q * REP) * kRow;
-          const float wgt = fast_exp2(row[kD] - Mt);
-          Lt = fmaf(wgt, row[kD + 1], Lt);
-          T0 = fmaf(wgt, row[lane], T0);
-          T1 = fmaf(wgt, row[kWave + lane], T1);
+          const float wgt = fast_exp2(row[D] - Mt);
+          Lt = fmaf(wgt, row[D + 1], Lt);
+#pragma unroll
+          for (int c = 0; c < CL; ++c) T[c] = fmaf(wgt, row[c * kWave + lane], T[c]);
         }
-        const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP + wi) * kD;
+        const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP + wi) * D;
         const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
-        a.out[orow + lane] = gated(a, orow + lane, T0 * inv);
-        a.out[orow + kWave + lane] = gated(a, orow + kWave + lane, T1 * inv);
+#pragma unroll
+        for (int c = 0; c < CL; ++c) a.out[orow + c * kWave + lane] = gated(a, orow + c * kWave + lane, T[c] * inv);
       }
       __syncthreads();
     }
@@ -1592,7 +1748,7 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
   // zero rows for the sequences with empty windows (wg, wg + G, ...)
   for (int s = wg; s < n_seq; s += n_wg) {  // block-uniform
     if (sk_fields<FUSED>(a, s, n_seq).np == 0)
-      for (int i = threadIdx.x; i < a.n_heads * kD; i += kWave * NW) a.out[(size_t)s * a.n_heads * kD + i] = 0.0f;
+      for (int i = threadIdx.x; i < a.n_heads * D; i += kWave * NW) a.out[(size_t)s * a.n_heads * D + i] = 0.0f;
   }
 }
 
@@ -1600,31 +1756,47 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
 
 namespace {
 // RoPE variants exist for fused calls only (a.rope_half > 0).
-template <int REP, bool FUSED>
+template <int REP, bool FUSED, int NH>
 void launch_mfma_rep(const DecodeArgs& a, int n_seq, hipStream_t st) {
   const dim3 grid((unsigned)a.n_kv, (unsigned)a.max_parts, (unsigned)n_seq);
   if (FUSED && a.rope_half > 0)
-    decode_mfma_kernel<REP, FUSED, FUSED><<<grid, kWave, 0, st>>>(a);
+    decode_mfma_kernel<REP, FUSED, FUSED, NH><<<grid, kWave, 0, st>>>(a);
   else
-    decode_mfma_kernel<REP, FUSED, false><<<grid, kWave, 0, st>>>(a);
-  launch_combine<REP, kD, FUSED>(a, n_seq, st);
+    decode_mfma_kernel<REP, FUSED, false, NH><<<grid, kWave, 0, st>>>(a);
+  launch_combine<REP, NH * kD, FUSED>(a, n_seq, st);
+}
+
+// rep (1, 2, 4, 8) and head dim (128: NH = 1, 256: NH = 2) as compile-time
+// constants: f(rep_c, nh_c).
+template <typename F>
+int with_rep_nh(int rep, int d, F&& f) {
+  if (d != 128 && d != 256) return fail(LNSKV_ERR_UNSUPPORTED, "head_dim %d: the matrix-core decode takes 128 or 256", d);
+  auto go = [&](auto rep_c) {
+    if (d == 256) f(rep_c, std::integral_constant<int, 2>{});
+    else f(rep_c, std::integral_constant<int, 1>{});
+  };
+  switch (rep) {
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 4: go(std::integral_constant<int, 4>{}); break;
+    case 8: go(std::integral_constant<int, 8>{}); break;
+    default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
+  }
+  return LNSKV_OK;
 }
 }  // namespace
 
 template <bool FUSED>
-int launch_decode_mfma_f16_d128(const DecodeArgs& a, int rep, int n_seq, hipStream_t st) {
-  switch (rep) {
-    case 1: launch_mfma_rep<1, FUSED>(a, n_seq, st); break;
-    case 2: launch_mfma_rep<2, FUSED>(a, n_seq, st); break;
-    case 4: launch_mfma_rep<4, FUSED>(a, n_seq, st); break;
-    case 8: launch_mfma_rep<8, FUSED>(a, n_seq, st); break;
-    default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
-  }
+int launch_decode_mfma_f16(const DecodeArgs& a, int rep, int d, int n_seq, hipStream_t st) {
+  if (int rc = with_rep_nh(rep, d, [&](auto rep_c, auto nh_c) {
+        launch_mfma_rep<decltype(rep_c)::value, FUSED, decltype(nh_c)::value>(a, n_seq, st);
+      }))
+    return rc;
   return hip_check("decode kernel launch");
 }
 
-template int launch_decode_mfma_f16_d128<false>(const DecodeArgs&, int, int, hipStream_t);
-template int launch_decode_mfma_f16_d128<true>(const DecodeArgs&, int, int, hipStream_t);
+template int launch_decode_mfma_f16<false>(const DecodeArgs&, int, int, int, hipStream_t);
+template int launch_decode_mfma_f16<true>(const DecodeArgs&, int, int, int, hipStream_t);
 
 namespace {
 // Stream-K launch shape: two pages in flight per wave and four waves per CU
@@ -1640,48 +1812,46 @@ constexpr int kSkWavesPerCu = 4;
 constexpr int kSkDepthQ8 = 2;
 constexpr int kSkWavesPerCuQ8 = 8;
 
-template <int REP, bool FUSED, bool Q8>
+template <int REP, bool FUSED, bool Q8, int NH>
 int sk_waves_of(int cus, int* waves) {
-  // f16 pages: the smaller occupancy of the plain and (fused) RoPE variants,
-  // so one wave count serves both
+  // the smaller occupancy of the plain and (fused) RoPE variants, so one wave
+  // count serves both
   int per_cu = 0, per_cu_rope = 0;
-  if (Q8) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, kSkDepthQ8, false, true>,
-                                                     kWave, 0) != hipSuccess)
-      per_cu = 0;
-    per_cu_rope = per_cu;
-  } else if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, kSkDepth, false>,
-                                                          kWave, 0) != hipSuccess ||
-             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rope, decode_sk_kernel<REP, FUSED, kSkDepth, FUSED>,
-                                                          kWave, 0) != hipSuccess) {
+  constexpr int depth = Q8 ? kSkDepthQ8 : kSkDepth;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, depth, false, Q8, NH>,
+                                                   kWave, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rope, decode_sk_kernel<REP, FUSED, depth, FUSED, Q8, NH>,
+                                                   kWave, 0) != hipSuccess)
     per_cu = 0;
-  }
   if (per_cu <= 0 || per_cu_rope <= 0) return fail(LNSKV_ERR_HIP, "occupancy query of the stream-K decode kernel failed");
   *waves = cus * std::min(std::min(per_cu, per_cu_rope), Q8 ? kSkWavesPerCuQ8 : kSkWavesPerCu);
   return LNSKV_OK;
 }
 
-template <int REP, bool FUSED>
+template <int REP, bool FUSED, int NH>
 void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, bool q8, hipStream_t st) {
-  if (q8)
-    decode_sk_kernel<REP, FUSED, kSkDepthQ8, false, true><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
-  else if (FUSED && a.rope_half > 0)
-    decode_sk_kernel<REP, FUSED, kSkDepth, FUSED><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+  const bool rope = FUSED && a.rope_half > 0;
+  if (q8 && rope)
+    decode_sk_kernel<REP, FUSED, kSkDepthQ8, FUSED, true, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+  else if (q8)
+    decode_sk_kernel<REP, FUSED, kSkDepthQ8, false, true, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+  else if (rope)
+    decode_sk_kernel<REP, FUSED, kSkDepth, FUSED, false, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
   else
-    decode_sk_kernel<REP, FUSED, kSkDepth, false><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
-  combine_sk_kernel<REP, FUSED><<<n_waves, kBlock, 0, st>>>(a, n_seq, n_waves);
+    decode_sk_kernel<REP, FUSED, kSkDepth, false, false, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+  combine_sk_kernel<REP, FUSED, NH><<<n_waves, kBlock, 0, st>>>(a, n_seq, n_waves);
 }
 }  // namespace
 
-int mfma_sk_waves(int rep, bool fused, bool q8, int* waves) {
+int mfma_sk_waves(int rep, int d, bool fused, bool q8, int* waves) {
   // resident waves used per launch on the current device, kept per
-  // (device, rep, fused, q8)
+  // (device, rep, head dim, fused, q8)
   static std::mutex mu;
-  static std::map<std::tuple<int, int, bool, bool>, int> cache;
+  static std::map<std::tuple<int, int, int, bool, bool>, int> cache;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
   std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_tuple(dev, rep, fused, q8);
+  const auto key = std::make_tuple(dev, rep, d, fused, q8);
   const auto it = cache.find(key);
   if (it != cache.end()) {
     *waves = it->second;
@@ -1689,39 +1859,30 @@ int mfma_sk_waves(int rep, bool fused, bool q8, int* waves) {
   }
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     return fail(LNSKV_ERR_HIP, "compute-unit count query failed");
-  int rc = LNSKV_ERR_UNSUPPORTED;
-  auto of = [&](auto rep_c) {
-    constexpr int R = decltype(rep_c)::value;
-    if (q8) return fused ? sk_waves_of<R, true, true>(cus, waves) : sk_waves_of<R, false, true>(cus, waves);
-    return fused ? sk_waves_of<R, true, false>(cus, waves) : sk_waves_of<R, false, false>(cus, waves);
-  };
-  switch (rep) {
-    case 1: rc = of(std::integral_constant<int, 1>{}); break;
-    case 2: rc = of(std::integral_constant<int, 2>{}); break;
-    case 4: rc = of(std::integral_constant<int, 4>{}); break;
-    case 8: rc = of(std::integral_constant<int, 8>{}); break;
-    default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
-  }
+  int rc = LNSKV_OK;
+  if (int r = with_rep_nh(rep, d, [&](auto rep_c, auto nh_c) {
+        constexpr int R = decltype(rep_c)::value, NH = decltype(nh_c)::value;
+        if (q8) rc = fused ? sk_waves_of<R, true, true, NH>(cus, waves) : sk_waves_of<R, false, true, NH>(cus, waves);
+        else rc = fused ? sk_waves_of<R, true, false, NH>(cus, waves) : sk_waves_of<R, false, false, NH>(cus, waves);
+      }))
+    return r;
   if (rc == LNSKV_OK) cache[key] = *waves;
   return rc;
 }
 
 template <bool FUSED>
-int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, bool q8, hipStream_t st) {
+int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int d, int n_seq, int n_waves, bool q8, hipStream_t st) {
   if (n_seq > kSkMaxSeqs)
     return fail(LNSKV_ERR_INVALID, "stream-K decode serves at most %d sequences", kSkMaxSeqs);
-  switch (rep) {
-    case 1: launch_sk_rep<1, FUSED>(a, n_seq, n_waves, q8, st); break;
-    case 2: launch_sk_rep<2, FUSED>(a, n_seq, n_waves, q8, st); break;
-    case 4: launch_sk_rep<4, FUSED>(a, n_seq, n_waves, q8, st); break;
-    case 8: launch_sk_rep<8, FUSED>(a, n_seq, n_waves, q8, st); break;
-    default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
-  }
+  if (int rc = with_rep_nh(rep, d, [&](auto rep_c, auto nh_c) {
+        launch_sk_rep<decltype(rep_c)::value, FUSED, decltype(nh_c)::value>(a, n_seq, n_waves, q8, st);
+      }))
+    return rc;
   return hip_check("stream-K decode kernel launch");
 }
 
-template int launch_decode_mfma_sk<false>(const DecodeArgs&, int, int, int, bool, hipStream_t);
-template int launch_decode_mfma_sk<true>(const DecodeArgs&, int, int, int, bool, hipStream_t);
+template int launch_decode_mfma_sk<false>(const DecodeArgs&, int, int, int, int, bool, hipStream_t);
+template int launch_decode_mfma_sk<true>(const DecodeArgs&, int, int, int, int, bool, hipStream_t);
 
 namespace {
 // Workgroup schedule launch shape: two workgroups per CU, of two waves (f16
@@ -1732,15 +1893,21 @@ constexpr int kWgWaves = 2;
 constexpr int kWgWavesQ8 = 4;
 constexpr int kWgPerCu = 2;
 
-template <int REP, bool FUSED>
+template <int REP, bool FUSED, int NH>
 void launch_wg_rep(const DecodeArgs& a, int n_seq, int n_wg, bool q8, hipStream_t st) {
-  if (q8)
-    decode_wg_kernel<REP, FUSED, kSkDepthQ8, false, true, kWgWavesQ8>
+  const bool rope = FUSED && a.rope_half > 0;
+  if (q8 && rope)
+    decode_wg_kernel<REP, FUSED, kSkDepthQ8, FUSED, true, kWgWavesQ8, NH>
         <<<n_wg, kWave * kWgWavesQ8, 0, st>>>(a, n_seq, n_wg);
-  else if (FUSED && a.rope_half > 0)
-    decode_wg_kernel<REP, FUSED, kSkDepth, FUSED, false, kWgWaves><<<n_wg, kWave * kWgWaves, 0, st>>>(a, n_seq, n_wg);
+  else if (q8)
+    decode_wg_kernel<REP, FUSED, kSkDepthQ8, false, true, kWgWavesQ8, NH>
+        <<<n_wg, kWave * kWgWavesQ8, 0, st>>>(a, n_seq, n_wg);
+  else if (rope)
+    decode_wg_kernel<REP, FUSED, kSkDepth, FUSED, false, kWgWaves, NH>
+        <<<n_wg, kWave * kWgWaves, 0, st>>>(a, n_seq, n_wg);
   else
-    decode_wg_kernel<REP, FUSED, kSkDepth, false, false, kWgWaves><<<n_wg, kWave * kWgWaves, 0, st>>>(a, n_seq, n_wg);
+    decode_wg_kernel<REP, FUSED, kSkDepth, false, false, kWgWaves, NH>
+        <<<n_wg, kWave * kWgWaves, 0, st>>>(a, n_seq, n_wg);
 }
 }  // namespace
 
@@ -1765,7 +1932,7 @@ int mfma_wg_count(int* n_wg) {
 }
 
 template <bool FUSED>
-int launch_decode_mfma_wg(const DecodeArgs& a, int rep, int n_seq, int n_wg, bool q8, hipStream_t st) {
+int launch_decode_mfma_wg(const DecodeArgs& a, int rep, int d, int n_seq, int n_wg, bool q8, hipStream_t st) {
   if (n_seq > kSkMaxSeqs)
     return fail(LNSKV_ERR_INVALID, "the workgroup schedule serves at most %d sequences", kSkMaxSeqs);
   if (n_wg <= 0 || n_wg > kWgMaxGroups) return fail(LNSKV_ERR_INVALID, "%d workgroups", n_wg);
@@ -1777,18 +1944,15 @@ int launch_decode_mfma_wg(const DecodeArgs& a, int rep, int n_seq, int n_wg, boo
   const int64_t bound = (int64_t)n_seq * a.n_kv * ((int64_t)a.max_kv_len / kPage + 1);
   const int64_t per = (int64_t)nw * kWgMinPages;
   const int groups = (int)std::max<int64_t>(1, std::min<int64_t>(n_wg, (bound + per - 1) / per));
-  switch (rep) {
-    case 1: launch_wg_rep<1, FUSED>(a, n_seq, groups, q8, st); break;
-    case 2: launch_wg_rep<2, FUSED>(a, n_seq, groups, q8, st); break;
-    case 4: launch_wg_rep<4, FUSED>(a, n_seq, groups, q8, st); break;
-    case 8: launch_wg_rep<8, FUSED>(a, n_seq, groups, q8, st); break;
-    default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
-  }
+  if (int rc = with_rep_nh(rep, d, [&](auto rep_c, auto nh_c) {
+        launch_wg_rep<decltype(rep_c)::value, FUSED, decltype(nh_c)::value>(a, n_seq, groups, q8, st);
+      }))
+    return rc;
   return hip_check("workgroup decode kernel launch");
 }
 
-template int launch_decode_mfma_wg<false>(const DecodeArgs&, int, int, int, bool, hipStream_t);
-template int launch_decode_mfma_wg<true>(const DecodeArgs&, int, int, int, bool, hipStream_t);
+template int launch_decode_mfma_wg<false>(const DecodeArgs&, int, int, int, int, bool, hipStream_t);
+template int launch_decode_mfma_wg<true>(const DecodeArgs&, int, int, int, int, bool, hipStream_t);
 
 
 // ---------------------------------------------------------------------------

@@ -360,20 +360,21 @@ inline void launch_combine(const DecodeArgs& a, int n_seq, hipStream_t st) {
 // Launchers (defined in the decode translation units).
 template <int DT, bool FUSED>
 int launch_decode_valu(const DecodeArgs& a, int d, int rep, int n_seq, hipStream_t st);
+// Matrix-core decode of f16 pages, split-K schedule (head_dim d of 128 or 256).
 template <bool FUSED>
-int launch_decode_mfma_f16_d128(const DecodeArgs& a, int rep, int n_seq, hipStream_t st);
+int launch_decode_mfma_f16(const DecodeArgs& a, int rep, int d, int n_seq, hipStream_t st);
 // Stream-K schedule of the MFMA kernel (n_seq <= kSkMaxSeqs): n_waves single-wave
 // blocks, workspace of n_waves * 2 * rep partial rows.  q8: Q8A pages.
 template <bool FUSED>
-int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int n_seq, int n_waves, bool q8, hipStream_t st);
+int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int d, int n_seq, int n_waves, bool q8, hipStream_t st);
 // Waves of the stream-K kernel resident at once on the current device.
-int mfma_sk_waves(int rep, bool fused, bool q8, int* waves);
+int mfma_sk_waves(int rep, int d, bool fused, bool q8, int* waves);
 // Workgroup schedule of the MFMA kernels (n_seq <= kSkMaxSeqs): up to n_wg
 // workgroups (mfma_wg_count: two per CU); the workspace holds the header of
 // kWsHeaderBytes (a count per workgroup, zero between calls) and then 2 * rep
 // partial rows per workgroup.
 template <bool FUSED>
-int launch_decode_mfma_wg(const DecodeArgs& a, int rep, int n_seq, int n_wg, bool q8, hipStream_t st);
+int launch_decode_mfma_wg(const DecodeArgs& a, int rep, int d, int n_seq, int n_wg, bool q8, hipStream_t st);
 int mfma_wg_count(int* n_wg);
 
 // Chunked prefill over f16 pages with head_dim 128 (lnskv_prefill_attention).

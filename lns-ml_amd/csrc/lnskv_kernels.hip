@@ -337,15 +337,16 @@ bool force_valu() {
   return e && e[0] == '1';
 }
 
-// The MFMA kernel serves f16 pages with head_dim 128 (the Llama/Mixtral
-// shapes); every other combination runs the generic VALU kernel.
+// The MFMA kernels serve f16 and Q8A pages with head_dim 128 (the Llama /
+// Mixtral shapes) or 256 (lns-ml's Qwen3.5 full-attention layers); every
+// other combination runs the generic VALU kernel.
 bool mfma_path(int dtype, int d, int rep);
 bool mfma_q8_path(int dtype, int d, int rep);
 
 template <bool FUSED>
 int launch_decode(const DecodeArgs& a, int dtype, int d, int rep, int n_seq, hipStream_t st) {
   if (mfma_path(dtype, d, rep))
-    return launch_decode_mfma_f16_d128<FUSED>(a, rep, n_seq, st);
+    return launch_decode_mfma_f16<FUSED>(a, rep, d, n_seq, st);
   switch (dtype) {
     case LNSKV_DTYPE_F32: return launch_decode_valu<LNSKV_DTYPE_F32, FUSED>(a, d, rep, n_seq, st);
     case LNSKV_DTYPE_F16: return launch_decode_valu<LNSKV_DTYPE_F16, FUSED>(a, d, rep, n_seq, st);
@@ -374,14 +375,16 @@ size_t workspace_bytes(int n_seq, int n_heads, int d, int max_parts) {
 }
 
 bool mfma_path(int dtype, int d, int rep) {
-  return dtype == LNSKV_DTYPE_F16 && d == 128 && (rep == 1 || rep == 2 || rep == 4 || rep == 8) && !force_valu();
+  return dtype == LNSKV_DTYPE_F16 && (d == 128 || d == 256) && (rep == 1 || rep == 2 || rep == 4 || rep == 8) &&
+         !force_valu();
 }
 
-// Q8A pages with head_dim 128 also run on the matrix cores, on the stream-K
-// and workgroup schedules only (split_tokens = 0, at most kSkMaxSeqs
-// sequences).
+// Q8A pages with head_dim 128 or 256 also run on the matrix cores, on the
+// stream-K and workgroup schedules only (split_tokens = 0, at most
+// kSkMaxSeqs sequences).
 bool mfma_q8_path(int dtype, int d, int rep) {
-  return dtype == LNSKV_DTYPE_Q8A && d == 128 && (rep == 1 || rep == 2 || rep == 4 || rep == 8) && !force_valu();
+  return dtype == LNSKV_DTYPE_Q8A && (d == 128 || d == 256) && (rep == 1 || rep == 2 || rep == 4 || rep == 8) &&
+         !force_valu();
 }
 
 // Gated query split (split_gated_query_kernel, lns_decode.metal:193-209): the
@@ -467,9 +470,9 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
     // larger
     int w0 = 0, w1 = 0;
     if (fused <= 0)
-      if (int rc = mfma_sk_waves(rep, false, q8, &w0)) return rc;
+      if (int rc = mfma_sk_waves(rep, d, false, q8, &w0)) return rc;
     if (fused != 0)
-      if (int rc = mfma_sk_waves(rep, true, q8, &w1)) return rc;
+      if (int rc = mfma_sk_waves(rep, d, true, q8, &w1)) return rc;
     p->sk_waves = std::max(w0, w1);
     // the header, then partial rows (acc, then (m, l)) of two pieces per
     // wave, then one 16-byte descriptor per wave
@@ -585,10 +588,11 @@ int noalloc_scratch(void** out) {
     if (e != hipSuccess || !p)
       return fail(LNSKV_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
     for (int rep : {1, 2, 4, 8})
-      for (bool q8 : {false, true}) {
-        int waves = 0;
-        if (int rc = mfma_sk_waves(rep, true, q8, &waves)) return rc;
-      }
+      for (int d : {128, 256})
+        for (bool q8 : {false, true}) {
+          int waves = 0;
+          if (int rc = mfma_sk_waves(rep, d, true, q8, &waves)) return rc;
+        }
     int n_wg = 0;
     if (int rc = mfma_wg_count(&n_wg)) return rc;
     g_scratch_ptr[dev] = p;
@@ -640,14 +644,18 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
   // in a library buffer when the caller passes none
   int rope_half = 0;
   bool rope_rows = false;
+  DecodePlan plan;
+  if (int rc = plan_decode(c, n_seq, n_heads, max_kv_len, split, FUSED ? 1 : 0, &plan)) return rc;
   if (rope) {
     if (!FUSED) return fail(LNSKV_ERR_INVALID, "RoPE needs the fused append");
     if (int rc = check_rope(rope, d, &rope_half)) return rc;
-    rope_rows = !(mfma_path((int)c->dtype, d, rep) && d == 128 && (rope_half == 32 || rope_half == 64) &&
-                  aligned16(rope->inv_freqs_dev));
+    // turned in place by the matrix-core kernels (f16 pages on every
+    // schedule, Q8A pages on stream-K and the workgroup schedule) for a
+    // rotary width of 64 or 128 of a 128- or 256-wide head
+    const bool mfma = mfma_path((int)c->dtype, d, rep) ||
+                      (mfma_q8_path((int)c->dtype, d, rep) && (plan.wg > 0 || plan.sk_waves > 0));
+    rope_rows = !(mfma && (rope_half == 32 || rope_half == 64) && aligned16(rope->inv_freqs_dev));
   }
-  DecodePlan plan;
-  if (int rc = plan_decode(c, n_seq, n_heads, max_kv_len, split, FUSED ? 1 : 0, &plan)) return rc;
   const size_t need = plan.ws_bytes;
   const size_t qn = (size_t)n_seq * n_heads * d, kn = (size_t)n_seq * c->n_kv_heads * d;
   const size_t rope_off = rope_rows_offset(need);
@@ -713,13 +721,13 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
     a.wg_cnt = static_cast<uint32_t*>(ws);
     a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeaderBytes);
     a.ws_ml = a.ws_acc + (size_t)plan.wg * 2 * rep * c->head_dim;
-    return launch_decode_mfma_wg<FUSED>(a, rep, n_seq, plan.wg, c->dtype == LNSKV_DTYPE_Q8A, (hipStream_t)stream);
+    return launch_decode_mfma_wg<FUSED>(a, rep, d, n_seq, plan.wg, c->dtype == LNSKV_DTYPE_Q8A, (hipStream_t)stream);
   }
   if (plan.sk_waves > 0) {
     a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeaderBytes);
     a.ws_ml = a.ws_acc + (size_t)plan.sk_waves * 2 * rep * c->head_dim;
     a.sk_desc = reinterpret_cast<int4*>(a.ws_ml + (size_t)plan.sk_waves * 2 * rep * 2);
-    return launch_decode_mfma_sk<FUSED>(a, rep, n_seq, plan.sk_waves, c->dtype == LNSKV_DTYPE_Q8A,
+    return launch_decode_mfma_sk<FUSED>(a, rep, d, n_seq, plan.sk_waves, c->dtype == LNSKV_DTYPE_Q8A,
                                         (hipStream_t)stream);
   }
   if (need > 0) {

@@ -267,7 +267,8 @@ SCHEDULES = ["stream-k", "workgroup"]
 @pytest.mark.parametrize("schedule", SCHEDULES)
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_Q8A])
 @pytest.mark.parametrize("rep", [1, 2, 4, 8])
-def test_stream_k_schedule(gpu, monkeypatch, rep, dtype, schedule):
+@pytest.mark.parametrize("d", [128, 256])
+def test_stream_k_schedule(gpu, monkeypatch, rep, dtype, schedule, d):
     """split_tokens = 0 on the MFMA path runs one of two schedules, forced
     here through LNSKV_DECODE_SCHEDULE: stream-K (every wave an equal share
     of all pages; pieces merged by combine_sk_kernel) or the workgroup
@@ -275,10 +276,11 @@ def test_stream_k_schedule(gpu, monkeypatch, rep, dtype, schedule):
     workgroups, by the last workgroup to finish).  64 sequences (one group)
     with empty, short and long lengths, windows, a missing page; unfused and
     fused, against the f64 oracle and against the split-K schedule; f16 and
-    Q8A pages (pages and scales bit-exact)."""
+    Q8A pages (pages and scales bit-exact); heads of 128 and of 256 dims (two
+    halves sharing one softmax)."""
     monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", schedule)
-    say(schedule, "rep", rep, DTYPE_NAMES[dtype])
-    n_kv, d = 8, 128
+    say(schedule, "rep", rep, DTYPE_NAMES[dtype], "d", d)
+    n_kv = 8 if d == 128 else 4
     lens = _sk_lens(64, seed=rep)
     pk, tables, kv_len, q = _case(gpu, dtype, d, rep, n_kv, lens, seed=90 + rep)
     tables[5, 0] = NO_PAGE  # a missing page: its tokens are skipped
@@ -532,25 +534,27 @@ def test_out_of_range_kv_len_stores_nothing(gpu, dtype):
 @pytest.mark.parametrize("schedule", SCHEDULES)
 def test_schedules_random_batches(gpu, monkeypatch, schedule):
     """Seeded random small batches on each schedule against the f64 oracle:
-    1-70 sequences of 0-900 tokens, rep 1/2/4/8, f16 or Q8A pages, random
+    1-70 sequences of 0-900 tokens, rep 1/2/4/8, f16 or Q8A pages, head_dim
+    128 or 256, random
     window starts, a missing page now and then, unfused and fused (pages and
     Q8A scales bit-exact after the fused call)."""
     monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", schedule)
     rng = np.random.default_rng(2024 if schedule == "stream-k" else 2025)
-    for case in range(12):
+    for case in range(16):
         dtype = DTYPE_F16 if case % 2 == 0 else DTYPE_Q8A
+        d = 256 if case % 4 >= 2 else 128
         rep = int(rng.choice([1, 2, 4, 8]))
         n_kv = int(rng.choice([1, 2, 4]))
         n_seq = int(rng.integers(1, 71))
         lens = tuple(int(x) for x in rng.integers(0, 901, n_seq))
-        say(schedule, "random case", case, DTYPE_NAMES[dtype], "rep", rep, "n_kv", n_kv, "n_seq", n_seq)
-        pk, tables, kv_len, q = _case(gpu, dtype, 128, rep, n_kv, lens, seed=1000 + case)
+        say(schedule, "random case", case, DTYPE_NAMES[dtype], "d", d, "rep", rep, "n_kv", n_kv, "n_seq", n_seq)
+        pk, tables, kv_len, q = _case(gpu, dtype, d, rep, n_kv, lens, seed=1000 + case)
         if case % 3 == 0 and kv_len.max() > 40:
             s_miss = int(np.argmax(kv_len))
             tables[s_miss, 1] = NO_PAGE
         p_start = np.array([int(rng.integers(0, L + 1)) if rng.random() < 0.4 else 0 for L in kv_len], np.int32)
         hp, _ = host_pages(pk)
-        scale = 1.0 / np.sqrt(128)
+        scale = 1.0 / np.sqrt(d)
         ref = O.decode_f64(hp, q, tables, kv_len, p_start, scale)
         mkv = max(int(kv_len.max()), 1)
         out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
@@ -562,8 +566,8 @@ def test_schedules_random_batches(gpu, monkeypatch, schedule):
         # skipped, by the oracle as by the library)
         kv1 = (kv_len + 1).astype(np.int32)
         assert (kv1 <= tables.shape[1] * 16).all()
-        k_new = rng.standard_normal((n_seq, n_kv, 128)).astype(np.float32)
-        v_new = rng.standard_normal((n_seq, n_kv, 128)).astype(np.float32)
+        k_new = rng.standard_normal((n_seq, n_kv, d)).astype(np.float32)
+        v_new = rng.standard_normal((n_seq, n_kv, d)).astype(np.float32)
         O.append(hp, k_new, v_new, np.arange(n_seq, dtype=np.int32), kv1 - 1, tables)
         ref1 = O.decode_f64(hp, q, tables, kv1, np.minimum(p_start, kv1), scale)
         out1 = pk.append_decode(dev_f32(q, gpu), dev_f32(k_new, gpu), dev_f32(v_new, gpu), dev_i32(tables, gpu),

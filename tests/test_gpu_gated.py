@@ -58,6 +58,10 @@ CASES = [  # dtype, head_dim, rep, split, force_valu, rotary_dim
     (DTYPE_Q8A, 128, 4, 0, "0", 0),      # Q8A stream-K MFMA after the quantizing append
     (DTYPE_F16, 128, 4, 0, "0", 128),    # RoPE turned inside the MFMA kernel
     (DTYPE_F16, 128, 8, 0, "0", 96),     # RoPE pre-pass (rotary 96), REP 8
+    (DTYPE_Q8A, 128, 4, 0, "0", 128),    # Q8A, RoPE turned inside the MFMA kernel
+    (DTYPE_Q8A, 256, 4, 0, "0", 64),     # lns-ml's Qwen3.5 shape: Q8A, 256-wide heads, rotary 64
+    (DTYPE_F16, 256, 4, 0, "0", 64),     # f16, 256-wide heads, rotary 64
+    (DTYPE_F16, 256, 2, 64, "0", 0),     # split-K MFMA, 256-wide heads
 ]
 
 

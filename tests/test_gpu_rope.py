@@ -75,7 +75,12 @@ CASES = [  # dtype, head_dim, rep, rotary_dim, split, force_valu
     (DTYPE_F16, 128, 4, 96, 0, "0"),
     (DTYPE_F16, 128, 4, 128, 0, "1"),
     (DTYPE_F32, 64, 2, 64, 0, "0"),
-    (DTYPE_Q8A, 128, 4, 128, 0, "0"),
+    (DTYPE_Q8A, 128, 4, 128, 0, "0"),   # Q8A: turned in registers before the quantizer
+    (DTYPE_Q8A, 128, 4, 64, 0, "0"),
+    (DTYPE_Q8A, 256, 4, 64, 0, "0"),    # lns-ml's Qwen3.5 layers: rotary 64 of 256
+    (DTYPE_F16, 256, 4, 64, 0, "0"),
+    (DTYPE_F16, 256, 2, 128, 128, "0"),  # split-K, 256-wide heads
+    (DTYPE_F16, 256, 4, 96, 0, "0"),    # pre-pass (rotary 96)
 ]
 
 
