@@ -435,14 +435,59 @@ __device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh,
   }
 }
 
-// RoPE: the wave's copy of the inverse frequencies in LDS (64 floats), read
-// where the rotation needs them so that no table values are held in
-// registers while the pages are in flight.
+// RoPE: the wave's table in LDS (kRopeTableBytes): the inverse frequencies
+// (floats 0..63, copied once per wave), then the (sin, cos) pairs of the
+// current piece's position (pair i at floats 64 + 2i), read where the
+// rotation needs them so that no table values are held in registers while
+// the pages are in flight.
+constexpr int kRopeTableBytes = 3 * 64 * 4;
 template <bool ROPE>
 __device__ __forceinline__ void stage_rope_table(const DecodeArgs& a, lds_u8* table) {
   if constexpr (ROPE) {
     const int lane = (int)(threadIdx.x & (kWave - 1));
     ((__attribute__((address_space(3))) float*)table)[lane] = lane < a.rope_half ? a.rope_inv[lane] : 0.0f;
+  }
+}
+
+// The sines and cosines of one position: lane i < half evaluates angle i
+// (pos * inv_freq[i], the reference's f32 product) once, for every head and
+// lane that turns a pair of that frequency.
+__device__ __forceinline__ void rope_angles(lds_u8* table, int half, float fpos) {
+  typedef __attribute__((address_space(3))) float lds_f32;
+  lds_f32* t = (lds_f32*)table;
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  if (lane < half) {
+    float sn, cs;
+    rope_sincos(fpos * t[lane], &sn, &cs);
+    t[64 + 2 * lane] = sn;
+    t[65 + 2 * lane] = cs;
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// (sin, cos) of frequencies fi and fi + 1 (fi even): one 16-byte LDS read.
+__device__ __forceinline__ float4v rope_pairs(const lds_u8* table, int fi) {
+  typedef __attribute__((address_space(3))) float4v lds_float4v;
+  return ((const lds_float4v*)(table + 256))[fi >> 1];
+}
+
+// The new token's K in the f16 lane order (lane: elements 2 lane, 2 lane + 1
+// of half 0) turned by the table's position: the partner of element i sits
+// half/2 lanes away; elements past the rotary width stay.
+__device__ __forceinline__ void rope_new_k(float2v& kn, int half, const lds_u8* table) {
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  const int mlane = half / 2;
+  const bool first = (lane & mlane) == 0;
+  const float p0 = __shfl_xor(kn.x, mlane, kWave);
+  const float p1 = __shfl_xor(kn.y, mlane, kWave);
+  if (half == 64 || lane < 32) {  // half 32: elements 64.. stay
+    const float4v sc = rope_pairs(table, 2 * (lane & (mlane - 1)));
+    float a0, b0, a1, b1;
+    // first half: (x, partner) -> x c - partner s; second: (partner, x) -> partner s + x c
+    rope_turn(first ? kn.x : p0, first ? p0 : kn.x, sc[0], sc[1], &a0, &b0);
+    rope_turn(first ? kn.y : p1, first ? p1 : kn.y, sc[2], sc[3], &a1, &b1);
+    kn.x = first ? a0 : b0;
+    kn.y = first ? a1 : b1;
   }
 }
 
@@ -717,27 +762,23 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
   // 128 lies in the first 128 dims (half 0 of a 256-wide head).
   if constexpr (FUSED && ROPE) {
     {
-      const float fpos = (float)max(pos, 0);
+      rope_angles(rope_table, a.rope_half, (float)max(pos, 0));
       // this lane's q holds elements 8g + 32j + e, and element i < half pairs
       // with i + half (j and j+2 when half is 64, j = 0 and 1 when it is 32)
-      typedef __attribute__((address_space(3))) float4v lds_float4v;
-      const lds_float4v* tq = (const lds_float4v*)rope_table;
       const int i1 = a.rope_half == 64 ? 8 * g + 32 : 8 * g;
-      float4v qinv[4];
-      qinv[0] = tq[2 * g];
-      qinv[1] = tq[2 * g + 1];
-      qinv[2] = tq[i1 / 4];
-      qinv[3] = tq[i1 / 4 + 1];
       // q pairs: vectors (v0, v1) hold the first halves, (w0, w1) the
-      // partners: (j, j+2) for half 64, (0, 1) for half 32
-      auto turn4 = [&](float4v& x, float4v& y, const float4v& f) {
+      // partners: (j, j+2) for half 64, (0, 1) for half 32; x[e] turns with
+      // frequency fi + e
+      auto turn4 = [&](float4v& x, float4v& y, int fi) {
+        const float4v p01 = rope_pairs(rope_table, fi), p23 = rope_pairs(rope_table, fi + 2);
+        const float sn[4] = {p01[0], p01[2], p23[0], p23[2]};
+        const float cs[4] = {p01[1], p01[3], p23[1], p23[3]};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float sn, cs;
-          rope_sincos(fpos * f[e], &sn, &cs);
-          const float x0 = x[e], x1 = y[e];
-          x[e] = x0 * cs - x1 * sn;
-          y[e] = x0 * sn + x1 * cs;
+          float y0, y1;
+          rope_turn(x[e], y[e], sn[e], cs[e], &y0, &y1);
+          x[e] = y0;
+          y[e] = y1;
         }
       };
       // Partners are picked by value, not by array index: a branch on the
@@ -748,36 +789,17 @@ __device__ __forceinline__ void run_piece(const DecodeArgs& a, lds_u8* vring, ld
       float4v y0 = h64 ? pl.qv[4] : pl.qv[2];
       float4v y1 = h64 ? pl.qv[5] : pl.qv[3];
       float4v x2 = pl.qv[2], x3 = pl.qv[3], y2 = pl.qv[6], y3 = pl.qv[7];
-      turn4(pl.qv[0], y0, qinv[0]);
-      turn4(pl.qv[1], y1, qinv[1]);
-      turn4(x2, y2, qinv[2]);
-      turn4(x3, y3, qinv[3]);
+      turn4(pl.qv[0], y0, 8 * g);
+      turn4(pl.qv[1], y1, 8 * g + 4);
+      turn4(x2, y2, i1);
+      turn4(x3, y3, i1 + 4);
       pl.qv[2] = h64 ? x2 : y0;
       pl.qv[3] = h64 ? x3 : y1;
       pl.qv[4] = h64 ? y0 : pl.qv[4];
       pl.qv[5] = h64 ? y1 : pl.qv[5];
       pl.qv[6] = h64 ? y2 : pl.qv[6];
       pl.qv[7] = h64 ? y3 : pl.qv[7];
-      if (append) {
-        // new K: lane holds elements 2*lane, 2*lane+1; the partner half sits
-        // half/2 lanes away
-        const int mlane = a.rope_half / 2;
-        const bool first = (lane & mlane) == 0;
-        const float p0 = __shfl_xor(pl.knew[0].x, mlane, kWave);
-        const float p1 = __shfl_xor(pl.knew[0].y, mlane, kWave);
-        const bool rotated = a.rope_half == 64 || lane < 32;  // half 32: elements 64.. stay
-        if (rotated) {
-          // its new-K pair is elements 2*(lane % (half/2)) + {0, 1}
-          typedef __attribute__((address_space(3))) float2v lds_float2v;
-          const float2v kinv = ((const lds_float2v*)rope_table)[lane & (mlane - 1)];
-          float sn0, cs0, sn1, cs1;
-          rope_sincos(fpos * kinv.x, &sn0, &cs0);
-          rope_sincos(fpos * kinv.y, &sn1, &cs1);
-          // first half: x*cos - partner*sin; second half: partner*sin + x*cos
-          pl.knew[0].x = first ? pl.knew[0].x * cs0 - p0 * sn0 : p0 * sn0 + pl.knew[0].x * cs0;
-          pl.knew[0].y = first ? pl.knew[0].y * cs1 - p1 * sn1 : p1 * sn1 + pl.knew[0].y * cs1;
-        }
-      }
+      if (append) rope_new_k(pl.knew[0], a.rope_half, rope_table);
     }
   }
 
@@ -908,32 +930,32 @@ struct PageQ8 {
 
 // RoPE on the Q8A lane order (lane (g, n): dims 32g .. 32g+31 of half 0):
 // rotary width 2H (H = 32: dims 0..63, H = 64: dims 0..127), dim i < H pairs
-// with i + H, which lives in lane g ^ (H/32) at the same element; the angle of
-// dim i is pos * inv_freq[i % H] (the table in LDS).
-__device__ __forceinline__ void rope_q8_lanes(float4v (&qv)[8], int half, float fpos, const lds_u8* rope_table,
-                                              int g) {
-  typedef __attribute__((address_space(3))) float lds_f32;
-  const lds_f32* tq = (const lds_f32*)rope_table;
+// with i + H, which lives in lane g ^ (H/32) at the same element; dim i turns
+// with frequency i % H, whose (sin, cos) the table holds.
+__device__ __forceinline__ void rope_q8_lanes(float4v (&qv)[8], int half, const lds_u8* rope_table, int g) {
+  const int lane = (int)(threadIdx.x & (kWave - 1));
   const bool h64 = half == 64;
   const bool rotated = h64 || g < 2;
   const bool first = h64 ? g < 2 : g == 0;
-  const int fb = h64 ? 32 * (g & 1) : 0;  // first table index of this lane's 32 dims
+  const int fb = h64 ? 32 * (g & 1) : 0;  // frequency of this lane's element 0
 #pragma unroll
-  for (int e = 0; e < 32; ++e) {
-    const float x = qv[e >> 2][e & 3];
-    const auto r16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false,
-                                                      false);
-    const auto r32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false,
-                                                      false);
-    // the value of lane ^ 16 / lane ^ 32 (the swaps return the pair in lane order)
-    const int lane = (int)(threadIdx.x & (kWave - 1));
-    const float p16 = __builtin_bit_cast(float, (int)((lane & 16) ? r16[0] : r16[1]));
-    const float p32 = __builtin_bit_cast(float, (int)((lane & 32) ? r32[0] : r32[1]));
-    const float p = h64 ? p32 : p16;
-    float sn, cs;
-    rope_sincos(fpos * tq[fb + e], &sn, &cs);
-    const float y = first ? x * cs - p * sn : p * sn + x * cs;
-    qv[e >> 2][e & 3] = rotated ? y : x;
+  for (int e = 0; e < 32; e += 2) {
+    const float4v sc = rope_pairs(rope_table, fb + e);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float x = qv[(e + u) >> 2][(e + u) & 3];
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
+                                                        false, false);
+      const auto r32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
+                                                        false, false);
+      // the value of lane ^ 16 / lane ^ 32 (the swaps return the pair in lane order)
+      const float p16 = __builtin_bit_cast(float, (int)((lane & 16) ? r16[0] : r16[1]));
+      const float p32 = __builtin_bit_cast(float, (int)((lane & 32) ? r32[0] : r32[1]));
+      const float p = h64 ? p32 : p16;
+      float y0, y1;
+      rope_turn(first ? x : p, first ? p : x, sc[2 * u], sc[2 * u + 1], &y0, &y1);
+      qv[(e + u) >> 2][(e + u) & 3] = rotated ? (first ? y0 : y1) : x;
+    }
   }
 }
 
@@ -1056,29 +1078,14 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
   // kernels' lane order for it: elements 2 lane, 2 lane + 1 of half 0) by the
   // new token's position.
   if constexpr (FUSED && ROPE) {
-    const float fpos = (float)max(pos, 0);
+    rope_angles(rope_table, a.rope_half, (float)max(pos, 0));
     float4v q0[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) q0[j] = pl.qv[j];
-    rope_q8_lanes(q0, a.rope_half, fpos, rope_table, g);
+    rope_q8_lanes(q0, a.rope_half, rope_table, g);
 #pragma unroll
     for (int j = 0; j < 8; ++j) pl.qv[j] = q0[j];
-    if (append) {
-      const int mlane = a.rope_half / 2;
-      const bool first = (lane & mlane) == 0;
-      const float p0 = __shfl_xor(pl.knew[0].x, mlane, kWave);
-      const float p1 = __shfl_xor(pl.knew[0].y, mlane, kWave);
-      const bool rotated = a.rope_half == 64 || lane < 32;
-      if (rotated) {
-        typedef __attribute__((address_space(3))) float2v lds_float2v;
-        const float2v kinv = ((const lds_float2v*)rope_table)[lane & (mlane - 1)];
-        float sn0, cs0, sn1, cs1;
-        rope_sincos(fpos * kinv.x, &sn0, &cs0);
-        rope_sincos(fpos * kinv.y, &sn1, &cs1);
-        pl.knew[0].x = first ? pl.knew[0].x * cs0 - p0 * sn0 : p0 * sn0 + pl.knew[0].x * cs0;
-        pl.knew[0].y = first ? pl.knew[0].y * cs1 - p1 * sn1 : p1 * sn1 + pl.knew[0].y * cs1;
-      }
-    }
+    if (append) rope_new_k(pl.knew[0], a.rope_half, rope_table);
   }
 
   // Fused append: quantize the new token (lane: elements 2*lane, 2*lane+1 of
@@ -1206,7 +1213,7 @@ __global__ __launch_bounds__(kWave) void decode_mfma_kernel(DecodeArgs a) {
   // sliding window), so that every load of the piece is issued before the
   // sequence's length is known; a wrong guess reloads it.
   PieceLoads<REP, NH> pl;
-  __shared__ __attribute__((aligned(16))) uint8_t rope_table_[ROPE ? 256 : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t rope_table_[ROPE ? kRopeTableBytes : 16];
   stage_rope_table<ROPE>(a, (lds_u8*)rope_table_);
   piece_loads<REP, FUSED, ROPE, false, NH>(a, s, kvh, part * (a.split / kPage), pl);
   const SeqWindow w = seq_window<FUSED>(a, s);
@@ -1325,7 +1332,7 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
   constexpr int kSlots = Q8 ? 1 : DEPTH;  // Q8A: V is written to its slot when it is used
   __shared__ __attribute__((aligned(16))) uint8_t vring_[kSlots * NH * kVSlot];
   __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * NH * kRowBytes];  // K row, V row (f16)
-  __shared__ __attribute__((aligned(16))) uint8_t rope_table_[ROPE ? 256 : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t rope_table_[ROPE ? kRopeTableBytes : 16];
   stage_rope_table<ROPE>(a, (lds_u8*)rope_table_);
   const int wv = blockIdx.x;
   const int n_groups = (n_seq + kWave - 1) / kWave;
@@ -1488,7 +1495,7 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
   typedef __attribute__((address_space(3))) float lds_f32;
   __shared__ __attribute__((aligned(16))) uint8_t vring_[NW][kSlots * NH * kVSlot];
   __shared__ __attribute__((aligned(16))) uint8_t newtok_[NW][2 * NH * kRowBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t rope_table_[NW][ROPE ? 256 : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t rope_table_[NW][ROPE ? kRopeTableBytes : 16];
   __shared__ __attribute__((aligned(16))) float part_[NW * 2 * REP * kRow];
   __shared__ int split_[NW + 1][4];  // cut segments: s, kv head, x0, x1
   __shared__ int n_split_;

@@ -99,17 +99,55 @@ __device__ __forceinline__ float cross_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// sin and cos of a RoPE angle theta (the f32 product pos * inv_freq, as the
-// reference forms it): the angle is reduced to [0, 1) revolutions in f64
-// (theta/2pi exact to ~1e-16 relative, so even angles of ~1e5 rad keep ~1e-11
-// revolutions of precision), then v_sin_f32 / v_cos_f32, which take
-// revolutions.  Absolute error ~1e-6, against ~1e-3 relative for one f16 ulp.
+// RoPE's sine and cosine of the f32 angle theta (pos * inv_freq, the
+// reference's angle), each rounded once to f32 from an f64 evaluation:
+// Cody-Waite reduction by pi/2 (pi/2 split into two 26-bit parts and a 53-bit
+// tail, so that k times a part is exact for |k| < 2^27), then Taylor
+// polynomials in r^2 on |r| <= pi/4 (sine to r^17, cosine to r^18:
+// truncation below 1e-19), every step one IEEE f64 operation or fma, none
+// contracted.  The oracle evaluates the same steps in the same order, so the
+// rotated values agree bit for bit; both equal the correctly rounded sin/cos
+// unless the exact value lies within ~1e-16 (relative) of an f32 rounding
+// boundary.
 __device__ __forceinline__ void rope_sincos(float theta, float* s, float* c) {
-  double r = (double)theta * 0.15915494309189533577;  // 1 / (2 pi)
-  r -= floor(r);
-  const float rf = (float)r;
-  *s = __builtin_amdgcn_sinf(rf);
-  *c = __builtin_amdgcn_cosf(rf);
+#pragma clang fp contract(off)
+  const double t = (double)theta;
+  const double k = rint(t * 0x1.45f306dc9c883p-1);  // nearest multiple of pi/2
+  const double r = ((t - k * 0x1.921fb5p+0) - k * 0x1.110b46p-26) - k * 0x1.1a62633145c07p-54;
+  const double z = r * r;
+  double ps = 0x1.952c77030ad4ap-49;  // 1/17!
+  ps = fma(ps, z, -0x1.ae7f3e733b81fp-41);
+  ps = fma(ps, z, 0x1.6124613a86d09p-33);
+  ps = fma(ps, z, -0x1.ae64567f544e4p-26);
+  ps = fma(ps, z, 0x1.71de3a556c734p-19);
+  ps = fma(ps, z, -0x1.a01a01a01a01ap-13);
+  ps = fma(ps, z, 0x1.1111111111111p-7);
+  ps = fma(ps, z, -0x1.5555555555555p-3);  // -1/3!
+  const double sr = fma(r * z, ps, r);
+  double pc = -0x1.6827863b97d97p-53;  // -1/18!
+  pc = fma(pc, z, 0x1.ae7f3e733b81fp-45);
+  pc = fma(pc, z, -0x1.93974a8c07c9dp-37);
+  pc = fma(pc, z, 0x1.1eed8eff8d898p-29);
+  pc = fma(pc, z, -0x1.27e4fb7789f5cp-22);
+  pc = fma(pc, z, 0x1.a01a01a01a01ap-16);
+  pc = fma(pc, z, -0x1.6c16c16c16c17p-10);
+  pc = fma(pc, z, 0x1.5555555555555p-5);
+  pc = fma(pc, z, -0x1.0000000000000p-1);  // -1/2!
+  const double cr = fma(z, pc, 1.0);
+  const int q = (int)((long long)k & 3);
+  const double sv = q == 0 ? sr : (q == 1 ? cr : (q == 2 ? -sr : -cr));
+  const double cv = q == 0 ? cr : (q == 1 ? -sr : (q == 2 ? -cr : sr));
+  *s = (float)sv;
+  *c = (float)cv;
+}
+
+// One RoPE pair (x0, x1) = (dim i, dim i + half) turned by (s, c): x0 c - x1 s
+// and x0 s + x1 c, each product and each sum rounded once (no fused
+// multiply-add), as the oracle computes them.
+__device__ __forceinline__ void rope_turn(float x0, float x1, float s, float c, float* y0, float* y1) {
+#pragma clang fp contract(off)
+  *y0 = x0 * c - x1 * s;
+  *y1 = x0 * s + x1 * c;
 }
 
 // Converts one f32 to the page dtype's bits; Q8A needs the head's scale.

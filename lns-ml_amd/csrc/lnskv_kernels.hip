@@ -175,9 +175,11 @@ __global__ __launch_bounds__(kBlock) void append_vec_kernel(AppendArgs a, int ro
       const float fpos = (float)pos;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        float sn, cs;
+        float sn, cs, y0, y1;
         rope_sincos(fpos * f[j], &sn, &cs);
-        x[j] = first ? x[j] * cs - p[j] * sn : p[j] * sn + x[j] * cs;
+        // (dim i, dim i + half) = (x, partner) in the first half, (partner, x) in the second
+        rope_turn(first ? x[j] : p[j], first ? p[j] : x[j], sn, cs, &y0, &y1);
+        x[j] = first ? y0 : y1;
       }
       k0 = make_float4(x[0], x[1], x[2], x[3]);
       k1 = make_float4(x[4], x[5], x[6], x[7]);
@@ -292,10 +294,10 @@ __global__ __launch_bounds__(kBlock) void rope_rows_kernel(const float* x, float
     float v = xr[idx];
     if (i < 2 * half) {
       const int kk = i < half ? i : i - half;
-      float sn, cs;
+      float sn, cs, y0, y1;
       rope_sincos(fpos * inv[kk], &sn, &cs);
-      const float x0 = xr[h * d + kk], x1 = xr[h * d + kk + half];
-      v = i < half ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
+      rope_turn(xr[h * d + kk], xr[h * d + kk + half], sn, cs, &y0, &y1);
+      v = i < half ? y0 : y1;
     }
     yr[idx] = v;
   }

@@ -71,6 +71,7 @@ def lib() -> C.CDLL:
             "orc_max_threads": (i32, []),
             "orc_rope_inv_freqs": (None, [i32, C.c_float, i32, vp, vp]),
             "orc_rope_apply": (None, [vp, i32, i32, i32, i32, vp, i32, vp]),
+            "orc_rope_sincos": (None, [C.c_float, vp, vp]),
             "orc_split_gated_query": (None, [vp, vp, vp, i32, i32, i32]),
             "orc_q4l_prepare": (None, [vp, i32, vp]),
             "orc_q4l_decode_block": (None, [vp, vp]),
@@ -300,6 +301,18 @@ def rope_inv_freqs(rotary_dim: int, theta: float, mode: int = ROPE_DEFAULT, para
     out = np.zeros(rotary_dim // 2, np.float32)
     lib().orc_rope_inv_freqs(rotary_dim, theta, mode, _p(p), _p(out))
     return out
+
+
+def rope_sincos(theta) -> tuple[np.ndarray, np.ndarray]:
+    """orc_rope_sincos over an array of f32 angles: (sin, cos) float32."""
+    th = np.ascontiguousarray(theta, np.float32).ravel()
+    sn = np.empty_like(th)
+    cs = np.empty_like(th)
+    a, b = C.c_float(), C.c_float()
+    for i, t in enumerate(th):
+        lib().orc_rope_sincos(float(t), C.byref(a), C.byref(b))
+        sn[i], cs[i] = a.value, b.value
+    return sn, cs
 
 
 def rope_apply(x, rotary_dim: int, inv_freqs, pos) -> np.ndarray:

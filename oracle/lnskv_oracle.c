@@ -552,6 +552,49 @@ void orc_rope_inv_freqs(int rotary_dim, float theta, int mode, const float* para
   }
 }
 
+/* sin and cos of a RoPE angle (the f32 product pos * inv_freq[i], as
+ * engine.rs:217 and lns_decode.metal:176 form it).  The reference takes them
+ * from the platform's f32 sin_cos (engine.rs:218, Rust -> libm) or Metal's
+ * fast sincos (lns_decode.metal:178), whose last bits differ between
+ * platforms; this restatement fixes them as one rounding to f32 of an f64
+ * evaluation: Cody-Waite reduction by pi/2 (pi/2 split into two 26-bit parts
+ * and a 53-bit tail, derived from pi to 80 digits; k times a part is exact
+ * for |k| < 2^27), then the Taylor series of sin to r^17 and of cos to r^18
+ * on |r| <= pi/4, in Horner form with fused multiply-adds.  The library
+ * evaluates the same steps in the same order.  Pinned against libm's double
+ * sin/cos (tests/test_rope_oracle.py): within 4 ulp of f64, and its f32
+ * roundings equal the f32 roundings of libm's double results. */
+void orc_rope_sincos(float theta, float* s, float* c) {
+  const double t = (double)theta;
+  const double k = rint(t * 0x1.45f306dc9c883p-1);
+  const double r = ((t - k * 0x1.921fb5p+0) - k * 0x1.110b46p-26) - k * 0x1.1a62633145c07p-54;
+  const double z = r * r;
+  double ps = 0x1.952c77030ad4ap-49;
+  ps = fma(ps, z, -0x1.ae7f3e733b81fp-41);
+  ps = fma(ps, z, 0x1.6124613a86d09p-33);
+  ps = fma(ps, z, -0x1.ae64567f544e4p-26);
+  ps = fma(ps, z, 0x1.71de3a556c734p-19);
+  ps = fma(ps, z, -0x1.a01a01a01a01ap-13);
+  ps = fma(ps, z, 0x1.1111111111111p-7);
+  ps = fma(ps, z, -0x1.5555555555555p-3);
+  const double sr = fma(r * z, ps, r);
+  double pc = -0x1.6827863b97d97p-53;
+  pc = fma(pc, z, 0x1.ae7f3e733b81fp-45);
+  pc = fma(pc, z, -0x1.93974a8c07c9dp-37);
+  pc = fma(pc, z, 0x1.1eed8eff8d898p-29);
+  pc = fma(pc, z, -0x1.27e4fb7789f5cp-22);
+  pc = fma(pc, z, 0x1.a01a01a01a01ap-16);
+  pc = fma(pc, z, -0x1.6c16c16c16c17p-10);
+  pc = fma(pc, z, 0x1.5555555555555p-5);
+  pc = fma(pc, z, -0x1.0000000000000p-1);
+  const double cr = fma(z, pc, 1.0);
+  const int q = (int)((long long)k & 3);
+  const double sv = q == 0 ? sr : (q == 1 ? cr : (q == 2 ? -sr : -cr));
+  const double cv = q == 0 ? cr : (q == 1 ? -sr : (q == 2 ? -cr : sr));
+  *s = (float)sv;
+  *c = (float)cv;
+}
+
 /* apply_cpu_rope_with_freqs, engine.rs:200-229 (the same rotation as the
  * rope_with_freqs kernel, lns_decode.metal:158-191): the first rotary_dim
  * elements of a head are two halves (x0 = first[i], x1 = second[i]) rotated
@@ -568,7 +611,8 @@ void orc_rope_apply(float* x, int n_rows, int heads, int head_dim, int rotary_di
       float* v = x + ((size_t)r * heads + h) * head_dim;
       for (int i = 0; i < n; ++i) {
         const float angle = (float)pos[r] * inv_freqs[i];
-        const float sn = sinf(angle), cs = cosf(angle);
+        float sn, cs;
+        orc_rope_sincos(angle, &sn, &cs);
         const float x0 = v[i], x1 = v[half + i];
         v[i] = x0 * cs - x1 * sn;
         v[half + i] = x0 * sn + x1 * cs;

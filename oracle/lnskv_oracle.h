@@ -117,6 +117,9 @@ enum { ORC_ROPE_DEFAULT = 0, ORC_ROPE_LINEAR = 1, ORC_ROPE_LLAMA3 = 2, ORC_ROPE_
  * low_freq_factor, high_freq_factor}, YARN {factor, original_max_pos,
  * beta_fast, beta_slow}.  f32 arithmetic throughout, as the reference. */
 void orc_rope_inv_freqs(int rotary_dim, float theta, int mode, const float* params, float* out);
+/* sin and cos of the f32 angle theta: one f32 rounding of an f64 evaluation
+ * (Cody-Waite by pi/2, Taylor series; see the definition). */
+void orc_rope_sincos(float theta, float* s, float* c);
 /* apply_cpu_rope_with_freqs (engine.rs:200-229) on x[n_rows][heads][head_dim]
  * in place; row r is at position pos[r]; angle_i = pos * inv_freqs[i]. */
 void orc_rope_apply(float* x, int n_rows, int heads, int head_dim, int rotary_dim, const float* inv_freqs,

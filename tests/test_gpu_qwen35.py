@@ -9,12 +9,10 @@ lnskv_gated_append_decode call.
 Cases: the reference's one-sequence call at position 4095 (the workgroup
 schedule) and a batch of 32 at contexts U[512, 4096] (stream-K), Q8A and f16
 pages, some sequences on a sliding window.  Against the oracle, which
-rotates, appends (quantizes) and attends in float64: the pages the call
-writes match the oracle's (bit for bit but for the rotated K, whose values
-are within the rotation's bound: one unit in the last place / one int8 code
-plus 4e-6 of the row's largest value), every other byte is unchanged, and the
-output rows are within the tolerance (1e-5 Q8A, 1e-3 f16) of the float64
-attention over the pages the call stored, times the gate."""
+rotates, appends (quantizes) and attends in float64: every byte of the pools
+and scales matches the oracle's (the rotated, quantized new token included),
+and the output rows are within the tolerance (1e-5 Q8A, 1e-3 f16) of the
+float64 attention times the gate."""
 import numpy as np
 import pytest
 import torch
@@ -77,7 +75,7 @@ def test_qwen35_step(gpu, dtype, case):
     sync()
     got, _ = host_pages(pk)
     _check_pages(got, hp, before, dtype)
-    ref = O.decode_f64(got, q_r, tables, lens, p_start, scale) * gate.astype(np.float64)
+    ref = O.decode_f64(hp, q_r, tables, lens, p_start, scale) * gate.astype(np.float64)
     err = rel_err(out, ref)
     say("max row error", float(err.max()))
     assert err.max() < TOL[dtype]

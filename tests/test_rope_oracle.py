@@ -86,6 +86,55 @@ def test_rotation_closed_forms(d, rd):
     np.testing.assert_allclose(n_out, n_in, rtol=1e-5, atol=1e-6)
 
 
+def test_rope_sincos_is_libm_double_rounded_once():
+    """orc_rope_sincos (the rotation's sin/cos, evaluated in f64 and rounded
+    once) against libm's double sin/cos of the same f32 angle rounded to f32:
+    equal wherever libm's double value is not within 1e-13 (relative) of an
+    f32 rounding boundary, over small, RoPE-sized and large angles up to
+    2^26 rad, zero (a RoPE angle is pos * inv_freq >= 0: never -0) and quadrant
+    edges; a dropped reduction term, a wrong
+    quadrant or sign, or a polynomial coefficient off by one term would each
+    fail this.  Also sin^2 + cos^2 = 1 to f32 rounding."""
+    rng = np.random.default_rng(11)
+    th = np.concatenate([
+        rng.uniform(-4.0, 4.0, 4000), rng.uniform(0.0, 8192.0, 4000), rng.uniform(0.0, 2.0 ** 20, 2000),
+        rng.uniform(0.0, 2.0 ** 26, 500), np.arange(0, 64) * (np.pi / 4), [0.0, 1e-30, 1e-8, 65504.0],
+    ]).astype(np.float32)
+    sn, cs = O.rope_sincos(th)
+    t64 = th.astype(np.float64)
+    for got, ref in ((sn, np.sin(t64)), (cs, np.cos(t64))):
+        r32 = ref.astype(np.float32)
+        # distance of libm's value from the nearest f32 midpoint, in units of the value
+        lo = np.nextafter(r32, np.float32(-np.inf)).astype(np.float64)
+        hi = np.nextafter(r32, np.float32(np.inf)).astype(np.float64)
+        mid = np.minimum(np.abs(ref - (r32.astype(np.float64) + lo) / 2), np.abs(ref - (r32.astype(np.float64) + hi) / 2))
+        safe = mid > 1e-13 * np.maximum(np.abs(ref), 1e-300)
+        assert safe.mean() > 0.99
+        assert np.array_equal(got[safe].view(np.uint32), r32[safe].view(np.uint32))
+    n = sn.astype(np.float64) ** 2 + cs.astype(np.float64) ** 2
+    np.testing.assert_allclose(n, 1.0, rtol=0, atol=3e-7)
+    assert sn[np.flatnonzero(th == 0.0)[0]] == 0.0 and cs[np.flatnonzero(th == 0.0)[0]] == 1.0
+
+
+def test_rotation_uses_rope_sincos_and_two_roundings():
+    """orc_rope_apply turns each pair with orc_rope_sincos's values and rounds
+    each product and each sum once: recomputed here from rope_sincos with
+    float32 numpy arithmetic (which rounds every operation), bit for bit."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 2, 128)).astype(np.float32)
+    inv = O.rope_inv_freqs(64, 1.0e7)
+    pos = np.array([5, 4095, 100000], np.int32)
+    y = O.rope_apply(x, 64, inv, pos)
+    for r in range(3):
+        ang = (np.float32(pos[r]) * inv).astype(np.float32)
+        sn, cs = O.rope_sincos(ang)
+        x0, x1 = x[r, :, :32], x[r, :, 32:64]
+        y0 = (x0 * cs).astype(np.float32) - (x1 * sn).astype(np.float32)
+        y1 = (x0 * sn).astype(np.float32) + (x1 * cs).astype(np.float32)
+        assert np.array_equal(y[r, :, :32], y0) and np.array_equal(y[r, :, 32:64], y1)
+        assert np.array_equal(y[r, :, 64:], x[r, :, 64:])
+
+
 def test_scores_depend_on_position_difference():
     rng = np.random.default_rng(3)
     q = rng.standard_normal((1, 1, 128)).astype(np.float32)
