@@ -131,6 +131,15 @@ def read_ceiling(dev, mib: int = 1024, reps: int = 10) -> dict:
             "sweep_gbs": sweep, "note": "loads in flight per thread x workgroups of 256 threads per CU"}
 
 
+def sk_waves(w, runner) -> int:
+    """The stream-K decode's wave count for this workload, read back from the
+    library's workspace size (header + per wave 2 * rep partial rows of
+    (acc[d], m, l) and a 16-byte descriptor)."""
+    ws = runner.layers[0].workspace_size(runner.n_dec, w.n_heads, runner.max_kv_len, 0)
+    per_wave = 2 * w.rep * (w.head_dim + 2) * 4 + 16
+    return (ws - 4096) // per_wave
+
+
 def pattern_ceiling(w, runner, dev, reps: int) -> dict | None:
     """Load ceiling of the step's decode page pattern, timed live with HIP
     events: lnskv_read_units over the same (page, kv head) units as the
@@ -149,7 +158,7 @@ def pattern_ceiling(w, runner, dev, reps: int) -> dict | None:
 
     row_bytes = w.head_dim * {0: 4, 1: 2, 2: 1}[w.dtype]
     q8 = w.dtype == 2
-    if reps <= 0 or runner.n_dec == 0 or not (row_bytes == 256 and not q8 or row_bytes == 128 and q8):
+    if reps <= 0 or runner.n_dec == 0 or not (row_bytes in (256, 512) and not q8 or row_bytes in (128, 256) and q8):
         return None
     pages, kvhs = [], []
     for s in runner.dec_rows:
@@ -161,7 +170,7 @@ def pattern_ceiling(w, runner, dev, reps: int) -> dict | None:
     unit_page = np.concatenate(pages)
     unit_kvh = np.concatenate(kvhs)
     n_units = len(unit_page)
-    waves = torch.cuda.get_device_properties(dev).multi_processor_count * (8 if q8 else 4)
+    waves = sk_waves(w, runner)
     chunk = max(4, -(-n_units // waves))
     start = np.minimum(np.arange(waves + 1, dtype=np.int64) * chunk, n_units).astype(np.int32)
     d_page = torch.from_numpy(unit_page.view(np.int32)).to(dev)
@@ -480,6 +489,64 @@ def full_copy_fork(w, runner, dev, reps: int = 20) -> dict:
             "note": "every page of the 8 forked children copied (the page-sharing fork copies only tail pages)"}
 
 
+def qwen35_measure(dev, steps: int, layers: int = 4, pattern_reps: int = 40) -> dict:
+    """lns-ml's own full-attention layer (Qwen3.5: Hq16/Hkv4/d256) on the
+    engine's Q8A pages, the engine's per-layer order in one call
+    (lnskv_gated_append_decode: RoPE rotary 64 of 256 with theta 1e7 turned
+    in registers, the quantizing append, the decode, the query gate): a batch
+    of 32 at c2's contexts U[512, 4096] (stream-K), with its page pattern's
+    load ceiling; and the reference's one-sequence call at pos 4095 (one
+    kernel, the workgroup schedule), per call from HIP graph replay over 32
+    layers.  Bytes: the K/V codes and scales of every attended token, the
+    append, q/out, the gate read, table entries."""
+    import torch
+
+    from lnskv import DTYPE_Q8A
+    from lnskv.configs import make
+    from lnskv.device import RopeTable
+    from lnskv.step import StepRunner
+
+    def gated_bytes(w):
+        return w.algorithmic_bytes()["total"] + int(w.decode.sum()) * w.n_heads * w.head_dim * 4
+
+    rope = RopeTable(64, 1.0e7, device=dev)
+    w = make("qwen35", dtype=DTYPE_Q8A)
+    runner = StepRunner(w, dev, n_layers=layers, seed=1, rope=rope, gated=True)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    step = lambda i: runner.run(i % layers)  # noqa: E731
+    ev, wall = timed_steps(step, stream, steps, 10)
+    nb = gated_bytes(w)
+    res = {"shape": "32 sequences at U[512,4096], Hq16/Hkv4/d256, Q8A pages, RoPE rotary 64 (theta 1e7), gated",
+           "us_per_step_events": round(ev * 1e6, 2), "us_per_step_wall": round(wall * 1e6, 2),
+           "algorithmic_bytes": int(nb), "gb_per_s": round(nb / ev / 1e9, 1),
+           "frac_of_hbm_peak": round(nb / ev / 1e9 / HBM_PEAK_GBS, 4)}
+    pc = pattern_ceiling(w, runner, dev, pattern_reps)
+    if pc:
+        res["pattern_ceiling_us"] = pc["us_per_launch"]
+        res["frac_of_pattern_ceiling"] = round(pc["us_per_launch"] / (ev * 1e6), 4)
+    del runner
+    torch.cuda.empty_cache()
+    # the one-sequence call, 32 layers' pools cycled
+    w1 = make("qwen35", n_seq=1, lo=4095, hi=4095, num_pages=256 + 8, dtype=DTYPE_Q8A)
+    r1 = StepRunner(w1, dev, n_layers=32, seed=2, rope=rope, gated=True)
+    for i in range(64):
+        r1.run(i % 32)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(32):
+            r1.run(i)
+    torch.cuda.synchronize()
+    ev_g, _ = timed_steps(lambda i: graph.replay(), stream, 20, 3)
+    nb1 = gated_bytes(w1)
+    res["b1_pos4095"] = {"us_per_call_graph_replay": round(ev_g / 32 * 1e6, 2), "bytes_per_call": int(nb1),
+                         "gb_per_s": round(nb1 / (ev_g / 32) / 1e9, 1)}
+    del graph, r1
+    torch.cuda.empty_cache()
+    return res
+
+
 def reference_call_measure(dev, calls: int = 400, n_layers: int = 32) -> dict:
     """The reference's own call: lnskv_attention_paged (encode_attention_paged_q8a's
     arguments) for ONE sequence, Hq32/Hkv8/d128 on Q8A pages, appending the
@@ -714,6 +781,7 @@ def main():
         extras = {"c2_q8a_pages": config_measure("c2", dev, args.steps, layers=args.layers, kv_dtype=2,
                                                  pattern_reps=args.pattern_reps),
                   "reference_call_b1_q8a": reference_call_measure(dev),
+                  "qwen35_shape": qwen35_measure(dev, min(args.steps, 100), pattern_reps=args.pattern_reps),
                   "block_table_upload": table_upload_measure(w, dev)}
         for name in ("c1", "c3", "c4", "c5"):
             extras[name] = config_measure(name, dev, min(args.steps, 100))

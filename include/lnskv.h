@@ -495,15 +495,15 @@ int lnskv_block_tables_upload(const lnskv_block_tables* t, uint32_t* dst_dev,
  * wave w taking units [wave_start[w], wave_start[w + 1]) with two units in
  * flight.  Given the units of a decode step in the decode's order and wave
  * split, its duration is the load ceiling of that step's page pattern.  Rows
- * of 256 bytes (head_dim x dtype bytes: f16 d128, f32 d64) or Q8A rows of 128
- * bytes (d128); page ids >= num_pages and kv heads outside [0, n_kv_heads)
- * read page 0 / kv head 0.  wave_start holds n_waves + 1 non-decreasing
- * indices into the unit lists.  sink[w * 64 + lane] receives the XOR of the
- * 32-bit words lane loaded for wave w's units, each unit once: 256-byte rows,
- * lane (r, c) = (lane / 16, lane % 16): 16-byte chunk c of rows r, r + 4,
- * r + 8, r + 12 of K and V; Q8A, lane (r, c) = (lane / 8, lane % 8): chunk c
- * of rows r and r + 8 of K and V, and the scale of token lane % 16 (V for
- * lanes with bit 4 set, K otherwise). */
+ * (head_dim x dtype bytes) of 256 bytes (f16 d128, f32 d64) or 512 (f16
+ * d256), Q8A rows of 128 (d128) or 256 bytes (d256); page ids >= num_pages
+ * and kv heads outside [0, n_kv_heads) read page 0 / kv head 0.  wave_start
+ * holds n_waves + 1 non-decreasing indices into the unit lists.
+ * sink[w * 64 + lane] receives the XOR of the 32-bit words lane loaded for
+ * wave w's units, each unit once: with L = row bytes / 16 lanes per row, lane
+ * (r, c) = (lane / L, lane % L) loads 16-byte chunk c of rows r, r + 64/L,
+ * ... (< 16) of K and of V, and for Q8A pages also the scale of token
+ * lane % 16 (V for lanes with bit 4 set, K otherwise). */
 int lnskv_read_units(const lnskv_pages* c, const uint32_t* unit_page, const int32_t* unit_kvh,
                      const int32_t* wave_start, int32_t n_waves, uint32_t* sink,
                      lnskv_stream_t stream);

@@ -8,6 +8,8 @@
 // units, in the same order and wave split, as a decode step, it gives the
 // bandwidth the memory system delivers for that pattern with nothing else in
 // the way.
+#include <type_traits>
+
 #include "lnskv_device.h"
 
 namespace lnskv {
@@ -20,81 +22,79 @@ __device__ __forceinline__ void wait_loads() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// The loads of one unit (16 token rows of one kv head in K and in V):
-// ROW = 256 (f16 / d128, f32 / d64): lane (r, c) = (lane / 16, lane % 16)
-//   loads 16-byte chunk c of rows r, r + 4, r + 8, r + 12: 8 loads.
-// ROW = 128 (Q8A / d128): lane (r, c) = (lane / 8, lane % 8) loads chunk c of
-//   rows r and r + 8 in K and V, plus one 4-byte scale: that of token
-//   lane % 16, from V for lanes with bit 4 set and from K otherwise: 5 loads,
-//   the bytes the Q8A decode reads per unit.
-template <int ROW>
+// The loads of one unit (16 token rows of one kv head in K and in V), rows
+// of ROW bytes (128: Q8A d128; 256: f16 d128, f32 d64, Q8A d256; 512: f16
+// d256), kL = ROW / 16 lanes per row: lane (r, c) = (lane / kL, lane % kL)
+// loads 16-byte chunk c of rows r, r + 64/kL, ... of K and of V (the 16
+// rows once each), then, with SC (Q8A pages), one 4-byte scale: that of
+// token lane % 16, from V for lanes with bit 4 set and from K otherwise --
+// the bytes a decode reads per unit.
+template <int ROW, bool SC>
 struct Unit {
-  static constexpr int kLoads = ROW == 256 ? 8 : 5;
+  static constexpr int kLanesPerRow = ROW / 16;
+  static constexpr int kRowsPerLoad = kWave / kLanesPerRow;
+  static constexpr int kLoadsPerPool = kPage / kRowsPerLoad;
+  static constexpr int kLoads = 2 * kLoadsPerPool + (SC ? 1 : 0);
 };
 
-template <int ROW>
+template <int ROW, bool SC>
 __device__ __forceinline__ void load_unit(const uint8_t* k, const uint8_t* v, const float* ks, const float* vs,
                                           uint32_t page, int32_t kvh, uint32_t num_pages, int32_t n_kv,
-                                          u32x4 (&b)[8]) {
+                                          u32x4 (&b)[Unit<ROW, SC>::kLoads]) {
+  using U = Unit<ROW, SC>;
   const int lane = (int)(threadIdx.x & (kWave - 1));
   // ids outside the pools read page 0 / kv head 0 (in bounds)
   const size_t pg = page < num_pages ? page : 0u;
   const size_t h = kvh >= 0 && kvh < n_kv ? (size_t)kvh : 0u;
   const size_t row_bytes = (size_t)n_kv * ROW;
-  if constexpr (ROW == 256) {
-    const size_t base = pg * kPage * row_bytes + h * ROW + (size_t)(lane >> 4) * row_bytes + (size_t)(lane & 15) * 16;
+  const size_t base = pg * kPage * row_bytes + h * ROW + (size_t)(lane / U::kLanesPerRow) * row_bytes +
+                      (size_t)(lane % U::kLanesPerRow) * 16;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      b[j] = *reinterpret_cast<const u32x4*>(k + base + (size_t)j * 4 * row_bytes);
-      b[4 + j] = *reinterpret_cast<const u32x4*>(v + base + (size_t)j * 4 * row_bytes);
-    }
-  } else {
-    const size_t base = pg * kPage * row_bytes + h * ROW + (size_t)(lane >> 3) * row_bytes + (size_t)(lane & 7) * 16;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      b[j] = *reinterpret_cast<const u32x4*>(k + base + (size_t)j * 8 * row_bytes);
-      b[2 + j] = *reinterpret_cast<const u32x4*>(v + base + (size_t)j * 8 * row_bytes);
-    }
+  for (int j = 0; j < U::kLoadsPerPool; ++j) {
+    b[j] = *reinterpret_cast<const u32x4*>(k + base + (size_t)j * U::kRowsPerLoad * row_bytes);
+    b[U::kLoadsPerPool + j] = *reinterpret_cast<const u32x4*>(v + base + (size_t)j * U::kRowsPerLoad * row_bytes);
+  }
+  if constexpr (SC) {
     const float* sp = (lane & 16) ? vs : ks;
     const float sc = sp[(pg * kPage + (size_t)(lane & 15)) * (size_t)n_kv + h];
-    b[4] = u32x4{__builtin_bit_cast(uint32_t, sc), 0u, 0u, 0u};
+    b[2 * U::kLoadsPerPool] = u32x4{__builtin_bit_cast(uint32_t, sc), 0u, 0u, 0u};
   }
 }
 
-template <int ROW>
-__device__ __forceinline__ void fold(u32x4& acc, const u32x4 (&b)[8]) {
+template <int ROW, bool SC>
+__device__ __forceinline__ void fold(u32x4& acc, const u32x4 (&b)[Unit<ROW, SC>::kLoads]) {
 #pragma unroll
-  for (int j = 0; j < Unit<ROW>::kLoads; ++j) acc ^= b[j];
+  for (int j = 0; j < Unit<ROW, SC>::kLoads; ++j) acc ^= b[j];
 }
 
-template <int ROW>
+template <int ROW, bool SC>
 __global__ __launch_bounds__(kWave) void read_units_kernel(const uint8_t* k, const uint8_t* v, const float* ks,
                                                            const float* vs, const uint32_t* unit_page,
                                                            const int32_t* unit_kvh, const int32_t* wave_start,
                                                            uint32_t num_pages, int32_t n_kv, uint32_t* sink) {
-  constexpr int L = Unit<ROW>::kLoads;
+  constexpr int L = Unit<ROW, SC>::kLoads;
   const int w = blockIdx.x, lane = (int)(threadIdx.x & (kWave - 1));
   const int u0 = wave_start[w], u1 = wave_start[w + 1];
   u32x4 acc = {0u, 0u, 0u, 0u};
   if (u1 > u0) {
-    u32x4 b0[8], b1[8];
-    load_unit<ROW>(k, v, ks, vs, unit_page[u0], unit_kvh[u0], num_pages, n_kv, b0);
+    u32x4 b0[L], b1[L];
+    load_unit<ROW, SC>(k, v, ks, vs, unit_page[u0], unit_kvh[u0], num_pages, n_kv, b0);
     const int v1 = min(u0 + 1, u1 - 1);
-    load_unit<ROW>(k, v, ks, vs, unit_page[v1], unit_kvh[v1], num_pages, n_kv, b1);
+    load_unit<ROW, SC>(k, v, ks, vs, unit_page[v1], unit_kvh[v1], num_pages, n_kv, b1);
     int u = u0;
     for (; u + 2 < u1; u += 2) {
       wait_loads<L>();
-      fold<ROW>(acc, b0);
-      load_unit<ROW>(k, v, ks, vs, unit_page[u + 2], unit_kvh[u + 2], num_pages, n_kv, b0);
+      fold<ROW, SC>(acc, b0);
+      load_unit<ROW, SC>(k, v, ks, vs, unit_page[u + 2], unit_kvh[u + 2], num_pages, n_kv, b0);
       wait_loads<L>();
-      fold<ROW>(acc, b1);
+      fold<ROW, SC>(acc, b1);
       const int n1 = min(u + 3, u1 - 1);
-      load_unit<ROW>(k, v, ks, vs, unit_page[n1], unit_kvh[n1], num_pages, n_kv, b1);
+      load_unit<ROW, SC>(k, v, ks, vs, unit_page[n1], unit_kvh[n1], num_pages, n_kv, b1);
     }
     // b1 holds unit u + 1 when it exists, else a stand-in copy of unit u
     wait_loads<0>();
-    fold<ROW>(acc, b0);
-    if (u + 1 < u1) fold<ROW>(acc, b1);
+    fold<ROW, SC>(acc, b0);
+    if (u + 1 < u1) fold<ROW, SC>(acc, b1);
   }
   sink[(size_t)w * kWave + lane] = acc.x ^ acc.y ^ acc.z ^ acc.w;
 }
@@ -163,17 +163,24 @@ extern "C" int lnskv_read_units(const lnskv_pages* c, const uint32_t* unit_page,
   if (n_waves <= 0 || n_waves > 65535) return fail(LNSKV_ERR_INVALID, "n_waves %d out of range [1, 65535]", n_waves);
   const size_t row = (size_t)c->head_dim * dtype_bytes(c->dtype);
   const bool q8 = c->dtype == LNSKV_DTYPE_Q8A;
-  if (!(row == 256 && !q8) && !(row == 128 && q8))
-    return fail(LNSKV_ERR_UNSUPPORTED,
-                "the load probe reads 256-byte kv-head rows (f16 d128, f32 d64) or Q8A d128 rows (got %zu bytes)", row);
   const hipStream_t st = (hipStream_t)stream;
   const uint8_t* kp = static_cast<const uint8_t*>(c->k_pages);
   const uint8_t* vp = static_cast<const uint8_t*>(c->v_pages);
-  if (q8)
-    read_units_kernel<128><<<(unsigned)n_waves, kWave, 0, st>>>(kp, vp, c->k_scales, c->v_scales, unit_page, unit_kvh,
-                                                                wave_start, c->num_pages, (int32_t)c->n_kv_heads, sink);
+  const unsigned grid = (unsigned)n_waves;
+  const int32_t nkv = (int32_t)c->n_kv_heads;
+  auto probe = [&](auto row_c, auto sc_c) {
+    constexpr int R = decltype(row_c)::value;
+    constexpr bool S = decltype(sc_c)::value;
+    read_units_kernel<R, S><<<grid, kWave, 0, st>>>(kp, vp, S ? c->k_scales : nullptr, S ? c->v_scales : nullptr,
+                                                    unit_page, unit_kvh, wave_start, c->num_pages, nkv, sink);
+  };
+  if (row == 128 && q8) probe(std::integral_constant<int, 128>{}, std::true_type{});
+  else if (row == 256 && q8) probe(std::integral_constant<int, 256>{}, std::true_type{});
+  else if (row == 256) probe(std::integral_constant<int, 256>{}, std::false_type{});
+  else if (row == 512 && !q8) probe(std::integral_constant<int, 512>{}, std::false_type{});
   else
-    read_units_kernel<256><<<(unsigned)n_waves, kWave, 0, st>>>(kp, vp, nullptr, nullptr, unit_page, unit_kvh,
-                                                                wave_start, c->num_pages, (int32_t)c->n_kv_heads, sink);
+    return fail(LNSKV_ERR_UNSUPPORTED,
+                "the load probe reads kv-head rows of 256 or 512 bytes (f16 d128/d256, f32 d64) or Q8A rows of "
+                "128 or 256 bytes (d128/d256); got %zu bytes", row);
   return hip_check("load probe launch");
 }

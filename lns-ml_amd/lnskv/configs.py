@@ -25,7 +25,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from ._lib import DTYPE_F16, DTYPE_F32, NO_PAGE, PAGE_SIZE
+from ._lib import DTYPE_F16, DTYPE_F32, DTYPE_Q8A, NO_PAGE, PAGE_SIZE
 from .host import BlockTables, PagePool
 
 MASK64 = (1 << 64) - 1
@@ -321,7 +321,26 @@ def churn_plan(w: Workload, n_steps: int, seed: int = 1, n_free: int = 32, lo: i
     return plan
 
 
-MAKERS = {"c1": make_c1, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5}
+def make_qwen35(seed: int = 0, n_seq: int = 32, lo: int = 512, hi: int = 4096, num_pages: int = 16384,
+                dtype: int = DTYPE_Q8A) -> Workload:
+    """lns-ml's own full-attention layer (Qwen3.5, model_config.rs:563-593):
+    16 query heads, 4 kv heads, head_dim 256, on the engine's Q8A pages
+    (engine.rs:731-734), with c2's batch: n_seq sequences at seeded contexts
+    U[lo, hi], pages from a shuffled free list.  The step it is measured with
+    turns q and k by RoPE (rotary 64 of 256, theta 1e7) and multiplies the
+    output by the query gate (engine.rs:1700-1720, 3424-3431)."""
+    rl = SplitMix64(seed, S_LEN)
+    ctx = np.array([rl.randint(lo, hi) for _ in range(n_seq)], np.int32)
+    pool, _ = _shuffled_pool(num_pages, SplitMix64(seed, S_PERM))
+    stride = (hi + 1 + PAGE_SIZE - 1) // PAGE_SIZE
+    bt = BlockTables(n_seq, stride)
+    _alloc_rows(bt, pool, range(n_seq), ctx + 1)
+    w = Workload("qwen35", 16, 4, 256, dtype, num_pages, ctx, np.ones(n_seq, np.int32),
+                 np.ones(n_seq, bool), None, value_scale=0.5, seed=seed, pool=pool, bt=bt)
+    return _finish(w)
+
+
+MAKERS = {"c1": make_c1, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5, "qwen35": make_qwen35}
 
 
 def make(name: str, **kw) -> Workload:

@@ -32,9 +32,11 @@ def _i32(a: np.ndarray, dev) -> torch.Tensor:
 
 class StepRunner:
     def __init__(self, w: Workload, device="cuda", n_layers: int = 1, seed: int = 0,
-                 fill: bool = True, rope=None):
+                 fill: bool = True, rope=None, gated: bool = False):
         """rope: a RopeTable to run the step through the fused RoPE entry
-        points (q and the new K/chunk K are then taken before the rotation)."""
+        points (q and the new K/chunk K are then taken before the rotation).
+        gated: multiply the output by a per-element query gate in the same
+        call (lnskv_gated_append_decode, the gated attention's last step)."""
         self.w = w
         self.rope = rope
         self.dev = torch.device(device)
@@ -58,6 +60,7 @@ class StepRunner:
         self.k_new = torch.randn((self.n_dec, nkv, d), generator=g, device=self.dev) * w.value_scale
         self.v_new = torch.randn((self.n_dec, nkv, d), generator=g, device=self.dev) * w.value_scale
         self.out = torch.empty((self.n_dec, hq, d), device=self.dev)
+        self.gate = torch.rand((self.n_dec, hq, d), generator=g, device=self.dev) if gated else None
         cs, cp = w.chunk_tokens()
         self.n_chunk_tok = len(cs)
         self.chunk_seq = _i32(cs, self.dev)
@@ -100,7 +103,11 @@ class StepRunner:
             else:
                 pk.append(self.chunk_k, self.chunk_v, self.chunk_seq, self.chunk_pos, self.tables)
         if self.n_dec:
-            if self.rope is not None:
+            if self.gate is not None:
+                pk.gated_append_decode(self.gate, self.q, self.k_new, self.v_new, self.dec_tables, self.dec_kv_len,
+                                       n_heads=w.n_heads, max_kv_len=self.max_kv_len, scale=w.scale,
+                                       rope=self.rope, split=w.split, workspace=self.workspace, out=self.out)
+            elif self.rope is not None:
                 pk.rope_append_decode(self.rope, self.q, self.k_new, self.v_new, self.dec_tables, self.dec_kv_len,
                                       n_heads=w.n_heads, max_kv_len=self.max_kv_len, scale=w.scale,
                                       split=w.split, workspace=self.workspace, out=self.out)

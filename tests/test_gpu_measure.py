@@ -2,7 +2,8 @@
 equals the host XOR of exactly the bytes the header says it loads -- each
 unit once, empty waves zero, odd and even unit counts, page ids and kv heads
 outside the pools reading page 0 / kv head 0; 256-byte rows (f16 d128, f32
-d64) and Q8A rows (128 bytes plus the K and V scales)."""
+d64), 512-byte rows (f16 d256) and Q8A rows (128 or 256 bytes plus the K and
+V scales)."""
 import ctypes as C
 
 import numpy as np
@@ -17,46 +18,32 @@ from lnskv.device import PagedKV, _stream, sync
 pytestmark = pytest.mark.gpu
 
 
-def _expected(k32, v32, pages, kvhs, start, num_pages, n_kv):
-    """sink[w*64 + 16r + c]: XOR over the wave's units, K and V, rows r + 4j
-    (j < 4), of the four words of 16-byte chunk c of the unit's kv-head row."""
+def _expected(k32, v32, ks, vs, pages, kvhs, start, num_pages, n_kv, row_bytes):
+    """sink[w*64 + lane], lane (r, c) = (lane // L, lane % L) with L = row
+    bytes / 16: XOR over the wave's units, K and V, of the four words of
+    16-byte chunk c of rows r, r + 64/L, ... of the unit's kv-head row, plus
+    (Q8A: ks/vs given) one scale word: the V scale of token lane % 16 for
+    lanes with bit 4 set, the K scale otherwise."""
     n_waves = len(start) - 1
-    out = np.zeros((n_waves, 64), np.uint32)
-    for w in range(n_waves):
-        acc = np.zeros((4, 16), np.uint32)
-        for u in range(start[w], start[w + 1]):
-            p = int(pages[u]) if pages[u] < num_pages else 0
-            h = int(kvhs[u]) if 0 <= kvhs[u] < n_kv else 0
-            for pool in (k32, v32):
-                words = pool[p, :, h, :].reshape(16, 16, 4)              # row, chunk, word
-                chunk = np.bitwise_xor.reduce(words, axis=2)            # row, chunk
-                acc ^= np.bitwise_xor.reduce(chunk.reshape(4, 4, 16), axis=0)  # rows r + 4j -> r
-        out[w] = acc.reshape(64)
-    return out.reshape(-1)
-
-
-def _expected_q8(k32, v32, ks, vs, pages, kvhs, start, num_pages, n_kv):
-    """Q8A rows (128 bytes): sink[w*64 + 8r + c] XORs, over the wave's units,
-    chunk c of rows r and r + 8 of K and V, plus one scale word: the V scale
-    of token lane % 16 for lanes with bit 4 set, the K scale otherwise."""
-    n_waves = len(start) - 1
-    out = np.zeros((n_waves, 64), np.uint32)
+    L = row_bytes // 16
     lane = np.arange(64)
+    out = np.zeros((n_waves, 64), np.uint32)
     for w in range(n_waves):
         acc = np.zeros(64, np.uint32)
         for u in range(start[w], start[w + 1]):
             p = int(pages[u]) if pages[u] < num_pages else 0
             h = int(kvhs[u]) if 0 <= kvhs[u] < n_kv else 0
             for pool in (k32, v32):
-                chunk = np.bitwise_xor.reduce(pool[p, :, h, :].reshape(16, 8, 4), axis=2)  # row, chunk
-                acc ^= (chunk[:8] ^ chunk[8:]).reshape(64)
-            sc = np.where(lane & 16, vs[p * 16 + (lane & 15), h], ks[p * 16 + (lane & 15), h])
-            acc ^= sc
+                chunk = np.bitwise_xor.reduce(pool[p, :, h, :].reshape(16, L, 4), axis=2)  # row, chunk
+                acc ^= np.bitwise_xor.reduce(chunk.reshape(16 // (64 // L), 64 // L, L), axis=0).reshape(64)
+            if ks is not None:
+                acc ^= np.where(lane & 16, vs[p * 16 + (lane & 15), h], ks[p * 16 + (lane & 15), h])
         out[w] = acc
     return out.reshape(-1)
 
 
-@pytest.mark.parametrize("dtype,d", [(DTYPE_F16, 128), (DTYPE_F32, 64), (DTYPE_Q8A, 128)])
+@pytest.mark.parametrize("dtype,d", [(DTYPE_F16, 128), (DTYPE_F32, 64), (DTYPE_Q8A, 128), (DTYPE_Q8A, 256),
+                                     (DTYPE_F16, 256)])
 def test_read_units_checksum(gpu, dtype, d):
     say("read_units", dtype, d)
     n_kv, num_pages = 4, 40
@@ -82,12 +69,12 @@ def test_read_units_checksum(gpu, dtype, d):
     sync()
     k32 = pk.k.view(torch.int32).cpu().numpy().view(np.uint32).reshape(num_pages, 16, n_kv, -1)
     v32 = pk.v.view(torch.int32).cpu().numpy().view(np.uint32).reshape(num_pages, 16, n_kv, -1)
+    ks = vs = None
     if dtype == DTYPE_Q8A:
         ks = pk.ks.view(torch.int32).cpu().numpy().view(np.uint32)
         vs = pk.vs.view(torch.int32).cpu().numpy().view(np.uint32)
-        exp = _expected_q8(k32, v32, ks, vs, pages, kvhs, start, num_pages, n_kv)
-    else:
-        exp = _expected(k32, v32, pages, kvhs, start, num_pages, n_kv)
+    row_bytes = d * {DTYPE_F32: 4, DTYPE_F16: 2, DTYPE_Q8A: 1}[dtype]
+    exp = _expected(k32, v32, ks, vs, pages, kvhs, start, num_pages, n_kv, row_bytes)
     got = sink.cpu().numpy().view(np.uint32)
     assert np.array_equal(got, exp)
 
