@@ -45,6 +45,8 @@
 // it into its own registers / V slot when it reaches that page, so the scan
 // never reads the slot back.  Partitions are merged by combine_kernel.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -1329,8 +1331,7 @@ __device__ __forceinline__ int sk_chunk(int total, int n_waves) {
 template <int REP, bool FUSED, int DEPTH, bool ROPE, bool Q8 = false, int NH = 1>
 __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
-  constexpr int kSlots = Q8 ? 1 : DEPTH;  // Q8A: V is written to its slot when it is used
-  __shared__ __attribute__((aligned(16))) uint8_t vring_[kSlots * NH * kVSlot];
+  __shared__ __attribute__((aligned(16))) uint8_t vring_[DEPTH * NH * kVSlot];
   __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * NH * kRowBytes];  // K row, V row (f16)
   __shared__ __attribute__((aligned(16))) uint8_t rope_table_[ROPE ? kRopeTableBytes : 16];
   stage_rope_table<ROPE>(a, (lds_u8*)rope_table_);
