@@ -1140,10 +1140,11 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
   auto step = [&](int i, PageQ8<NH>& pg, bool& valid, bool steady) {
     const int ahead = steady ? DEPTH - 1 : min(npg - 1 - i, DEPTH - 1);  // pages issued after page i
     constexpr int kLoads = 4 * NH + 2;  // vector-memory loads per page
-    if (ahead >= 3) wait_vmcnt<3 * kLoads>();
-    else if (ahead == 2) wait_vmcnt<2 * kLoads>();
-    else if (ahead == 1) wait_vmcnt<kLoads>();
-    else wait_vmcnt<0>();
+    static_assert(kLoads * (DEPTH - 1) < 64, "vmcnt range");
+    static_for<DEPTH>([&](auto c) {
+      constexpr int k = decltype(c)::value;
+      if (ahead == DEPTH - 1 - k) wait_vmcnt<kLoads * (DEPTH - 1 - k)>();
+    });
     const int tok0 = (pg_first + i) * kPage;
     if (attend_new && pos / kPage == pg_first + i) {
       // the loads may predate the store: take the new token's codes and
@@ -1817,22 +1818,24 @@ constexpr int kSkWavesPerCu = 4;
 // scales), so two waves per SIMD hide each other's per-page dependency chain:
 // c2-shaped Q8A step 57.2 us with four waves per CU, 53.7 with eight; two,
 // three or four pages in flight per wave measured the same.
+// Measured against codes by LDS DMA into a ring of code slots (no registers
+// for pages in flight): 56.4 us per c2 Q8A step with one wave per SIMD and six
+// pages in flight, 51.0-51.4 with two waves and three, against 49.5 here.
 constexpr int kSkDepthQ8 = 2;
 constexpr int kSkWavesPerCuQ8 = 8;
 
-template <int REP, bool FUSED, bool Q8, int NH>
+// Resident waves of one stream-K kernel (ROPE: the fused variant that turns
+// RoPE in registers, whose extra registers may fit fewer waves), capped at
+// the launch shape's waves per CU.
+template <int REP, bool FUSED, bool Q8, int NH, bool ROPE>
 int sk_waves_of(int cus, int* waves) {
-  // the smaller occupancy of the plain and (fused) RoPE variants, so one wave
-  // count serves both
-  int per_cu = 0, per_cu_rope = 0;
+  int per_cu = 0;
   constexpr int depth = Q8 ? kSkDepthQ8 : kSkDepth;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, depth, false, Q8, NH>,
-                                                   kWave, 0) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rope, decode_sk_kernel<REP, FUSED, depth, FUSED, Q8, NH>,
-                                                   kWave, 0) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, depth, ROPE, Q8, NH>, kWave,
+                                                   0) != hipSuccess)
     per_cu = 0;
-  if (per_cu <= 0 || per_cu_rope <= 0) return fail(LNSKV_ERR_HIP, "occupancy query of the stream-K decode kernel failed");
-  *waves = cus * std::min(std::min(per_cu, per_cu_rope), Q8 ? kSkWavesPerCuQ8 : kSkWavesPerCu);
+  if (per_cu <= 0) return fail(LNSKV_ERR_HIP, "occupancy query of the stream-K decode kernel failed");
+  *waves = cus * std::min(per_cu, Q8 ? kSkWavesPerCuQ8 : kSkWavesPerCu);
   return LNSKV_OK;
 }
 
@@ -1851,15 +1854,16 @@ void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, bool q8, hipStre
 }
 }  // namespace
 
-int mfma_sk_waves(int rep, int d, bool fused, bool q8, int* waves) {
+int mfma_sk_waves(int rep, int d, bool fused, bool q8, bool rope, int* waves) {
   // resident waves used per launch on the current device, kept per
-  // (device, rep, head dim, fused, q8)
+  // (device, rep, head dim, fused, q8, rope)
   static std::mutex mu;
-  static std::map<std::tuple<int, int, int, bool, bool>, int> cache;
+  static std::map<std::tuple<int, int, int, bool, bool, bool>, int> cache;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(LNSKV_ERR_HIP, "hipGetDevice failed");
+  rope = rope && fused;
   std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_tuple(dev, rep, d, fused, q8);
+  const auto key = std::make_tuple(dev, rep, d, fused, q8, rope);
   const auto it = cache.find(key);
   if (it != cache.end()) {
     *waves = it->second;
@@ -1870,8 +1874,12 @@ int mfma_sk_waves(int rep, int d, bool fused, bool q8, int* waves) {
   int rc = LNSKV_OK;
   if (int r = with_rep_nh(rep, d, [&](auto rep_c, auto nh_c) {
         constexpr int R = decltype(rep_c)::value, NH = decltype(nh_c)::value;
-        if (q8) rc = fused ? sk_waves_of<R, true, true, NH>(cus, waves) : sk_waves_of<R, false, true, NH>(cus, waves);
-        else rc = fused ? sk_waves_of<R, true, false, NH>(cus, waves) : sk_waves_of<R, false, false, NH>(cus, waves);
+        auto of = [&](auto q8_c) {
+          constexpr bool Q = decltype(q8_c)::value;
+          if (!fused) return sk_waves_of<R, false, Q, NH, false>(cus, waves);
+          return rope ? sk_waves_of<R, true, Q, NH, true>(cus, waves) : sk_waves_of<R, true, Q, NH, false>(cus, waves);
+        };
+        rc = q8 ? of(std::true_type{}) : of(std::false_type{});
       }))
     return r;
   if (rc == LNSKV_OK) cache[key] = *waves;

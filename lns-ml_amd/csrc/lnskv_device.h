@@ -406,7 +406,8 @@ int launch_decode_mfma_f16(const DecodeArgs& a, int rep, int d, int n_seq, hipSt
 template <bool FUSED>
 int launch_decode_mfma_sk(const DecodeArgs& a, int rep, int d, int n_seq, int n_waves, bool q8, hipStream_t st);
 // Waves of the stream-K kernel resident at once on the current device.
-int mfma_sk_waves(int rep, int d, bool fused, bool q8, int* waves);
+// rope: the fused kernel that turns RoPE in registers.
+int mfma_sk_waves(int rep, int d, bool fused, bool q8, bool rope, int* waves);
 // Workgroup schedule of the MFMA kernels (n_seq <= kSkMaxSeqs): up to n_wg
 // workgroups (mfma_wg_count: two per CU); the workspace holds the header of
 // kWsHeaderBytes (a count per workgroup, zero between calls) and then 2 * rep

@@ -432,6 +432,7 @@ struct DecodePlan {
   int split = 0;      // split-K: tokens per partition
   int max_parts = 1;  // split-K: partitions of the longest sequence
   int sk_waves = 0;   // > 0: stream-K with this many waves
+  int sk_waves_rope = 0;  // stream-K waves of a fused call that turns RoPE in the kernel
   int wg = 0;         // > 0: the workgroup schedule with this many workgroups
   size_t ws_bytes = 0;
 };
@@ -470,15 +471,21 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
     }
     // stream-K; fused < 0: either kind (the workspace query), sized for the
     // larger
-    int w0 = 0, w1 = 0;
+    // the RoPE variants may hold more registers, so fewer of their waves
+    // fit: each launch uses its own kernel's count, the workspace fits all
+    int w0 = 0, w1 = 0, w1r = 0;
     if (fused <= 0)
-      if (int rc = mfma_sk_waves(rep, d, false, q8, &w0)) return rc;
-    if (fused != 0)
-      if (int rc = mfma_sk_waves(rep, d, true, q8, &w1)) return rc;
+      if (int rc = mfma_sk_waves(rep, d, false, q8, false, &w0)) return rc;
+    if (fused != 0) {
+      if (int rc = mfma_sk_waves(rep, d, true, q8, false, &w1)) return rc;
+      if (int rc = mfma_sk_waves(rep, d, true, q8, true, &w1r)) return rc;
+    }
     p->sk_waves = std::max(w0, w1);
+    p->sk_waves_rope = w1r;
+    const int w_most = std::max(p->sk_waves, w1r);
     // the header, then partial rows (acc, then (m, l)) of two pieces per
     // wave, then one 16-byte descriptor per wave
-    p->ws_bytes = kWsHeaderBytes + (size_t)p->sk_waves * (2 * rep * ((size_t)d + 2) * sizeof(float) + 16);
+    p->ws_bytes = kWsHeaderBytes + (size_t)w_most * (2 * rep * ((size_t)d + 2) * sizeof(float) + 16);
     return LNSKV_OK;
   }
   p->split = split_tokens ? split_tokens : choose_split(n_seq, n_kv, max_kv_len);
@@ -593,7 +600,8 @@ int noalloc_scratch(void** out) {
       for (int d : {128, 256})
         for (bool q8 : {false, true}) {
           int waves = 0;
-          if (int rc = mfma_sk_waves(rep, d, true, q8, &waves)) return rc;
+          for (bool rope : {false, true})
+            if (int rc = mfma_sk_waves(rep, d, true, q8, rope, &waves)) return rc;
         }
     int n_wg = 0;
     if (int rc = mfma_wg_count(&n_wg)) return rc;
@@ -726,10 +734,11 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
     return launch_decode_mfma_wg<FUSED>(a, rep, d, n_seq, plan.wg, c->dtype == LNSKV_DTYPE_Q8A, (hipStream_t)stream);
   }
   if (plan.sk_waves > 0) {
+    const int n_waves = rope_half > 0 ? plan.sk_waves_rope : plan.sk_waves;
     a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeaderBytes);
-    a.ws_ml = a.ws_acc + (size_t)plan.sk_waves * 2 * rep * c->head_dim;
-    a.sk_desc = reinterpret_cast<int4*>(a.ws_ml + (size_t)plan.sk_waves * 2 * rep * 2);
-    return launch_decode_mfma_sk<FUSED>(a, rep, d, n_seq, plan.sk_waves, c->dtype == LNSKV_DTYPE_Q8A,
+    a.ws_ml = a.ws_acc + (size_t)n_waves * 2 * rep * c->head_dim;
+    a.sk_desc = reinterpret_cast<int4*>(a.ws_ml + (size_t)n_waves * 2 * rep * 2);
+    return launch_decode_mfma_sk<FUSED>(a, rep, d, n_seq, n_waves, c->dtype == LNSKV_DTYPE_Q8A,
                                         (hipStream_t)stream);
   }
   if (need > 0) {
