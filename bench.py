@@ -270,7 +270,7 @@ def prefill_measure(w, runner, dev, reps: int, chunk: int = 256) -> dict | None:
     import numpy as np
     import torch
 
-    if reps <= 0 or w.dtype != 1 or w.head_dim != 128:
+    if reps <= 0 or w.dtype not in (1, 2) or w.head_dim != 128:
         return None
     cs, cp = w.chunk_tokens()
     desc, tok = [], 0
@@ -315,7 +315,7 @@ def prefill_measure(w, runner, dev, reps: int, chunk: int = 256) -> dict | None:
         return s.elapsed_time(e) / 1e3 / reps
 
     dt = timed(launch)
-    res = {"shape": f"{what}, Hq{w.n_heads}/Hkv{w.n_kv}/d{w.head_dim} f16 pages",
+    res = {"shape": f"{what}, Hq{w.n_heads}/Hkv{w.n_kv}/d{w.head_dim} {('f32', 'f16', 'Q8A')[w.dtype]} pages",
            "us_per_launch": round(dt * 1e6, 1), "gflop": round(flops / 1e9, 2),
            "tflop_per_s": round(flops / dt / 1e12, 1),
            "frac_of_f16_mfma_peak": round(flops / dt / 1e12 / 2500.0, 4),
@@ -382,11 +382,12 @@ def timed_steps(step, stream, steps: int, warmup: int) -> tuple[float, float]:
 
 
 def config_measure(name: str, dev, steps: int, layers: int = 2, kv_dtype: int | None = None,
-                   pattern_reps: int = 0) -> dict:
+                   pattern_reps: int = 0, prefill_reps: int = 0) -> dict:
     """One configuration's step (its own workload and pools, `layers` of them
     cycled): event mean over `steps` steps, median of per-step events,
     algorithmic GB/s and fraction of 8 TB/s; optionally the load ceiling of
-    its page pattern.  c5 adds the full-copy fork variant."""
+    its page pattern and chunked prefill over its pages.  c5 adds the
+    full-copy fork variant."""
     import torch
 
     from lnskv.configs import make
@@ -408,6 +409,8 @@ def config_measure(name: str, dev, steps: int, layers: int = 2, kv_dtype: int | 
         if pc:
             res["pattern_ceiling_us"] = pc["us_per_launch"]
             res["frac_of_pattern_ceiling"] = round(pc["us_per_launch"] / (ev * 1e6), 4)
+    if prefill_reps > 0:
+        res["chunked_prefill_attention"] = prefill_measure(w, runner, dev, prefill_reps)
     if name == "c5" and w.info.get("parents"):
         res["full_copy_fork"] = full_copy_fork(w, runner, dev)
     del runner
@@ -779,7 +782,7 @@ def main():
     extras = None
     if args.extras and w.name == "c2" and args.kv_dtype == "config" and not args.rope:
         extras = {"c2_q8a_pages": config_measure("c2", dev, args.steps, layers=args.layers, kv_dtype=2,
-                                                 pattern_reps=args.pattern_reps),
+                                                 pattern_reps=args.pattern_reps, prefill_reps=args.prefill_reps),
                   "reference_call_b1_q8a": reference_call_measure(dev),
                   "qwen35_shape": qwen35_measure(dev, min(args.steps, 100), pattern_reps=args.pattern_reps),
                   "block_table_upload": table_upload_measure(w, dev)}

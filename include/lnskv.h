@@ -262,8 +262,10 @@ int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const
  *   row (NULL = 0).  window > 0 (a sliding-window layer): query row t attends
  *   [max(p_start, pos(t) - window + 1), pos(t)], each prompt token its own
  *   kv_p_start as the reference's per-token loop gives it (engine.rs:
- *   3007-3013); window = 0: [p_start, pos(t)].  f16 pages with head_dim 128
- *   only (LNSKV_ERR_UNSUPPORTED otherwise).
+ *   3007-3013); window = 0: [p_start, pos(t)].  f16 or Q8A pages with
+ *   head_dim 128 (LNSKV_ERR_UNSUPPORTED otherwise); Q8A codes are turned to
+ *   f16 in LDS (code x 1, the row scale applied to the scores and to the
+ *   probabilities), so the result is the dequantised pages' attention.
  * ------------------------------------------------------------------------- */
 int lnskv_prefill_attention(const lnskv_pages* c, const float* q_dev, float* out_dev,
                             const int32_t* chunks_dev, int32_t n_chunks, int32_t n_tok,

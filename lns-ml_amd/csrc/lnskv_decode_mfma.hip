@@ -2073,18 +2073,93 @@ __device__ __forceinline__ void pf_issue(const PrefillArgs& a, const PfLanes& pl
   }
 }
 
+// Q8A pages.  A pair's int8 codes (four 2 KiB regions: K of page 0, K of
+// page 1, V of page 0, V of page 1, 16 rows of 128 codes each) come by DMA,
+// wave w taking half w & 1 (rows 8 (w & 1) ..) of region w >> 1, so lane l
+// of wave w fetches row 8 (w & 1) + l / 8, codes 16 (l % 8) .. + 15 -- the
+// same 16 bytes it converts to f16 afterwards; each wave also DMAs its own
+// copy of the pair's 32 K and 32 V scales (lane l: page (l / 16) & 1, token
+// l % 16).  Three vector-memory instructions per wave and pair.
+constexpr int kPfCodeSlot = 4 * 2048;                     // the codes of a pair
+constexpr int kPfScaleWave = 512;                         // K scales [0, 256), V scales [256, 512)
+constexpr int kPfQ8Slot = kPfCodeSlot + 8 * kPfScaleWave;  // codes, then eight waves' scale copies
+constexpr int kPfQ8Rpw = 3;
+
+__device__ __forceinline__ void pf_issue_q8(const PrefillArgs& a, uint32_t rs, uint32_t kvh, lds_u8* slot,
+                                            uint32_t ph0, uint32_t ph1, int w) {
+  typedef __attribute__((address_space(3))) void lds_void;
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  const uint32_t page_bytes = kPage * rs;
+  const int r = w >> 1;  // wave-uniform
+  const uint32_t ph = (r & 1) ? ph1 : ph0;
+  const size_t base = (size_t)(ph < a.num_pages ? ph : 0u) * page_bytes + (size_t)kvh * kD;
+  const uint8_t* src = (r >> 1) ? a.v_pages : a.k_pages;
+  const __amdgpu_buffer_rsrc_t rsc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(src + base), (short)0, (int)page_bytes, kBufferFormat);
+  const uint32_t row = 8u * (uint32_t)(w & 1) + (uint32_t)(lane >> 3);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (lds_void*)(slot + r * 2048 + (w & 1) * 1024), 16,
+                                           (int)(row * rs + 16u * (uint32_t)(lane & 7)), 0, 0, 0);
+  // scales: token lane % 16 of page (lane / 16) & 1 (a missing page: page 0)
+  const uint32_t sp = ((lane >> 4) & 1) ? ph1 : ph0;
+  const uint32_t sidx = ((sp < a.num_pages ? sp : 0u) * kPage + (uint32_t)(lane & 15)) * (uint32_t)a.n_kv + kvh;
+  const int sbytes = (int)min((size_t)a.num_pages * kPage * (size_t)a.n_kv * 4, (size_t)0x7FFFFFF0);
+  const __amdgpu_buffer_rsrc_t ksr = __builtin_amdgcn_make_buffer_rsrc((void*)a.k_scales, (short)0, sbytes, kBufferFormat);
+  const __amdgpu_buffer_rsrc_t vsr = __builtin_amdgcn_make_buffer_rsrc((void*)a.v_scales, (short)0, sbytes, kBufferFormat);
+  lds_u8* sc = slot + kPfCodeSlot + w * kPfScaleWave;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(ksr, (lds_void*)sc, 4, (int)(4u * sidx), 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(vsr, (lds_void*)(sc + 256), 4, (int)(4u * sidx), 0, 0, 0);
+}
+
+// This wave's 16 codes of the pair (the ones it DMA'd) to f16 in the f16 pair
+// slot `dst` (the layout pf_consume reads): K token t's chunk c at c ^ t of
+// row t, V token t in row R = 4 (t % 4) + t / 4 with chunk c at c ^ sw(R).
+// The codes are exact in f16.
+__device__ __forceinline__ void pf_convert_q8(const lds_u8* codes, lds_u8* dst, int w) {
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  const int r = w >> 1;
+  const int t = 8 * (w & 1) + (lane >> 3), c16 = lane & 7;
+  u32x4 x;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+               : "=v"(x)
+               : "v"((uint32_t)(size_t)(codes + r * 2048 + (w & 1) * 1024 + 16 * lane))
+               : "memory");
+  const half8 lo = i8x8_to_f16(uint2v{x[0], x[1]}), hi = i8x8_to_f16(uint2v{x[2], x[3]});
+  const int p = r & 1;
+  uint32_t o0, o1;
+  if (r < 2) {  // K
+    o0 = (uint32_t)(p * kVSlot + t * kRowBytes) + 16u * ((uint32_t)(2 * c16) ^ (uint32_t)t);
+    o1 = (uint32_t)(p * kVSlot + t * kRowBytes) + 16u * ((uint32_t)(2 * c16 + 1) ^ (uint32_t)t);
+  } else {  // V
+    const int R = 4 * (t & 3) + (t >> 2);
+    o0 = (uint32_t)((2 + p) * kVSlot + R * kRowBytes) + 16u * ((uint32_t)(2 * c16) ^ v_swz(R));
+    o1 = (uint32_t)((2 + p) * kVSlot + R * kRowBytes) + 16u * ((uint32_t)(2 * c16 + 1) ^ v_swz(R));
+  }
+  // inline asm stores: the compiler would otherwise wait for every DMA in
+  // flight before a plain LDS store (it cannot tell which slot a DMA writes)
+  const uint32_t d = (uint32_t)(size_t)dst;
+  asm volatile("ds_write_b128 %0, %1" : : "v"(d + o0), "v"(lo) : "memory");
+  asm volatile("ds_write_b128 %0, %1" : : "v"(d + o1), "v"(hi) : "memory");
+}
+
 // MODE 0: every token of the pair is attended by every query of the wave;
 // 1: per-query masks only (causal, and the query's own sliding window
 // [qlo, qpos]); 2: some tokens are outside the tile's window or on a missing
 // page: mask them and zero their V rows (stale LDS or page bytes may hold NaN
 // patterns, and 0 * NaN would reach the accumulators).
-template <int HW, int MODE>
+// Q8 (Q8A pages): `slot` holds the pair's codes as f16 and `scales` this
+// wave's copy of their K and V scales.  The K scale of each token multiplies
+// its scores; the V scale multiplies its weights before P.V, over vnorm, a
+// power of two at or just above the largest V scale seen (kept within 16x of
+// each pair's largest; acc is rescaled exactly when it moves), so that the
+// f16 lo parts of the weights stay normal numbers; l sums the unscaled
+// weights and the output is acc * vnorm / l.
+template <int HW, int MODE, bool Q8 = false>
 __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW], float (&l)[HW],
                                            const half8 (&qh)[HW][4], const half8 (&ql)[HW][4],
                                            const float (&qexp)[HW], const PfLanes& pl, lds_u8* slot, int tok0,
                                            bool v0, bool v1, int ta, int tb, int qpos, int qlo, bool qok, int g,
-                                           int n) {
-  if constexpr (MODE == 2) {
+                                           int n, const lds_u8* scales = nullptr, float* vnorm = nullptr) {
+  if constexpr (MODE == 2 && !Q8) {
 #pragma unroll
     for (int p = 0; p < 2; ++p)
 #pragma unroll
@@ -2146,12 +2221,46 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
                  "+v"(bv[1][4]), "+v"(bv[1][5]), "+v"(bv[1][6]), "+v"(bv[1][7])
                :
                : "memory");
+  // Q8: the scales of the lane's tokens 16 p + 4g + ii (e = 4p + ii)
+  float ks[8], vsc[8], vinv = 1.0f;
+  if constexpr (Q8) {
+    float4v k0, k1, w0, w1;
+    const uint32_t sa = (uint32_t)(size_t)scales + 16u * (uint32_t)g;
+    asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:64\n\t"
+                 "ds_read_b128 %2, %4 offset:256\n\tds_read_b128 %3, %4 offset:320\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(k0), "=&v"(k1), "=&v"(w0), "=&v"(w1)  // early clobber: the address stays live
+                 : "v"(sa)
+                 : "memory");
+    float vmax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ks[e] = e < 4 ? k0[e] : k1[e - 4];
+      vsc[e] = e < 4 ? w0[e] : w1[e - 4];
+      const int t = tok0 + 16 * (e >> 2) + 4 * g + (e & 3);
+      if (MODE == 2 && !(((e >> 2) ? v1 : v0) && t >= ta && t < tb)) vsc[e] = 0.0f;  // stale bytes
+      vmax = fmaxf(vmax, vsc[e]);
+    }
+    vmax = max_xor16(max_xor32(vmax));  // over the pair's 32 tokens; wave-uniform
+    if ((vmax > *vnorm || vmax * 16.0f < *vnorm) && vmax > 0.0f) {
+      int ex = 0;
+      (void)frexpf(vmax, &ex);
+      if (*vnorm > 0.0f) {
+        const float rr = *vnorm * ldexpf(1.0f, -ex);  // a power of two: exact
+#pragma unroll
+        for (int hh = 0; hh < HW; ++hh)
+#pragma unroll
+          for (int nb = 0; nb < 8; ++nb) acc[hh][nb] *= rr;
+      }
+      *vnorm = ldexpf(1.0f, ex);
+    }
+    vinv = *vnorm > 0.0f ? 1.0f / *vnorm : 0.0f;
+  }
 #pragma unroll
   for (int hh = 0; hh < HW; ++hh) {
     // raw scores (still scaled by 2^-E); masked tokens -inf
     float s[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s[e] = sacc[hh][e >> 2][e & 3];
+    for (int e = 0; e < 8; ++e) s[e] = Q8 ? sacc[hh][e >> 2][e & 3] * ks[e] : sacc[hh][e >> 2][e & 3];
     if constexpr (MODE != 0) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -2182,8 +2291,9 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
     float lsum = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
-      const float2v pp = {fast_exp2(fmaf(s[e], qexp[hh], nm)), fast_exp2(fmaf(s[e + 1], qexp[hh], nm))};
+      float2v pp = {fast_exp2(fmaf(s[e], qexp[hh], nm)), fast_exp2(fmaf(s[e + 1], qexp[hh], nm))};
       lsum += pp[0] + pp[1];
+      if constexpr (Q8) pp = float2v{pp[0] * (vsc[e] * vinv), pp[1] * (vsc[e + 1] * vinv)};
       const half2v h = __builtin_convertvector(pp, half2v);
       const float2v hf = __builtin_convertvector(h, float2v);
       const half2v lo = __builtin_convertvector(float2v{pp[0] - hf[0], pp[1] - hf[1]}, half2v);
@@ -2211,10 +2321,16 @@ __device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int i) {
   return ok ? (ch.z + QT - 1) / QT : 0;
 }
 
-template <int REP>
+// Q8: Q8A pages (int8 codes and scales, pf_issue_q8): every wave converts the
+// codes it fetched into a double-buffered f16 pair slot before the batch's
+// barrier, so a batch still costs one barrier.
+template <int REP, bool Q8 = false>
 __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(PrefillArgs a) {
-  constexpr int HW = PfShape<REP>::HW, WPQ = PfShape<REP>::WPQ, QT = PfShape<REP>::QT, RPW = PfShape<REP>::RPW;
-  __shared__ __attribute__((aligned(16))) uint8_t ring_[kPfDepth * kPfSlot];
+  constexpr int HW = PfShape<REP>::HW, WPQ = PfShape<REP>::WPQ, QT = PfShape<REP>::QT;
+  constexpr int RPW = Q8 ? kPfQ8Rpw : PfShape<REP>::RPW;  // vector-memory instructions per wave and pair
+  constexpr int kRingSlot = Q8 ? kPfQ8Slot : kPfSlot;
+  __shared__ __attribute__((aligned(16))) uint8_t ring_[kPfDepth * kRingSlot];
+  __shared__ __attribute__((aligned(16))) uint8_t f16buf_[Q8 ? 2 * kPfBatch * kPfSlot : 16];
   const int lane = (int)(threadIdx.x & (kWave - 1)), w = (int)(threadIdx.x / kWave);
   const int g = lane >> 4, n = lane & 15;
 
@@ -2347,7 +2463,10 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     const uint32_t ph1 = 2 * i + 1 < npg ? phys_of(2 * i + 1) : 0xFFFFFFFFu;
     const uint32_t bits = (ph0 < a.num_pages ? 1u : 0u) | (ph1 < a.num_pages ? 2u : 0u);
     vbits = (vbits & ~(3u << (2 * sl))) | (bits << (2 * sl));
-    pf_issue<RPW>(a, pl, page_bytes, kvh_off, ring + sl * kPfSlot, ph0, ph1, w);
+    if constexpr (Q8)
+      pf_issue_q8(a, (uint32_t)a.n_kv * kD, (uint32_t)kvh, ring + sl * kRingSlot, ph0, ph1, w);
+    else
+      pf_issue<PfShape<REP>::RPW>(a, pl, page_bytes, kvh_off, ring + sl * kPfSlot, ph0, ph1, w);
   };
 #pragma unroll
   for (int i = 0; i < 2 * kPfBatch; ++i)
@@ -2381,6 +2500,7 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
   }
   float4v acc[HW][8];
   float m[HW], l[HW];
+  float vnorm = 0.0f;  // Q8: acc is in units of vnorm
 #pragma unroll
   for (int hh = 0; hh < HW; ++hh) {
     m[hh] = kMInit;
@@ -2404,6 +2524,15 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
       wait_vmcnt<RPW>();
     else if (later == 0)
       wait_vmcnt<0>();
+    // Q8: this wave's codes of the batch (its own DMAs, just waited for) to
+    // f16 in the batch's buffer; the buffer was last read by the batch before
+    // the previous one, which every wave finished before the last barrier
+    lds_u8* f16b = (lds_u8*)f16buf_ + ((i0 / kPfBatch) & 1) * (kPfBatch * kPfSlot);
+    if constexpr (Q8) {
+#pragma unroll
+      for (int k = 0; k < kPfBatch; ++k)
+        if (i0 + k < npairs) pf_convert_q8(ring + ((i0 + k) % kPfDepth) * kRingSlot, f16b + k * kPfSlot, w);
+    }
     pf_barrier();  // every wave's quarters of this batch landed; the previous batch is consumed
 #pragma unroll
     for (int k = 0; k < kPfBatch; ++k)
@@ -2411,16 +2540,17 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     for (int i = i0; i < min(i0 + kPfBatch, npairs); ++i) {
     if (active) {
       const int sl = i % kPfDepth;
-      lds_u8* sp = ring + sl * kPfSlot;
+      lds_u8* sp = Q8 ? f16b + (i - i0) * kPfSlot : ring + sl * kPfSlot;
+      const lds_u8* sc = ring + sl * kRingSlot + kPfCodeSlot + w * kPfScaleWave;  // Q8: this wave's scales
       const bool v0 = (vbits >> (2 * sl)) & 1u, v1 = (vbits >> (2 * sl + 1)) & 1u;
       const int tok0 = (pg_first + 2 * i) * kPage;
       const bool whole = v0 && v1 && tok0 >= ta && tok0 + 2 * kPage <= tb;
       if (whole && tok0 + 2 * kPage - 1 <= wq && tok0 >= wlo)
-        pf_consume<HW, 0>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n);
+        pf_consume<HW, 0, Q8>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n, sc, &vnorm);
       else if (whole)
-        pf_consume<HW, 1>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n);
+        pf_consume<HW, 1, Q8>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n, sc, &vnorm);
       else
-        pf_consume<HW, 2>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n);
+        pf_consume<HW, 2, Q8>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n, sc, &vnorm);
     }
     }
   }
@@ -2435,7 +2565,7 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
       const float L = __shfl(lt, 20 * g + ii, kWave);  // query 4g + ii
       const int qq = 4 * g + ii;
       if (qq < qn_w) {
-        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        const float inv = L > 0.0f ? (Q8 ? vnorm : 1.0f) / L : 0.0f;
         float* orow = a.out + ((size_t)(tq + qq) * a.n_heads + h0 + hh) * kD;
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) orow[16 * nb + n] = acc[hh][nb][ii] * inv;
@@ -2447,7 +2577,10 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
 template <int REP>
 void launch_prefill_rep(const PrefillArgs& a, int n_tiles, hipStream_t st) {
   const unsigned blocks = (unsigned)n_tiles * (unsigned)a.n_kv;
-  prefill_mfma_kernel<REP><<<blocks, kWave * PfShape<REP>::NW, 0, st>>>(a);
+  if (a.k_scales)
+    prefill_mfma_kernel<REP, true><<<blocks, kWave * PfShape<REP>::NW, 0, st>>>(a);
+  else
+    prefill_mfma_kernel<REP, false><<<blocks, kWave * PfShape<REP>::NW, 0, st>>>(a);
 }
 }  // namespace
 

@@ -420,6 +420,8 @@ int mfma_wg_count(int* n_wg);
 struct PrefillArgs {
   const uint8_t* k_pages;
   const uint8_t* v_pages;
+  const float* k_scales;   // Q8A pages: per (slot, kv head) scales; nullptr for f16
+  const float* v_scales;
   const float* q;          // [n_tok][n_heads][128]
   float* out;              // [n_tok][n_heads][128]
   const int4* chunks;      // [n_chunks]: {table row, first position, length, first token}

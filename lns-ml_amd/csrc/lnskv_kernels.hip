@@ -1049,12 +1049,14 @@ int lnskv_prefill_attention(const lnskv_pages* c, const float* q, float* out, co
     return fail(LNSKV_ERR_INVALID, "n_heads %d is not a multiple of n_kv_heads %u", n_heads, c->n_kv_heads);
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(LNSKV_ERR_INVALID, "scale must be positive and finite");
   if (window < 0) return fail(LNSKV_ERR_INVALID, "window %d is negative", window);
-  if (c->dtype != LNSKV_DTYPE_F16 || c->head_dim != 128)
-    return fail(LNSKV_ERR_UNSUPPORTED, "prefill attention is built for f16 pages with head_dim 128");
+  if ((c->dtype != LNSKV_DTYPE_F16 && c->dtype != LNSKV_DTYPE_Q8A) || c->head_dim != 128)
+    return fail(LNSKV_ERR_UNSUPPORTED, "prefill attention is built for f16 and Q8A pages with head_dim 128");
   if (!aligned16(chunks) || !aligned16(q)) return fail(LNSKV_ERR_INVALID, "chunks and q must be 16-byte aligned");
   PrefillArgs a{};
   a.k_pages = static_cast<const uint8_t*>(c->k_pages);
   a.v_pages = static_cast<const uint8_t*>(c->v_pages);
+  a.k_scales = c->dtype == LNSKV_DTYPE_Q8A ? c->k_scales : nullptr;
+  a.v_scales = c->dtype == LNSKV_DTYPE_Q8A ? c->v_scales : nullptr;
   a.q = q;
   a.out = out;
   a.chunks = reinterpret_cast<const int4*>(chunks);

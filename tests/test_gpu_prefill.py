@@ -1,8 +1,8 @@
 """GPU chunked-prefill attention (lnskv_prefill_attention) against the
 float64 oracle run token by token: query t of a chunk must equal the decode
 of that token alone with kv_len = pos(t) + 1 (what the reference's
-token-at-a-time forward computes), within the f16 tolerance (1e-3 relative
-per row).  Covers head ratios 1/2/4/8, a chunk with no earlier context, a
+token-at-a-time forward computes), within the page type's tolerance (1e-3
+relative per row for f16 pages, 1e-5 for Q8A pages).  f16 and Q8A pages.  Covers head ratios 1/2/4/8, a chunk with no earlier context, a
 single-token chunk, ragged tile ends, a sliding window, a missing page, a
 chunk naming a table row outside the tables (skipped: its rows untouched),
 chunks out of sequence order, and two 128-token chunks over ~1500-token
@@ -13,20 +13,21 @@ import torch
 
 import oracle as O
 from gpu_util import TOL, dev_f32, dev_i32, fill_pages, host_pages, rel_err, say
-from lnskv import DTYPE_F16, NO_PAGE
+from lnskv import DTYPE_F16, DTYPE_NAMES, DTYPE_Q8A, NO_PAGE
 from lnskv.device import PagedKV, sync
 
 pytestmark = pytest.mark.gpu
 
 
-def _run(gpu, rep, chunks, ctx_pages, p_start=None, missing=(), n_kv=2, seed=0, extra_rows=0, window=0):
+def _run(gpu, rep, chunks, ctx_pages, p_start=None, missing=(), n_kv=2, seed=0, extra_rows=0, window=0,
+         dtype=DTYPE_F16):
     """chunks: list of (table row, first position, length); tokens laid out in list order.
     window > 0: every token's reference start is max(p_start, kv_p_start(pos, window))."""
     d = 128
     rng = np.random.default_rng(seed)
     n_rows = len(ctx_pages)
     num_pages = sum(ctx_pages) + 8
-    pk = PagedKV(num_pages, n_kv, d, DTYPE_F16, gpu)
+    pk = PagedKV(num_pages, n_kv, d, dtype, gpu)
     fill_pages(pk, seed=seed + 1)
     perm = rng.permutation(num_pages).astype(np.uint32)
     stride = max(ctx_pages) + 1
@@ -69,29 +70,36 @@ def _run(gpu, rep, chunks, ctx_pages, p_start=None, missing=(), n_kv=2, seed=0, 
                        scale)
     got = out.cpu().numpy()
     err = rel_err(got[idx], ref)
-    say("prefill rep", rep, "tokens", len(idx), "max rel err", float(err.max()))
-    assert err.max() < TOL[DTYPE_F16]
+    say("prefill", DTYPE_NAMES[dtype], "rep", rep, "tokens", len(idx), "max rel err", float(err.max()))
+    assert err.max() < TOL[dtype]
     untouched = np.setdiff1d(np.arange(n_tok), idx)
     assert np.all(got[untouched] == 7.0)
 
 
+DTYPES = [DTYPE_F16, DTYPE_Q8A]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rep", [1, 2, 4, 8])
-def test_prefill_small_cases(gpu, rep):
+def test_prefill_small_cases(gpu, rep, dtype):
     chunks = [(1, 1000, 16),   # a whole tile at a long context, with a missing page in its window
               (0, 0, 37),      # no earlier context; 3 tiles, the last ragged
               (2, 15, 1),      # a single token at the end of page 0
               (3, 300, 100),   # windowed: attends [200, pos]
               (9, 5, 4)]       # table row outside the tables: skipped
     ctx_pages = [3, 64, 1, 26]
-    _run(gpu, rep, chunks, ctx_pages, p_start=[0, 0, 0, 200], missing=[(1, 20)], seed=rep, extra_rows=4)
+    _run(gpu, rep, chunks, ctx_pages, p_start=[0, 0, 0, 200], missing=[(1, 20)], seed=rep, extra_rows=4,
+         dtype=dtype)
 
 
-def test_prefill_long_chunks(gpu):
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_prefill_long_chunks(gpu, dtype):
     chunks = [(0, 1400, 128), (1, 1600, 128)]
-    _run(gpu, 4, chunks, [(1400 + 128 + 15) // 16, (1600 + 128 + 15) // 16], n_kv=8, seed=11)
+    _run(gpu, 4, chunks, [(1400 + 128 + 15) // 16, (1600 + 128 + 15) // 16], n_kv=8, seed=11, dtype=dtype)
 
 
-def test_prefill_many_chunks(gpu):
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_prefill_many_chunks(gpu, dtype):
     """70 chunks (past one 64-chunk scan group), lengths 1..40, some sharing a
     table row at different offsets, one outside the tables (skipped)."""
     rng = np.random.default_rng(5)
@@ -106,11 +114,12 @@ def test_prefill_many_chunks(gpu):
         chunks.append((row, pos0, ln))
     chunks[33] = (n_rows + 3, 0, 8)
     for rep in (4, 8):
-        _run(gpu, rep, chunks, ctx_pages, seed=20 + rep)
+        _run(gpu, rep, chunks, ctx_pages, seed=20 + rep, dtype=dtype)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rep", [2, 4, 8])
-def test_prefill_sliding_window(gpu, rep):
+def test_prefill_sliding_window(gpu, rep, dtype):
     """A sliding-window layer: each prompt token attends its own window
     [pos - w + 1, pos] (the reference's per-token kv_p_start), checked token by
     token against the oracle.  Chunks that cross the window (longer than it,
@@ -123,4 +132,4 @@ def test_prefill_sliding_window(gpu, rep):
     ctx_pages = [13, 53, 7, 35]
     for w in (100, 1, 16, 33):
         _run(gpu, rep, chunks, ctx_pages, p_start=[0, 0, 0, 520], missing=[(1, 44)], seed=30 + rep + w,
-             window=w)
+             window=w, dtype=dtype)
