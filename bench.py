@@ -19,7 +19,9 @@ softmax per query head, OpenMP over sequence x kv head) on this host.
 `roofline.traffic` is the HBM bytes per step that rocprofv3's FETCH_SIZE and
 WRITE_SIZE counters gave for the same workload, scaled by what they read for
 a plain copy of known size; it is read from profiles/<config>_traffic.json
-(written from those counter runs) and is null when that file is absent.
+(profiles/<config>_q8a_traffic.json for Q8A pages; written from those counter
+runs, with the commit whose build they measured) and is null when that file is
+absent.
 """
 from __future__ import annotations
 
@@ -409,6 +411,11 @@ def config_measure(name: str, dev, steps: int, layers: int = 2, kv_dtype: int | 
         if pc:
             res["pattern_ceiling_us"] = pc["us_per_launch"]
             res["frac_of_pattern_ceiling"] = round(pc["us_per_launch"] / (ev * 1e6), 4)
+    traffic = measured_traffic(name, w.dtype)
+    if traffic:
+        res["traffic_bytes"] = traffic["bytes"]
+        res["traffic_over_algorithmic"] = traffic["over_algorithmic"]
+        res["traffic_measured_at_commit"] = traffic["measured_at_commit"]
     if prefill_reps > 0:
         res["chunked_prefill_attention"] = prefill_measure(w, runner, dev, prefill_reps)
     if name == "c5" and w.info.get("parents"):
@@ -646,14 +653,21 @@ def table_upload_measure(w, dev, reps: int = 200) -> dict:
             "note": "hipMemcpyAsync from pageable host memory; the step's kernels are not in the timed region"}
 
 
-def measured_traffic(name: str):
-    """HBM bytes per step from the committed counter summary, or None."""
-    path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+def measured_traffic(name: str, dtype: int, rope: bool = False) -> dict | None:
+    """HBM bytes per step from the committed counter summary of this workload
+    and page type (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), with
+    the commit whose build it measured; None when there is none."""
+    if rope:
+        return None
+    path = os.path.join(ROOT, "profiles", f"{name}_{'q8a_' if dtype == 2 else ''}traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         t = json.load(f)
-    return int(t["hbm_bytes_per_step"])
+    if t.get("kv_dtype", "f16") != {0: "f32", 1: "f16", 2: "q8a"}[dtype]:
+        return None
+    return {"bytes": int(t["hbm_bytes_per_step"]), "over_algorithmic": t.get("traffic_over_algorithmic"),
+            "measured_at_commit": t.get("measured_at_commit")}
 
 
 def cpu_baseline(w, runner, seconds: float, threads: int):
@@ -795,6 +809,7 @@ def main():
         threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
         cpu = cpu_baseline(w, runner, args.cpu_seconds, threads)
 
+    traffic = measured_traffic(w.name, w.dtype, bool(args.rope))
     line = {
         "metric": METRIC,
         "value": round(gbs_wall, 1),
@@ -837,7 +852,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs_ev / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(w.name),
+            "traffic": (traffic or {}).get("bytes"),
+            "traffic_over_algorithmic": (traffic or {}).get("over_algorithmic"),
+            "traffic_measured_at_commit": (traffic or {}).get("measured_at_commit"),
             "kernel": ("one step's kernels on their stream (c2: decode_sk_kernel + combine_sk_kernel "
                        "of one lnskv_append_decode call), mean HIP-event duration per step"),
             "copy_ceiling_gbs": copy["gb_per_s"] if copy else None,
