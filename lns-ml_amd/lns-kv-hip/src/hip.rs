@@ -19,6 +19,8 @@ extern "C" {
     pub fn hipMalloc(ptr: *mut *mut c_void, size: usize) -> HipError;
     pub fn hipFree(ptr: *mut c_void) -> HipError;
     pub fn hipMemcpy(dst: *mut c_void, src: *const c_void, size: usize, kind: c_int) -> HipError;
+    pub fn hipMemcpyAsync(dst: *mut c_void, src: *const c_void, size: usize, kind: c_int, stream: HipStream)
+        -> HipError;
     pub fn hipMemset(dst: *mut c_void, value: c_int, size: usize) -> HipError;
     pub fn hipStreamSynchronize(stream: HipStream) -> HipError;
     pub fn hipGetErrorString(err: HipError) -> *const c_char;
@@ -70,6 +72,30 @@ impl<T: Copy> DeviceBuffer<T> {
     /// Host-to-device copy of `host` into the first `host.len()` elements;
     /// returns when the data is on the device (the reference writes its
     /// shared buffers from the host before committing, `engine.rs:3218-3220`).
+    /// `host` into the buffer's first elements, ordered on `stream` after the
+    /// work already queued there.  The runtime stages pageable host memory
+    /// before the call returns, so `host` may change as soon as it does.
+    pub fn copy_from_async(&mut self, host: &[T], stream: HipStream) -> Result<(), String> {
+        if host.len() > self.len {
+            return Err(format!("{} elements into a buffer of {}", host.len(), self.len));
+        }
+        if host.is_empty() {
+            return Ok(());
+        }
+        hip(
+            unsafe {
+                hipMemcpyAsync(
+                    self.ptr as *mut c_void,
+                    host.as_ptr() as *const c_void,
+                    host.len() * size_of::<T>(),
+                    HIP_MEMCPY_HOST_TO_DEVICE,
+                    stream,
+                )
+            },
+            "hipMemcpyAsync host to device",
+        )
+    }
+
     pub fn copy_from(&mut self, host: &[T]) -> Result<(), String> {
         if host.len() > self.len {
             return Err(format!("{} elements into a buffer of {}", host.len(), self.len));

@@ -340,17 +340,20 @@ impl KvPaging {
     }
 
     /// The step before the attention at `pos` (`engine.rs:3218-3233`): evict
-    /// what left the window, map the page of `pos`, upload the table.
-    pub fn step(&mut self, pos: usize, window: usize) -> Result<(), String> {
+    /// what left the window, map the page of `pos`, upload the table on the
+    /// stream the attention is then enqueued on.
+    pub fn step(&mut self, pos: usize, window: usize, stream: HipStream) -> Result<(), String> {
         self.table.step_pages(&mut self.pool, self.layer, pos, window)?;
-        self.upload()
+        self.upload(stream)
     }
 
     /// `upload_block_table` (`engine.rs:2992-3005`): the table's entries into
-    /// the device table (a host-to-device copy that completes before return).
-    pub fn upload(&mut self) -> Result<(), String> {
+    /// the device table, ordered on `stream` after the work already queued
+    /// there (a previous step's attention still reading the table finishes
+    /// first); the host rows are staged before the call returns.
+    pub fn upload(&mut self, stream: HipStream) -> Result<(), String> {
         let n = self.table.as_slice().len();
-        self.table_dev.copy_from(&self.table.as_slice()[..n])
+        self.table_dev.copy_from_async(&self.table.as_slice()[..n], stream)
     }
 
     /// The device table `attention_paged` reads.

@@ -59,7 +59,7 @@ fn attention_paged_matches_host_restatement_on_q8a_pages() {
         q_dev.copy_from(&q).unwrap();
         k_dev.copy_from(&k).unwrap();
         v_dev.copy_from(&v).unwrap();
-        paging.step(pos, window).unwrap();
+        paging.step(pos, window, ptr::null_mut()).unwrap();
         let p_start = kv_p_start(pos, window);
         layer
             .dispatch_attention_paged(
