@@ -443,12 +443,24 @@ __device__ __forceinline__ void piece_loads(const DecodeArgs& a, int s, int kvh,
 // rotation needs them so that no table values are held in registers while
 // the pages are in flight.
 constexpr int kRopeTableBytes = 3 * 64 * 4;
+// The wave's copy of the inverse frequencies in LDS, in two steps: the load
+// issued at the kernel's start, the LDS store once the layout's own loads are
+// in (storing at once would wait for this load before they are issued).
 template <bool ROPE>
-__device__ __forceinline__ void stage_rope_table(const DecodeArgs& a, lds_u8* table) {
+__device__ __forceinline__ float rope_inv_load(const DecodeArgs& a) {
   if constexpr (ROPE) {
     const int lane = (int)(threadIdx.x & (kWave - 1));
-    ((__attribute__((address_space(3))) float*)table)[lane] = lane < a.rope_half ? a.rope_inv[lane] : 0.0f;
+    return lane < a.rope_half ? a.rope_inv[lane] : 0.0f;
   }
+  return 0.0f;
+}
+template <bool ROPE>
+__device__ __forceinline__ void rope_inv_store(lds_u8* table, float v) {
+  if constexpr (ROPE) ((__attribute__((address_space(3))) float*)table)[threadIdx.x & (kWave - 1)] = v;
+}
+template <bool ROPE>
+__device__ __forceinline__ void stage_rope_table(const DecodeArgs& a, lds_u8* table) {
+  rope_inv_store<ROPE>(table, rope_inv_load<ROPE>(a));
 }
 
 // The sines and cosines of one position: lane i < half evaluates angle i
@@ -934,31 +946,43 @@ struct PageQ8 {
 // rotary width 2H (H = 32: dims 0..63, H = 64: dims 0..127), dim i < H pairs
 // with i + H, which lives in lane g ^ (H/32) at the same element; dim i turns
 // with frequency i % H, whose (sin, cos) the table holds.
-__device__ __forceinline__ void rope_q8_lanes(float4v (&qv)[8], int half, const lds_u8* rope_table, int g) {
+template <int H>
+__device__ __forceinline__ void rope_q8_lanes(float4v (&qv)[8], const lds_u8* rope_table, int g) {
+  static_assert(H == 32 || H == 64, "rotary half-width");
   const int lane = (int)(threadIdx.x & (kWave - 1));
-  const bool h64 = half == 64;
+  constexpr bool h64 = H == 64;
   const bool rotated = h64 || g < 2;
   const bool first = h64 ? g < 2 : g == 0;
   const int fb = h64 ? 32 * (g & 1) : 0;  // frequency of this lane's element 0
+  // one pair of elements at a time, the next pair's (sin, cos) read while
+  // this pair turns: unbounded, the scheduler would hoist every table read
+  // and lane swap of the 32 elements at once
+  float4v sc_next = rope_pairs(rope_table, fb);
 #pragma unroll
   for (int e = 0; e < 32; e += 2) {
-    const float4v sc = rope_pairs(rope_table, fb + e);
+    __builtin_amdgcn_sched_barrier(0);
+    const float4v sc = sc_next;
+    if (e + 2 < 32) sc_next = rope_pairs(rope_table, fb + e + 2);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const float x = qv[(e + u) >> 2][(e + u) & 3];
-      const auto r16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
+      // the value of lane ^ H/2 (the swap returns the pair in lane order)
+      float p;
+      if constexpr (h64) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
                                                         false, false);
-      const auto r32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
+        p = __builtin_bit_cast(float, (int)((lane & 32) ? r[0] : r[1]));
+      } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
                                                         false, false);
-      // the value of lane ^ 16 / lane ^ 32 (the swaps return the pair in lane order)
-      const float p16 = __builtin_bit_cast(float, (int)((lane & 16) ? r16[0] : r16[1]));
-      const float p32 = __builtin_bit_cast(float, (int)((lane & 32) ? r32[0] : r32[1]));
-      const float p = h64 ? p32 : p16;
+        p = __builtin_bit_cast(float, (int)((lane & 16) ? r[0] : r[1]));
+      }
       float y0, y1;
       rope_turn(first ? x : p, first ? p : x, sc[2 * u], sc[2 * u + 1], &y0, &y1);
       qv[(e + u) >> 2][(e + u) & 3] = rotated ? (first ? y0 : y1) : x;
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // FUSED: when `append`, this piece holds position pos = L-1; the wave
@@ -1084,7 +1108,10 @@ __device__ __forceinline__ void run_piece_q8(const DecodeArgs& a, lds_u8* vslot,
     float4v q0[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) q0[j] = pl.qv[j];
-    rope_q8_lanes(q0, a.rope_half, rope_table, g);
+    if (a.rope_half == 64)
+      rope_q8_lanes<64>(q0, rope_table, g);
+    else
+      rope_q8_lanes<32>(q0, rope_table, g);
 #pragma unroll
     for (int j = 0; j < 8; ++j) pl.qv[j] = q0[j];
     if (append) rope_new_k(pl.knew[0], a.rope_half, rope_table);
@@ -1330,12 +1357,17 @@ __device__ __forceinline__ int sk_chunk(int total, int n_waves) {
 }
 
 template <int REP, bool FUSED, int DEPTH, bool ROPE, bool Q8 = false, int NH = 1>
-__global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
+// Q8A pages with 128-wide heads run two waves per SIMD: the register budget
+// is held to 256 so that the RoPE variant (whose rotation the compiler would
+// otherwise schedule with every pair and sine/cosine live at once, 370
+// registers) keeps that occupancy too.
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(Q8 && NH == 1 ? 2 : 1)))
+void decode_sk_kernel(DecodeArgs a, int n_seq, int n_waves) {
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
   __shared__ __attribute__((aligned(16))) uint8_t vring_[DEPTH * NH * kVSlot];
   __shared__ __attribute__((aligned(16))) uint8_t newtok_[2 * NH * kRowBytes];  // K row, V row (f16)
   __shared__ __attribute__((aligned(16))) uint8_t rope_table_[ROPE ? kRopeTableBytes : 16];
-  stage_rope_table<ROPE>(a, (lds_u8*)rope_table_);
+  const float rinv = rope_inv_load<ROPE>(a);
   const int wv = blockIdx.x;
   const int n_groups = (n_seq + kWave - 1) / kWave;
   int total = 0, gb = 0, g = 0;
@@ -1346,6 +1378,7 @@ __global__ __launch_bounds__(kWave) void decode_sk_kernel(DecodeArgs a, int n_se
   } else {
     gb = sk_group_bases<FUSED>(a, n_seq, &total);
   }
+  rope_inv_store<ROPE>((lds_u8*)rope_table_, rinv);
   const int chunk = sk_chunk(total, n_waves);
   int cur = wv * chunk;
   const int end = min(total, cur + chunk);
@@ -1488,7 +1521,11 @@ __device__ __forceinline__ WgSeg wg_seg_at(const DecodeArgs& a, int n_seq, int n
 }
 
 template <int REP, bool FUSED, int DEPTH, bool ROPE, bool Q8, int NW, int NH = 1>
-__global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg) {
+// (As for stream-K; the RoPE variant at REP 8 would spill within 256
+// registers, so it keeps its registers and the occupancy they allow.)
+__global__ __launch_bounds__(kWave* NW)
+__attribute__((amdgpu_waves_per_eu(Q8 && NH == 1 && !(ROPE && REP == 8) ? 2 : 1)))
+void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg) {
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
   constexpr int kSlots = Q8 ? 1 : DEPTH;
   constexpr int D = NH * kD;                    // head dim
@@ -1504,7 +1541,7 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
   __shared__ int last_[2];           // cut segments this workgroup merges last (index or -1)
   const int wi = (int)(threadIdx.x / kWave), lane = (int)(threadIdx.x % kWave);
   const int wg = blockIdx.x;
-  stage_rope_table<ROPE>(a, (lds_u8*)rope_table_[wi]);
+  const float rinv = rope_inv_load<ROPE>(a);
 
   // the layout (every wave computes it)
   const int n_groups = (n_seq + kWave - 1) / kWave;
@@ -1517,6 +1554,7 @@ __global__ __launch_bounds__(kWave* NW) void decode_wg_kernel(DecodeArgs a, int 
     gb = sk_group_bases<FUSED>(a, n_seq, &total);
     q = sk_group<FUSED>(a, n_seq, 0, 0);
   }
+  rope_inv_store<ROPE>((lds_u8*)rope_table_[wi], rinv);
   const int C = wg_chunk(total, n_wg, NW);
   const int A = min(total, wg * C), B = min(total, A + C);
   const int Cw = (B - A + NW - 1) / NW;
