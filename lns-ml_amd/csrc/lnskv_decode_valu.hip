@@ -287,17 +287,27 @@ __global__ __launch_bounds__(kBlock) void decode_valu_kernel(DecodeArgs a) {
       uint32_t phys = page_phys(pg, valid);
       PageRegs<DT, D, REP> cur;
       load_page<DT, D, REP>(a, phys, kvh, r, c, cur);
+      // The next page is loaded while this one is consumed, except at
+      // head_dim 256 with 8 query heads on f32 or Q8A pages, where two pages
+      // in flight beside the state (and the Q8A element conversions) exceed
+      // the 512 registers and spilled; the block's other waves then cover
+      // the load latency.
+      constexpr bool kAhead = !(D == 256 && REP == 8 && DT != LNSKV_DTYPE_F16);
       for (; pg <= pg_last; pg += kWavesPerBlock) {
         const int nxt = pg + kWavesPerBlock;
         PageRegs<DT, D, REP> nx;
         bool nvalid = false;
-        if (nxt <= pg_last) {
+        if (kAhead && nxt <= pg_last) {
           const uint32_t nphys = page_phys(nxt, nvalid);
           load_page<DT, D, REP>(a, nphys, kvh, r, c, nx);
         }
         const int tok0 = pg * kPage;
         const bool full = valid && tok0 >= ta && tok0 + kPage <= tb;
         consume_page<DT, D, REP>(st, cur, full, valid, tok0, ta, tb, r);
+        if (!kAhead && nxt <= pg_last) {
+          const uint32_t nphys = page_phys(nxt, nvalid);
+          load_page<DT, D, REP>(a, nphys, kvh, r, c, nx);
+        }
         cur = nx;
         valid = nvalid;
       }
