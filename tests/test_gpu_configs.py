@@ -7,7 +7,10 @@ row-normwise tolerance (1e-3 f16, 1e-5 f32 and Q8A) of the f64 oracle over the e
 stored values, and within the same tolerance of the reference-order f32 scan
 (the reference CPU path); the element-wise relative error (floor 1e-6) is
 reported.  Every page outside the step's footprint is compared with its
-contents before the step."""
+contents before the step.  c2-rope / c2-q8a-rope run the same c2 step
+through the fused RoPE entry point (Llama-3.1 inverse frequencies, rotary =
+head_dim): the oracle rotates q and the new K at position kv_len - 1 before
+its append and scan, and the rotated pages must still match bit for bit."""
 import numpy as np
 import pytest
 import torch
@@ -16,19 +19,22 @@ import oracle as O
 from gpu_util import TOL, host_pages, rel_err, remap_tables, say
 from lnskv import DTYPE_Q8A, NO_PAGE
 from lnskv.configs import make, used_pages
-from lnskv.device import sync
+from lnskv.device import RopeTable, sync
 from lnskv.step import StepRunner
 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5", "c2-q8a"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5", "c2-q8a", "c2-rope", "c2-q8a-rope"])
 def test_config_step(gpu, name):
     """c2-q8a: the c2 draw with the reference's own page type (int8 codes
     and scales; the matrix-core Q8A decode with its in-kernel quantizer)."""
     say("config", name, "build")
-    w = make("c2", dtype=DTYPE_Q8A) if name == "c2-q8a" else make(name)
-    r = StepRunner(w, gpu, n_layers=1, seed=17)
+    w = make("c2", dtype=DTYPE_Q8A) if name.startswith("c2-q8a") else make(name.split("-")[0])
+    rope = None
+    if name.endswith("-rope"):
+        rope = RopeTable(w.head_dim, 500000.0, O.ROPE_LLAMA3, (8.0, 8192.0, 1.0, 4.0), device=gpu)
+    r = StepRunner(w, gpu, n_layers=1, seed=17, rope=rope)
     pk = r.layers[0]
     pages = used_pages(w.tables)
     if w.copies:
@@ -42,13 +48,15 @@ def test_config_step(gpu, name):
         dst = remap[np.array([c[1] for c in w.copies], np.uint32)]
         O.page_copy(hp, src, dst)
     cs, cp = w.chunk_tokens()
+    turn = (lambda x, pos: O.rope_apply(x, rope.rotary_dim, rope.inv_freqs_host, pos)) if rope else \
+        (lambda x, pos: x)
     if len(cs):
-        assert O.append(hp, r.chunk_k.cpu().numpy(), r.chunk_v.cpu().numpy(), cs, cp, tables) == 0
+        assert O.append(hp, turn(r.chunk_k.cpu().numpy(), cp), r.chunk_v.cpu().numpy(), cs, cp, tables) == 0
     rows = r.dec_rows
     dec_tables = tables[rows]
     kv_len = w.kv_len[rows]
-    assert O.append(hp, r.k_new.cpu().numpy(), r.v_new.cpu().numpy(), np.arange(len(rows), dtype=np.int32),
-                    kv_len - 1, dec_tables) == 0
+    assert O.append(hp, turn(r.k_new.cpu().numpy(), kv_len - 1), r.v_new.cpu().numpy(),
+                    np.arange(len(rows), dtype=np.int32), kv_len - 1, dec_tables) == 0
 
     # the whole pools before the step: pages outside its footprint must come
     # out untouched
@@ -70,7 +78,7 @@ def test_config_step(gpu, name):
     if w.dtype == DTYPE_Q8A:
         assert np.array_equal(got.ks, hp.ks) and np.array_equal(got.vs, hp.vs), "scales differ"
 
-    q = r.q.cpu().numpy()
+    q = turn(r.q.cpu().numpy(), kv_len - 1)
     o = out.cpu().numpy()
     assert np.isfinite(o).all()
     ref = O.decode_f64(hp, q, dec_tables, kv_len, None, w.scale)
@@ -80,7 +88,7 @@ def test_config_step(gpu, name):
         float(ele.max()), "median element", float(np.median(ele)))
     assert err.max() < TOL[w.dtype]
     assert np.isfinite(ele).all()
-    if name in ("c1", "c2", "c2-q8a"):
+    if name in ("c1", "c2", "c2-q8a", "c2-q8a-rope"):
         scan = O.decode_refscan(hp, q, dec_tables, kv_len, None, w.scale)
         assert rel_err(o, scan.astype(np.float64)).max() < TOL[w.dtype]
     # pages outside the step's footprint are untouched: a second step is
