@@ -1052,6 +1052,10 @@ int lnskv_prefill_attention(const lnskv_pages* c, const float* q, float* out, co
   if ((c->dtype != LNSKV_DTYPE_F16 && c->dtype != LNSKV_DTYPE_Q8A) || c->head_dim != 128)
     return fail(LNSKV_ERR_UNSUPPORTED, "prefill attention is built for f16 and Q8A pages with head_dim 128");
   if (!aligned16(chunks) || !aligned16(q)) return fail(LNSKV_ERR_INVALID, "chunks and q must be 16-byte aligned");
+  // the Q8A kernel addresses each scale array with 32-bit byte offsets
+  if (c->dtype == LNSKV_DTYPE_Q8A && (uint64_t)c->num_pages * kPage * c->n_kv_heads * sizeof(float) > 0x7FFFFFF0u)
+    return fail(LNSKV_ERR_UNSUPPORTED, "prefill over Q8A pages needs scale arrays under 2 GiB (%u pages x %u kv heads)",
+                c->num_pages, c->n_kv_heads);
   PrefillArgs a{};
   a.k_pages = static_cast<const uint8_t*>(c->k_pages);
   a.v_pages = static_cast<const uint8_t*>(c->v_pages);
