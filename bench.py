@@ -384,11 +384,12 @@ def timed_steps(step, stream, steps: int, warmup: int) -> tuple[float, float]:
 
 
 def config_measure(name: str, dev, steps: int, layers: int = 2, kv_dtype: int | None = None,
-                   pattern_reps: int = 0, prefill_reps: int = 0) -> dict:
+                   pattern_reps: int = 0, prefill_reps: int = 0, rope: bool = False) -> dict:
     """One configuration's step (its own workload and pools, `layers` of them
     cycled): event mean over `steps` steps, median of per-step events,
     algorithmic GB/s and fraction of 8 TB/s; optionally the load ceiling of
-    its page pattern and chunked prefill over its pages.  c5 adds the
+    its page pattern and chunked prefill over its pages.  rope: the step
+    through the fused RoPE entry point (the --rope table).  c5 adds the
     full-copy fork variant."""
     import torch
 
@@ -396,7 +397,12 @@ def config_measure(name: str, dev, steps: int, layers: int = 2, kv_dtype: int | 
     from lnskv.step import StepRunner
 
     w = make(name) if kv_dtype is None else make(name, dtype=kv_dtype)
-    runner = StepRunner(w, dev, n_layers=layers, seed=1)
+    table = None
+    if rope:
+        from lnskv.device import RopeTable
+
+        table = RopeTable(w.head_dim, 500000.0, 2, (8.0, 8192.0, 1.0, 4.0), device=dev)
+    runner = StepRunner(w, dev, n_layers=layers, seed=1, rope=table)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     step = lambda i: runner.run(i % layers)  # noqa: E731
@@ -411,7 +417,7 @@ def config_measure(name: str, dev, steps: int, layers: int = 2, kv_dtype: int | 
         if pc:
             res["pattern_ceiling_us"] = pc["us_per_launch"]
             res["frac_of_pattern_ceiling"] = round(pc["us_per_launch"] / (ev * 1e6), 4)
-    traffic = measured_traffic(name, w.dtype)
+    traffic = measured_traffic(name, w.dtype, rope)
     if traffic:
         res["traffic_bytes"] = traffic["bytes"]
         res["traffic_over_algorithmic"] = traffic["over_algorithmic"]
@@ -797,6 +803,8 @@ def main():
     if args.extras and w.name == "c2" and args.kv_dtype == "config" and not args.rope:
         extras = {"c2_q8a_pages": config_measure("c2", dev, args.steps, layers=args.layers, kv_dtype=2,
                                                  pattern_reps=args.pattern_reps, prefill_reps=args.prefill_reps),
+                  "c2_q8a_pages_rope": config_measure("c2", dev, args.steps, layers=args.layers, kv_dtype=2,
+                                                      rope=True),
                   "reference_call_b1_q8a": reference_call_measure(dev),
                   "qwen35_shape": qwen35_measure(dev, min(args.steps, 100), pattern_reps=args.pattern_reps),
                   "block_table_upload": table_upload_measure(w, dev)}
