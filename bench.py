@@ -265,14 +265,14 @@ def prefill_measure(w, runner, dev, reps: int, chunk: int = 256) -> dict | None:
     query attends [0, its position].  Algorithmic work: 4 * head_dim flops
     per (query, head, attended token) (q.k and p.v); the kernel runs q and p
     as f16 hi and lo parts, twice that on the matrix cores.  Layers cycled,
-    HIP events around `reps` launches.  For config chunks the same queries
+    HIP events around `reps` launches.  Up to 8192 queries, the same queries
     also go through lnskv_decode as one row each (kv_len = position + 1: the
     reference's token-at-a-time order of work, batched into one launch), and
     the two results are compared."""
     import numpy as np
     import torch
 
-    if reps <= 0 or w.dtype not in (1, 2) or w.head_dim != 128:
+    if reps <= 0 or w.dtype not in (1, 2) or w.head_dim not in (128, 256):
         return None
     cs, cp = w.chunk_tokens()
     desc, tok = [], 0
@@ -322,7 +322,10 @@ def prefill_measure(w, runner, dev, reps: int, chunk: int = 256) -> dict | None:
            "tflop_per_s": round(flops / dt / 1e12, 1),
            "frac_of_f16_mfma_peak": round(flops / dt / 1e12 / 2500.0, 4),
            "mfma_tflop_per_s_with_hi_lo": round(2 * flops / dt / 1e12, 1)}
-    if len(cs) and tok <= 4096:
+    if not len(cs):  # the queries' rows and positions, from the chunks
+        cs = np.concatenate([np.full(ln, r, np.int64) for (r, _, ln, _) in desc])
+        cp = np.concatenate([np.arange(p0, p0 + ln) for (_, p0, ln, _) in desc])
+    if tok <= 8192:
         # the same queries as single-token decode rows of one lnskv_decode call
         tables = runner.tables[torch.from_numpy(cs.astype(np.int64)).to(dev)].contiguous()
         kv_len = torch.from_numpy((cp + 1).astype(np.int32)).to(dev)
@@ -505,7 +508,7 @@ def full_copy_fork(w, runner, dev, reps: int = 20) -> dict:
             "note": "every page of the 8 forked children copied (the page-sharing fork copies only tail pages)"}
 
 
-def qwen35_measure(dev, steps: int, layers: int = 4, pattern_reps: int = 40) -> dict:
+def qwen35_measure(dev, steps: int, layers: int = 4, pattern_reps: int = 40, prefill_reps: int = 0) -> dict:
     """lns-ml's own full-attention layer (Qwen3.5: Hq16/Hkv4/d256) on the
     engine's Q8A pages, the engine's per-layer order in one call
     (lnskv_gated_append_decode: RoPE rotary 64 of 256 with theta 1e7 turned
@@ -514,7 +517,9 @@ def qwen35_measure(dev, steps: int, layers: int = 4, pattern_reps: int = 40) -> 
     load ceiling; and the reference's one-sequence call at pos 4095 (one
     kernel, the workgroup schedule), per call from HIP graph replay over 32
     layers.  Bytes: the K/V codes and scales of every attended token, the
-    append, q/out, the gate read, table entries."""
+    append, q/out, the gate read, table entries.  prefill_reps > 0: also the
+    chunked prefill of the batch's last 256 tokens per sequence over its
+    pages (the 256-wide heads' prompt path)."""
     import torch
 
     from lnskv import DTYPE_Q8A
@@ -541,6 +546,8 @@ def qwen35_measure(dev, steps: int, layers: int = 4, pattern_reps: int = 40) -> 
     if pc:
         res["pattern_ceiling_us"] = pc["us_per_launch"]
         res["frac_of_pattern_ceiling"] = round(pc["us_per_launch"] / (ev * 1e6), 4)
+    if prefill_reps > 0:
+        res["chunked_prefill_attention"] = prefill_measure(w, runner, dev, prefill_reps)
     del runner
     torch.cuda.empty_cache()
     # the one-sequence call, 32 layers' pools cycled
@@ -806,7 +813,8 @@ def main():
                   "c2_q8a_pages_rope": config_measure("c2", dev, args.steps, layers=args.layers, kv_dtype=2,
                                                       rope=True),
                   "reference_call_b1_q8a": reference_call_measure(dev),
-                  "qwen35_shape": qwen35_measure(dev, min(args.steps, 100), pattern_reps=args.pattern_reps),
+                  "qwen35_shape": qwen35_measure(dev, min(args.steps, 100), pattern_reps=args.pattern_reps,
+                                                 prefill_reps=args.prefill_reps),
                   "block_table_upload": table_upload_measure(w, dev)}
         for name in ("c1", "c3", "c4", "c5"):
             extras[name] = config_measure(name, dev, min(args.steps, 100))

@@ -263,7 +263,7 @@ int lnskv_rope_append_decode(const lnskv_pages* c, const lnskv_rope* rope, const
  *   [max(p_start, pos(t) - window + 1), pos(t)], each prompt token its own
  *   kv_p_start as the reference's per-token loop gives it (engine.rs:
  *   3007-3013); window = 0: [p_start, pos(t)].  f16 or Q8A pages with
- *   head_dim 128 (Q8A: scale arrays under 2 GiB, num_pages * 16 * n_kv_heads
+ *   head_dim 128 or 256 (Q8A: scale arrays under 2 GiB, num_pages * 16 * n_kv_heads
  *   < 2^29; LNSKV_ERR_UNSUPPORTED otherwise); Q8A codes are turned to
  *   f16 in LDS (code x 1, the row scale applied to the scores and to the
  *   probabilities), so the result is the dequantised pages' attention.

@@ -2051,21 +2051,26 @@ template int launch_decode_mfma_wg<true>(const DecodeArgs&, int, int, int, int, 
 namespace {
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-constexpr int kPfSlot = 4 * kVSlot;  // K and V of two pages
-constexpr int kPfBatch = 2;                 // pairs consumed per barrier (1 to 3)
-constexpr int kPfDepth = 3 * kPfBatch;      // ring slots: a batch consumed, a batch in flight, a batch issued
+// K and V of two pages, per 128-wide half of the head: [K p0 | K p1 | V p0 | V p1]
+template <int NH>
+constexpr int kPfSlot = NH * 4 * kVSlot;
 
 // Two query heads per wave and eight waves per workgroup (two per SIMD, 256
 // VGPRs each): measured against four heads with four waves (one per SIMD,
 // 20% slower), one head with eight waves (16% slower) and two heads with
 // four waves, two workgroups per CU (35% slower) on c2's pages.
-template <int REP>
+// 256-wide heads (NH = 2 halves): one query head per wave (the accumulators
+// and operands of a second would not fit in 256 VGPRs) and one pair per
+// barrier (a pair's slot is twice as large).
+template <int REP, int NH = 1>
 struct PfShape {
-  static constexpr int HW = REP < 2 ? REP : 2;  // query heads per wave
-  static constexpr int WPQ = REP / HW;           // waves per 16 queries
-  static constexpr int NW = 8;                   // waves per workgroup
-  static constexpr int QT = 16 * (NW / WPQ);     // queries per tile
-  static constexpr int RPW = 16 / NW;                          // page regions a wave DMAs per pair
+  static constexpr int HW = NH == 2 ? 1 : (REP < 2 ? REP : 2);  // query heads per wave
+  static constexpr int WPQ = REP / HW;                          // waves per 16 queries
+  static constexpr int NW = 8;                                  // waves per workgroup
+  static constexpr int QT = 16 * (NW / WPQ);                    // queries per tile
+  static constexpr int RPW = 16 * NH / NW;                      // quarter regions a wave DMAs per pair
+  static constexpr int kBatch = NH == 2 ? 1 : 2;                // pairs consumed per barrier (1 to 3)
+  static constexpr int kDepth = 3 * kBatch;  // ring slots: a batch consumed, a batch in flight, a batch issued
 };
 
 // Workgroup barrier after this wave's LDS accesses have completed.  No
@@ -2091,92 +2096,111 @@ struct PfLanes {
 };
 
 // DMA of this wave's share of pages ph0 and ph1 into `slot`: quarter w % 4
-// of page regions (w / 4) * RPW .. + RPW - 1 (region r: K of page r for r < 2,
-// V of page r - 2 otherwise), RPW vector-memory instructions.  A missing page
-// reads page 0 (in bounds); its tokens are masked and its V rows zeroed
-// before use.
+// of page regions (w / 4) * RPW .. + RPW - 1 (region r: half r / 4 of the
+// head; within it K of page r % 4 for r % 4 < 2, V of page r % 4 - 2
+// otherwise), RPW vector-memory instructions.  A missing page reads page 0
+// (in bounds); its tokens are masked and its V rows zeroed before use.
 template <int RPW>
 __device__ __forceinline__ void pf_issue(const PrefillArgs& a, const PfLanes& pl, uint32_t page_bytes,
                                          uint32_t kvh_off, lds_u8* slot, uint32_t ph0, uint32_t ph1, int w) {
 #pragma unroll
   for (int t = 0; t < RPW; ++t) {
     const int r = (w >> 2) * RPW + t;  // wave-uniform
-    const uint32_t ph = (r & 1) ? ph1 : ph0;
-    const size_t base = (size_t)(ph < a.num_pages ? ph : 0u) * page_bytes + kvh_off;
-    const uint8_t* src = (r >> 1) ? a.v_pages : a.k_pages;
+    // region within the half, and the half (one half: r < 4, eight waves)
+    const int rr = RPW == 2 ? r : r & 3, hf = RPW == 2 ? 0 : r >> 2;
+    const uint32_t ph = (rr & 1) ? ph1 : ph0;
+    const size_t base = (size_t)(ph < a.num_pages ? ph : 0u) * page_bytes + kvh_off + (size_t)hf * kRowBytes;
+    const uint8_t* src = (rr >> 1) ? a.v_pages : a.k_pages;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)(src + base), (short)0, (int)page_bytes, kBufferFormat);
+    // the offset as a value select (a select of the two fields' addresses
+    // would keep pl in memory)
+    const uint32_t off = pl.koff + ((rr >> 1) ? pl.voff - pl.koff : 0u);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(slot + r * kVSlot + pl.lds_q),
-                                             16, (int)((r >> 1) ? pl.voff : pl.koff), 0, 0, 0);
+                                             16, (int)off, 0, 0, 0);
   }
 }
 
-// Q8A pages.  A pair's int8 codes (four 2 KiB regions: K of page 0, K of
-// page 1, V of page 0, V of page 1, 16 rows of 128 codes each) come by DMA,
-// wave w taking half w & 1 (rows 8 (w & 1) ..) of region w >> 1, so lane l
-// of wave w fetches row 8 (w & 1) + l / 8, codes 16 (l % 8) .. + 15 -- the
-// same 16 bytes it converts to f16 afterwards; each wave also DMAs its own
-// copy of the pair's 32 K and 32 V scales (lane l: page (l / 16) & 1, token
-// l % 16).  Three vector-memory instructions per wave and pair.
-constexpr int kPfCodeSlot = 4 * 2048;                     // the codes of a pair
-constexpr int kPfScaleWave = 512;                         // K scales [0, 256), V scales [256, 512)
-constexpr int kPfQ8Slot = kPfCodeSlot + 8 * kPfScaleWave;  // codes, then eight waves' scale copies
-constexpr int kPfQ8Rpw = 3;
+// Q8A pages.  A pair's int8 codes (per 128-wide half of the head, four
+// 2 KiB regions: K of page 0, K of page 1, V of page 0, V of page 1, 16 rows
+// of 128 codes each) come by DMA in 1 KiB pieces: piece i = NH w + t (t <
+// NH) of wave w is half i & 1 (rows 8 (i & 1) ..) of region i >> 1 (region r:
+// half r / 4, region r % 4), so lane l fetches row 8 (i & 1) + l / 8, codes
+// 16 (l % 8) .. + 15 of that region -- the same 16 bytes it converts to f16
+// afterwards; each wave also DMAs its own copy of the pair's 32 K and 32 V
+// scales (lane l: page (l / 16) & 1, token l % 16).  NH + 2 vector-memory
+// instructions per wave and pair.
+template <int NH>
+constexpr int kPfCodeSlot = NH * 4 * 2048;                           // the codes of a pair
+constexpr int kPfScaleWave = 512;                                    // K scales [0, 256), V scales [256, 512)
+template <int NH>
+constexpr int kPfQ8Slot = kPfCodeSlot<NH> + 8 * kPfScaleWave;        // codes, then eight waves' scale copies
 
+template <int NH>
 __device__ __forceinline__ void pf_issue_q8(const PrefillArgs& a, uint32_t rs, uint32_t kvh, lds_u8* slot,
                                             uint32_t ph0, uint32_t ph1, int w) {
   typedef __attribute__((address_space(3))) void lds_void;
   const int lane = (int)(threadIdx.x & (kWave - 1));
   const uint32_t page_bytes = kPage * rs;
-  const int r = w >> 1;  // wave-uniform
-  const uint32_t ph = (r & 1) ? ph1 : ph0;
-  const size_t base = (size_t)(ph < a.num_pages ? ph : 0u) * page_bytes + (size_t)kvh * kD;
-  const uint8_t* src = (r >> 1) ? a.v_pages : a.k_pages;
-  const __amdgpu_buffer_rsrc_t rsc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(src + base), (short)0, (int)page_bytes, kBufferFormat);
-  const uint32_t row = 8u * (uint32_t)(w & 1) + (uint32_t)(lane >> 3);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (lds_void*)(slot + r * 2048 + (w & 1) * 1024), 16,
-                                           (int)(row * rs + 16u * (uint32_t)(lane & 7)), 0, 0, 0);
+#pragma unroll
+  for (int t = 0; t < NH; ++t) {
+    // wave-uniform; with one half, r < 4 (eight waves)
+    const int i = NH * w + t, r = i >> 1, rr = NH == 1 ? r : r & 3, hf = NH == 1 ? 0 : r >> 2;
+    const uint32_t ph = (rr & 1) ? ph1 : ph0;
+    const size_t base = (size_t)(ph < a.num_pages ? ph : 0u) * page_bytes + (size_t)kvh * (NH * kD) +
+                        (size_t)hf * kD;
+    const uint8_t* src = (rr >> 1) ? a.v_pages : a.k_pages;
+    const __amdgpu_buffer_rsrc_t rsc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(src + base), (short)0, (int)page_bytes, kBufferFormat);
+    const uint32_t row = 8u * (uint32_t)(i & 1) + (uint32_t)(lane >> 3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (lds_void*)(slot + r * 2048 + (i & 1) * 1024), 16,
+                                             (int)(row * rs + 16u * (uint32_t)(lane & 7)), 0, 0, 0);
+  }
   // scales: token lane % 16 of page (lane / 16) & 1 (a missing page: page 0)
   const uint32_t sp = ((lane >> 4) & 1) ? ph1 : ph0;
   const uint32_t sidx = ((sp < a.num_pages ? sp : 0u) * kPage + (uint32_t)(lane & 15)) * (uint32_t)a.n_kv + kvh;
   const int sbytes = (int)min((size_t)a.num_pages * kPage * (size_t)a.n_kv * 4, (size_t)0x7FFFFFF0);
   const __amdgpu_buffer_rsrc_t ksr = __builtin_amdgcn_make_buffer_rsrc((void*)a.k_scales, (short)0, sbytes, kBufferFormat);
   const __amdgpu_buffer_rsrc_t vsr = __builtin_amdgcn_make_buffer_rsrc((void*)a.v_scales, (short)0, sbytes, kBufferFormat);
-  lds_u8* sc = slot + kPfCodeSlot + w * kPfScaleWave;
+  lds_u8* sc = slot + kPfCodeSlot<NH> + w * kPfScaleWave;
   __builtin_amdgcn_raw_ptr_buffer_load_lds(ksr, (lds_void*)sc, 4, (int)(4u * sidx), 0, 0, 0);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(vsr, (lds_void*)(sc + 256), 4, (int)(4u * sidx), 0, 0, 0);
 }
 
-// This wave's 16 codes of the pair (the ones it DMA'd) to f16 in the f16 pair
-// slot `dst` (the layout pf_consume reads): K token t's chunk c at c ^ t of
-// row t, V token t in row R = 4 (t % 4) + t / 4 with chunk c at c ^ sw(R).
-// The codes are exact in f16.
+// This wave's codes of the pair (the NH pieces it DMA'd) to f16 in the f16
+// pair slot `dst` (the layout pf_consume reads, per half): K token t's chunk
+// c at c ^ t of row t, V token t in row R = 4 (t % 4) + t / 4 with chunk c at
+// c ^ sw(R).  The codes are exact in f16.
+template <int NH>
 __device__ __forceinline__ void pf_convert_q8(const lds_u8* codes, lds_u8* dst, int w) {
   const int lane = (int)(threadIdx.x & (kWave - 1));
-  const int r = w >> 1;
-  const int t = 8 * (w & 1) + (lane >> 3), c16 = lane & 7;
-  u32x4 x;
-  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
-               : "=v"(x)
-               : "v"((uint32_t)(size_t)(codes + r * 2048 + (w & 1) * 1024 + 16 * lane))
-               : "memory");
-  const half8 lo = i8x8_to_f16(uint2v{x[0], x[1]}), hi = i8x8_to_f16(uint2v{x[2], x[3]});
-  const int p = r & 1;
-  uint32_t o0, o1;
-  if (r < 2) {  // K
-    o0 = (uint32_t)(p * kVSlot + t * kRowBytes) + 16u * ((uint32_t)(2 * c16) ^ (uint32_t)t);
-    o1 = (uint32_t)(p * kVSlot + t * kRowBytes) + 16u * ((uint32_t)(2 * c16 + 1) ^ (uint32_t)t);
-  } else {  // V
-    const int R = 4 * (t & 3) + (t >> 2);
-    o0 = (uint32_t)((2 + p) * kVSlot + R * kRowBytes) + 16u * ((uint32_t)(2 * c16) ^ v_swz(R));
-    o1 = (uint32_t)((2 + p) * kVSlot + R * kRowBytes) + 16u * ((uint32_t)(2 * c16 + 1) ^ v_swz(R));
-  }
-  // inline asm stores: the compiler would otherwise wait for every DMA in
-  // flight before a plain LDS store (it cannot tell which slot a DMA writes)
   const uint32_t d = (uint32_t)(size_t)dst;
-  asm volatile("ds_write_b128 %0, %1" : : "v"(d + o0), "v"(lo) : "memory");
-  asm volatile("ds_write_b128 %0, %1" : : "v"(d + o1), "v"(hi) : "memory");
+#pragma unroll
+  for (int tt = 0; tt < NH; ++tt) {
+    const int i = NH * w + tt, r = i >> 1, rr = NH == 1 ? r : r & 3, hf = NH == 1 ? 0 : r >> 2;
+    const int t = 8 * (i & 1) + (lane >> 3), c16 = lane & 7;
+    u32x4 x;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                 : "=v"(x)
+                 : "v"((uint32_t)(size_t)(codes + r * 2048 + (i & 1) * 1024 + 16 * lane))
+                 : "memory");
+    const half8 lo = i8x8_to_f16(uint2v{x[0], x[1]}), hi = i8x8_to_f16(uint2v{x[2], x[3]});
+    const int p = rr & 1;
+    const uint32_t hb = (uint32_t)hf * (uint32_t)kPfSlot<1>;  // this half's 16 KiB
+    uint32_t o0, o1;
+    if (rr < 2) {  // K
+      o0 = hb + (uint32_t)(p * kVSlot + t * kRowBytes) + 16u * ((uint32_t)(2 * c16) ^ (uint32_t)t);
+      o1 = hb + (uint32_t)(p * kVSlot + t * kRowBytes) + 16u * ((uint32_t)(2 * c16 + 1) ^ (uint32_t)t);
+    } else {  // V
+      const int R = 4 * (t & 3) + (t >> 2);
+      o0 = hb + (uint32_t)((2 + p) * kVSlot + R * kRowBytes) + 16u * ((uint32_t)(2 * c16) ^ v_swz(R));
+      o1 = hb + (uint32_t)((2 + p) * kVSlot + R * kRowBytes) + 16u * ((uint32_t)(2 * c16 + 1) ^ v_swz(R));
+    }
+    // inline asm stores: the compiler would otherwise wait for every DMA in
+    // flight before a plain LDS store (it cannot tell which slot a DMA writes)
+    asm volatile("ds_write_b128 %0, %1" : : "v"(d + o0), "v"(lo) : "memory");
+    asm volatile("ds_write_b128 %0, %1" : : "v"(d + o1), "v"(hi) : "memory");
+  }
 }
 
 // MODE 0: every token of the pair is attended by every query of the wave;
@@ -2191,74 +2215,124 @@ __device__ __forceinline__ void pf_convert_q8(const lds_u8* codes, lds_u8* dst, 
 // each pair's largest; acc is rescaled exactly when it moves), so that the
 // f16 lo parts of the weights stay normal numbers; l sums the unscaled
 // weights and the output is acc * vnorm / l.
-template <int HW, int MODE, bool Q8 = false>
-__device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW], float (&l)[HW],
-                                           const half8 (&qh)[HW][4], const half8 (&ql)[HW][4],
+// NH = 2 (256-wide heads): the slot holds the two halves' pairs one after the
+// other (16 KiB apart); q operand 4 hf + j and accumulator 8 hf + nb belong
+// to half hf.  Both halves' K operands are read first (the scores sum over
+// them), then both halves' V operands, which stay in flight during the
+// softmax.
+template <int HW, int MODE, bool Q8 = false, int NH = 1>
+__device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8 * NH], float (&m)[HW], float (&l)[HW],
+                                           const half8 (&qh)[HW][4 * NH], const half8 (&ql)[HW][4 * NH],
                                            const float (&qexp)[HW], const PfLanes& pl, lds_u8* slot, int tok0,
                                            bool v0, bool v1, int ta, int tb, int qpos, int qlo, bool qok, int g,
                                            int n, const lds_u8* scales = nullptr, float* vnorm = nullptr) {
+  static_assert(NH == 1 || HW == 1, "256-wide heads: one query head per wave");
   if constexpr (MODE == 2 && !Q8) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = tok0 + 16 * p + 4 * g + j;
-        if (!((p ? v1 : v0) && t >= ta && t < tb))
-          *(lds_u32x4*)(slot + (2 + p) * kVSlot + (4 * j + g) * kRowBytes + 16 * n) = u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int t = tok0 + 16 * p + 4 * g + j;
+          if (!((p ? v1 : v0) && t >= ta && t < tb))
+            *(lds_u32x4*)(slot + hf * kPfSlot<1> + (2 + p) * kVSlot + (4 * j + g) * kRowBytes + 16 * n) =
+                u32x4{0u, 0u, 0u, 0u};
+        }
   }
-  // K operands of both pages, then the V operands of both pages; the reads
-  // are inline asm because the compiler cannot tell which slot a DMA writes
-  // and would wait for every DMA in flight before a plain LDS read.  This
-  // slot's DMAs have completed (vmcnt wait and barrier before the call).
-  // the XOR bases pass through an empty asm so that the compiler rebuilds
-  // the offsets here instead of hoisting all twelve out of the pair loop
-  uint32_t kx = pl.kx, vx = pl.vx;
-  asm volatile("" : "+v"(kx), "+v"(vx));
-  const uint32_t kb = (uint32_t)(size_t)slot + pl.krow;
-  half8 k[2][4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t ka = kb + ((64u * (uint32_t)j) ^ kx);
-    asm volatile("ds_read_b128 %0, %1" : "=v"(k[0][j]) : "v"(ka) : "memory");
-    asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(k[1][j]) : "v"(ka) : "memory");
-  }
-  const uint32_t vb = (uint32_t)(size_t)slot + 2 * kVSlot + pl.vrow;
-  short4v bv[2][8];
-  auto read_v = [&](int nb) {
-    const uint32_t a0 = vb + ((32u * (uint32_t)nb) ^ vx);
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[0][nb]) : "v"(a0) : "memory");
-    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(bv[1][nb]) : "v"(a0) : "memory");
-  };
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) read_v(nb);
-  // LDS reads complete in order: the 8 V reads just issued may be outstanding
-  asm volatile("s_waitcnt lgkmcnt(8)"
-               : "+v"(k[0][0]), "+v"(k[0][1]), "+v"(k[0][2]), "+v"(k[0][3]), "+v"(k[1][0]), "+v"(k[1][1]),
-                 "+v"(k[1][2]), "+v"(k[1][3])
-               :
-               : "memory");
-#pragma unroll
-  for (int nb = 4; nb < 8; ++nb) read_v(nb);
   float4v sacc[HW][2];
+  short4v bv[2][8];
+  if constexpr (NH == 1) {
+    // K operands of both pages, then the V operands of both pages; the reads
+    // are inline asm because the compiler cannot tell which slot a DMA writes
+    // and would wait for every DMA in flight before a plain LDS read.  This
+    // slot's DMAs have completed (vmcnt wait and barrier before the call).
+    // the XOR bases pass through an empty asm so that the compiler rebuilds
+    // the offsets here instead of hoisting all twelve out of the pair loop
+    uint32_t kx = pl.kx, vx = pl.vx;
+    asm volatile("" : "+v"(kx), "+v"(vx));
+    const uint32_t kb = (uint32_t)(size_t)slot + pl.krow;
+    half8 k[2][4];
 #pragma unroll
-  for (int hh = 0; hh < HW; ++hh)
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t ka = kb + ((64u * (uint32_t)j) ^ kx);
+      asm volatile("ds_read_b128 %0, %1" : "=v"(k[0][j]) : "v"(ka) : "memory");
+      asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(k[1][j]) : "v"(ka) : "memory");
+    }
+    const uint32_t vb = (uint32_t)(size_t)slot + 2 * kVSlot + pl.vrow;
+    auto read_v = [&](int nb) {
+      const uint32_t a0 = vb + ((32u * (uint32_t)nb) ^ vx);
+      asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[0][nb]) : "v"(a0) : "memory");
+      asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(bv[1][nb]) : "v"(a0) : "memory");
+    };
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int nb = 0; nb < 4; ++nb) read_v(nb);
+    // LDS reads complete in order: the 8 V reads just issued may be outstanding
+    asm volatile("s_waitcnt lgkmcnt(8)"
+                 : "+v"(k[0][0]), "+v"(k[0][1]), "+v"(k[0][2]), "+v"(k[0][3]), "+v"(k[1][0]), "+v"(k[1][1]),
+                   "+v"(k[1][2]), "+v"(k[1][3])
+                 :
+                 : "memory");
+#pragma unroll
+    for (int nb = 4; nb < 8; ++nb) read_v(nb);
+#pragma unroll
+    for (int hh = 0; hh < HW; ++hh)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[p][j], qh[hh][j], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[p][j], ql[hh][j], s, 0, 0, 0);
+        }
+        sacc[hh][p] = s;
+      }
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(bv[0][0]), "+v"(bv[0][1]), "+v"(bv[0][2]), "+v"(bv[0][3]), "+v"(bv[0][4]), "+v"(bv[0][5]),
+                   "+v"(bv[0][6]), "+v"(bv[0][7]), "+v"(bv[1][0]), "+v"(bv[1][1]), "+v"(bv[1][2]), "+v"(bv[1][3]),
+                   "+v"(bv[1][4]), "+v"(bv[1][5]), "+v"(bv[1][6]), "+v"(bv[1][7])
+                 :
+                 : "memory");
+  } else {
+    // one half's K operands at a time (the second half's at +16 KiB), each
+    // waited for before its products: the other wave on the SIMD covers the
+    // read latency, and 32 operand registers fewer stay live than with both
+    // halves in flight (the accumulators and q of a 256-wide head take 128)
+    uint32_t kx = pl.kx;
+    asm volatile("" : "+v"(kx));
+    const uint32_t kb = (uint32_t)(size_t)slot + pl.krow;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      half8 k[2][4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[p][j], qh[hh][j], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[p][j], ql[hh][j], s, 0, 0, 0);
+        const uint32_t ka = kb + ((64u * (uint32_t)j) ^ kx);
+        if (hf == 0) {
+          asm volatile("ds_read_b128 %0, %1" : "=v"(k[0][j]) : "v"(ka) : "memory");
+          asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(k[1][j]) : "v"(ka) : "memory");
+        } else {
+          asm volatile("ds_read_b128 %0, %1 offset:16384" : "=v"(k[0][j]) : "v"(ka) : "memory");
+          asm volatile("ds_read_b128 %0, %1 offset:20480" : "=v"(k[1][j]) : "v"(ka) : "memory");
+        }
       }
-      sacc[hh][p] = s;
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(k[0][0]), "+v"(k[0][1]), "+v"(k[0][2]), "+v"(k[0][3]), "+v"(k[1][0]), "+v"(k[1][1]),
+                     "+v"(k[1][2]), "+v"(k[1][3])
+                   :
+                   : "memory");
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        float4v sv = hf ? sacc[0][p] : float4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[p][j], qh[0][4 * hf + j], sv, 0, 0, 0);
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[p][j], ql[0][4 * hf + j], sv, 0, 0, 0);
+        }
+        sacc[0][p] = sv;
+      }
+      __builtin_amdgcn_sched_barrier(0);  // the next half's reads follow these products
     }
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(bv[0][0]), "+v"(bv[0][1]), "+v"(bv[0][2]), "+v"(bv[0][3]), "+v"(bv[0][4]), "+v"(bv[0][5]),
-                 "+v"(bv[0][6]), "+v"(bv[0][7]), "+v"(bv[1][0]), "+v"(bv[1][1]), "+v"(bv[1][2]), "+v"(bv[1][3]),
-                 "+v"(bv[1][4]), "+v"(bv[1][5]), "+v"(bv[1][6]), "+v"(bv[1][7])
-               :
-               : "memory");
+  }
   // Q8: the scales of the lane's tokens 16 p + 4g + ii (e = 4p + ii)
   float ks[8], vsc[8], vinv = 1.0f;
   if constexpr (Q8) {
@@ -2287,12 +2361,40 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
 #pragma unroll
         for (int hh = 0; hh < HW; ++hh)
 #pragma unroll
-          for (int nb = 0; nb < 8; ++nb) acc[hh][nb] *= rr;
+          for (int nb = 0; nb < 8 * NH; ++nb) acc[hh][nb] *= rr;
       }
       *vnorm = ldexpf(1.0f, ex);
     }
     vinv = *vnorm > 0.0f ? 1.0f / *vnorm : 0.0f;
   }
+  // NH = 2: V operands of half hf into bv[.][0 .. 7] (the first half's stay
+  // in flight during the softmax; the second half's are read after the
+  // first half's products, into the same registers)
+  auto read_v_half = [&](int hf) {
+    uint32_t vx = pl.vx;
+    asm volatile("" : "+v"(vx));
+    const uint32_t vb = (uint32_t)(size_t)slot + 2 * kVSlot + pl.vrow;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const uint32_t a0 = vb + ((32u * (uint32_t)nb) ^ vx);
+      if (hf == 0) {
+        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(bv[0][nb]) : "v"(a0) : "memory");
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(bv[1][nb]) : "v"(a0) : "memory");
+      } else {
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:16384" : "=v"(bv[0][nb]) : "v"(a0) : "memory");
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:20480" : "=v"(bv[1][nb]) : "v"(a0) : "memory");
+      }
+    }
+  };
+  auto wait_v = [&]() {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(bv[0][0]), "+v"(bv[0][1]), "+v"(bv[0][2]), "+v"(bv[0][3]), "+v"(bv[0][4]), "+v"(bv[0][5]),
+                   "+v"(bv[0][6]), "+v"(bv[0][7]), "+v"(bv[1][0]), "+v"(bv[1][1]), "+v"(bv[1][2]), "+v"(bv[1][3]),
+                   "+v"(bv[1][4]), "+v"(bv[1][5]), "+v"(bv[1][6]), "+v"(bv[1][7])
+                 :
+                 : "memory");
+  };
+  if constexpr (NH == 2) read_v_half(0);
 #pragma unroll
   for (int hh = 0; hh < HW; ++hh) {
     // raw scores (still scaled by 2^-E); masked tokens -inf
@@ -2319,7 +2421,7 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
       for (int ii = 0; ii < 4; ++ii) {
         const float aq = __shfl(alpha, 20 * g + ii, kWave);
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) acc[hh][nb][ii] *= aq;
+        for (int nb = 0; nb < 8 * NH; ++nb) acc[hh][nb][ii] *= aq;
       }
     }
     // p = 2^(s 2^E - m) (the product is exact, so one rounding as s - m);
@@ -2342,10 +2444,20 @@ __device__ __forceinline__ void pf_consume(float4v (&acc)[HW][8], float (&m)[HW]
     }
     l[hh] += lsum;
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const half8 b = __builtin_bit_cast(half8, __builtin_shufflevector(bv[0][nb], bv[1][nb], 0, 1, 2, 3, 4, 5, 6, 7));
-      acc[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b, acc[hh][nb], 0, 0, 0);
-      acc[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo, b, acc[hh][nb], 0, 0, 0);
+    for (int hf = 0; hf < NH; ++hf) {
+      if constexpr (NH == 2) {  // one query head per wave (hh == 0)
+        if (hf == 1) {
+          __builtin_amdgcn_sched_barrier(0);  // after the first half's products
+          read_v_half(1);
+        }
+        wait_v();
+      }
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const half8 b = __builtin_bit_cast(half8, __builtin_shufflevector(bv[0][nb], bv[1][nb], 0, 1, 2, 3, 4, 5, 6, 7));
+        acc[hh][8 * hf + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b, acc[hh][8 * hf + nb], 0, 0, 0);
+        acc[hh][8 * hf + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo, b, acc[hh][8 * hf + nb], 0, 0, 0);
+      }
     }
   }
 }
@@ -2362,13 +2474,16 @@ __device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int i) {
 // Q8: Q8A pages (int8 codes and scales, pf_issue_q8): every wave converts the
 // codes it fetched into a double-buffered f16 pair slot before the batch's
 // barrier, so a batch still costs one barrier.
-template <int REP, bool Q8 = false>
-__global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(PrefillArgs a) {
-  constexpr int HW = PfShape<REP>::HW, WPQ = PfShape<REP>::WPQ, QT = PfShape<REP>::QT;
-  constexpr int RPW = Q8 ? kPfQ8Rpw : PfShape<REP>::RPW;  // vector-memory instructions per wave and pair
-  constexpr int kRingSlot = Q8 ? kPfQ8Slot : kPfSlot;
+// NH: 128-wide halves of the head (1 or 2).
+template <int REP, bool Q8 = false, int NH = 1>
+__global__ __launch_bounds__((kWave * PfShape<REP, NH>::NW)) void prefill_mfma_kernel(PrefillArgs a) {
+  using Sh = PfShape<REP, NH>;
+  constexpr int HW = Sh::HW, WPQ = Sh::WPQ, QT = Sh::QT;
+  constexpr int kPfBatch = Sh::kBatch, kPfDepth = Sh::kDepth, kSlot = kPfSlot<NH>;
+  constexpr int RPW = Q8 ? NH + 2 : Sh::RPW;  // vector-memory instructions per wave and pair
+  constexpr int kRingSlot = Q8 ? kPfQ8Slot<NH> : kSlot;
   __shared__ __attribute__((aligned(16))) uint8_t ring_[kPfDepth * kRingSlot];
-  __shared__ __attribute__((aligned(16))) uint8_t f16buf_[Q8 ? 2 * kPfBatch * kPfSlot : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t f16buf_[Q8 ? 2 * kPfBatch * kSlot : 16];
   const int lane = (int)(threadIdx.x & (kWave - 1)), w = (int)(threadIdx.x / kWave);
   const int g = lane >> 4, n = lane & 15;
 
@@ -2417,7 +2532,9 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
   const int qn = min(QT, ch.z - QT * tile);  // queries in this tile
   const int p_last = pos0 + qn - 1;
   int p0 = a.p_start ? a.p_start[s] : 0;
-  p0 = min(max(p0, 0), p_last);
+  // a start past the tile's last query leaves every query nothing to attend:
+  // no pages are read and the rows are written as zeros
+  p0 = min(max(p0, 0), p_last + 1);
   // a sliding window gives query P the start max(p0, P - window + 1); the
   // tile reads from its first query's start
   const int ta = a.window > 0 ? max(p0, pos0 - a.window + 1) : p0;
@@ -2460,15 +2577,17 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     return __builtin_amdgcn_readlane(btv, idx);
   };
 
-  // q of query n, head h0 + hh: dims 32j + 8g .. +7, loaded before the pages
-  float4v qraw[HW][8];
+  // q of query n, head h0 + hh: dims 128 hf + 32j + 8g .. +7 in qraw[hh][8 hf
+  // + 2j ..], loaded before the pages
+  float4v qraw[HW][8 * NH];
   {
     const int trow = qok ? tq + n : ch.w;
 #pragma unroll
     for (int hh = 0; hh < HW; ++hh) {
-      const float4v* qsrc = reinterpret_cast<const float4v*>(a.q + ((size_t)trow * a.n_heads + h0 + hh) * kD + 8 * g);
+      const float4v* qsrc =
+          reinterpret_cast<const float4v*>(a.q + ((size_t)trow * a.n_heads + h0 + hh) * (NH * kD) + 8 * g);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 4 * NH; ++j) {
         qraw[hh][2 * j] = qsrc[8 * j];
         qraw[hh][2 * j + 1] = qsrc[8 * j + 1];
       }
@@ -2476,9 +2595,9 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
   }
 
   PfLanes pl;
-  const uint32_t rs = (uint32_t)a.n_kv * kRowBytes;
+  const uint32_t rs = (uint32_t)a.n_kv * (NH * kRowBytes);
   const uint32_t page_bytes = kPage * rs;
-  const uint32_t kvh_off = (uint32_t)kvh * kRowBytes;
+  const uint32_t kvh_off = (uint32_t)kvh * (NH * kRowBytes);
   {
     const int j = w & 3;  // this wave's quarter of a page region
     const uint32_t R = 4u * (uint32_t)j + (uint32_t)g;
@@ -2502,9 +2621,9 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     const uint32_t bits = (ph0 < a.num_pages ? 1u : 0u) | (ph1 < a.num_pages ? 2u : 0u);
     vbits = (vbits & ~(3u << (2 * sl))) | (bits << (2 * sl));
     if constexpr (Q8)
-      pf_issue_q8(a, (uint32_t)a.n_kv * kD, (uint32_t)kvh, ring + sl * kRingSlot, ph0, ph1, w);
+      pf_issue_q8<NH>(a, (uint32_t)a.n_kv * (NH * kD), (uint32_t)kvh, ring + sl * kRingSlot, ph0, ph1, w);
     else
-      pf_issue<PfShape<REP>::RPW>(a, pl, page_bytes, kvh_off, ring + sl * kPfSlot, ph0, ph1, w);
+      pf_issue<Sh::RPW>(a, pl, page_bytes, kvh_off, ring + sl * kSlot, ph0, ph1, w);
   };
 #pragma unroll
   for (int i = 0; i < 2 * kPfBatch; ++i)
@@ -2512,13 +2631,13 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
 
   // q -> B operands: per query and head, scale by 2^-E (E from max |q *
   // scale|) so that hi and lo stay in f16 range; scores are scaled back by 2^E
-  half8 qh[HW][4], ql[HW][4];
+  half8 qh[HW][4 * NH], ql[HW][4 * NH];
   float qexp[HW];
 #pragma unroll
   for (int hh = 0; hh < HW; ++hh) {
     float amax = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 8; ++r)
+    for (int r = 0; r < 8 * NH; ++r)
 #pragma unroll
       for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(qraw[hh][r][e] * a.scale_log2));
     amax = max_xor16(max_xor32(amax));  // over the 4 lanes of query n
@@ -2527,7 +2646,7 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     const float inv = ldexpf(1.0f, -E);
     qexp[hh] = ldexpf(1.0f, E);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4 * NH; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float y = qok ? qraw[hh][2 * j + (e >> 2)][e & 3] * a.scale_log2 * inv : 0.0f;
@@ -2536,7 +2655,7 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
         ql[hh][j][e] = (_Float16)(y - (float)hi);
       }
   }
-  float4v acc[HW][8];
+  float4v acc[HW][8 * NH];
   float m[HW], l[HW];
   float vnorm = 0.0f;  // Q8: acc is in units of vnorm
 #pragma unroll
@@ -2544,7 +2663,7 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     m[hh] = kMInit;
     l[hh] = 0.0f;
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc[hh][nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int nb = 0; nb < 8 * NH; ++nb) acc[hh][nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
   // kPfBatch pairs per barrier: pairs [i0, i0 + B) are consumed while the
@@ -2565,11 +2684,11 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     // Q8: this wave's codes of the batch (its own DMAs, just waited for) to
     // f16 in the batch's buffer; the buffer was last read by the batch before
     // the previous one, which every wave finished before the last barrier
-    lds_u8* f16b = (lds_u8*)f16buf_ + ((i0 / kPfBatch) & 1) * (kPfBatch * kPfSlot);
+    lds_u8* f16b = (lds_u8*)f16buf_ + ((i0 / kPfBatch) & 1) * (kPfBatch * kSlot);
     if constexpr (Q8) {
 #pragma unroll
       for (int k = 0; k < kPfBatch; ++k)
-        if (i0 + k < npairs) pf_convert_q8(ring + ((i0 + k) % kPfDepth) * kRingSlot, f16b + k * kPfSlot, w);
+        if (i0 + k < npairs) pf_convert_q8<NH>(ring + ((i0 + k) % kPfDepth) * kRingSlot, f16b + k * kSlot, w);
     }
     pf_barrier();  // every wave's quarters of this batch landed; the previous batch is consumed
 #pragma unroll
@@ -2578,17 +2697,18 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
     for (int i = i0; i < min(i0 + kPfBatch, npairs); ++i) {
     if (active) {
       const int sl = i % kPfDepth;
-      lds_u8* sp = Q8 ? f16b + (i - i0) * kPfSlot : ring + sl * kPfSlot;
-      const lds_u8* sc = ring + sl * kRingSlot + kPfCodeSlot + w * kPfScaleWave;  // Q8: this wave's scales
+      lds_u8* sp = Q8 ? f16b + (i - i0) * kSlot : ring + sl * kSlot;
+      const lds_u8* sc = ring + sl * kRingSlot + kPfCodeSlot<NH> + w * kPfScaleWave;  // Q8: this wave's scales
       const bool v0 = (vbits >> (2 * sl)) & 1u, v1 = (vbits >> (2 * sl + 1)) & 1u;
       const int tok0 = (pg_first + 2 * i) * kPage;
       const bool whole = v0 && v1 && tok0 >= ta && tok0 + 2 * kPage <= tb;
-      if (whole && tok0 + 2 * kPage - 1 <= wq && tok0 >= wlo)
-        pf_consume<HW, 0, Q8>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n, sc, &vnorm);
+      // 256-wide heads: no mask-free copy (its register allocation spilled)
+      if (NH == 1 && whole && tok0 + 2 * kPage - 1 <= wq && tok0 >= wlo)
+        pf_consume<HW, 0, Q8, NH>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n, sc, &vnorm);
       else if (whole)
-        pf_consume<HW, 1, Q8>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n, sc, &vnorm);
+        pf_consume<HW, 1, Q8, NH>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n, sc, &vnorm);
       else
-        pf_consume<HW, 2, Q8>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n, sc, &vnorm);
+        pf_consume<HW, 2, Q8, NH>(acc, m, l, qh, ql, qexp, pl, sp, tok0, v0, v1, ta, tb, qpos, qlo, qok, g, n, sc, &vnorm);
     }
     }
   }
@@ -2604,39 +2724,59 @@ __global__ __launch_bounds__(kWave* PfShape<REP>::NW) void prefill_mfma_kernel(P
       const int qq = 4 * g + ii;
       if (qq < qn_w) {
         const float inv = L > 0.0f ? (Q8 ? vnorm : 1.0f) / L : 0.0f;
-        float* orow = a.out + ((size_t)(tq + qq) * a.n_heads + h0 + hh) * kD;
+        float* orow = a.out + ((size_t)(tq + qq) * a.n_heads + h0 + hh) * (NH * kD);
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) orow[16 * nb + n] = acc[hh][nb][ii] * inv;
+        for (int nb = 0; nb < 8 * NH; ++nb) orow[16 * nb + n] = acc[hh][nb][ii] * inv;
       }
     }
   }
 }
 
-template <int REP>
+template <int REP, int NH>
 void launch_prefill_rep(const PrefillArgs& a, int n_tiles, hipStream_t st) {
   const unsigned blocks = (unsigned)n_tiles * (unsigned)a.n_kv;
   if (a.k_scales)
-    prefill_mfma_kernel<REP, true><<<blocks, kWave * PfShape<REP>::NW, 0, st>>>(a);
+    prefill_mfma_kernel<REP, true, NH><<<blocks, kWave * PfShape<REP, NH>::NW, 0, st>>>(a);
   else
-    prefill_mfma_kernel<REP, false><<<blocks, kWave * PfShape<REP>::NW, 0, st>>>(a);
+    prefill_mfma_kernel<REP, false, NH><<<blocks, kWave * PfShape<REP, NH>::NW, 0, st>>>(a);
 }
-}  // namespace
 
-int prefill_queries_per_tile(int rep) {
+template <int NH>
+int prefill_qt(int rep) {
   switch (rep) {
-    case 1: return PfShape<1>::QT;
-    case 2: return PfShape<2>::QT;
-    case 4: return PfShape<4>::QT;
-    default: return PfShape<8>::QT;
+    case 1: return PfShape<1, NH>::QT;
+    case 2: return PfShape<2, NH>::QT;
+    case 4: return PfShape<4, NH>::QT;
+    default: return PfShape<8, NH>::QT;
   }
 }
 
-int launch_prefill_mfma(const PrefillArgs& a, int rep, int n_tiles, hipStream_t st) {
+template <int NH>
+void launch_prefill_nh(const PrefillArgs& a, int rep, int n_tiles, hipStream_t st) {
   switch (rep) {
-    case 1: launch_prefill_rep<1>(a, n_tiles, st); break;
-    case 2: launch_prefill_rep<2>(a, n_tiles, st); break;
-    case 4: launch_prefill_rep<4>(a, n_tiles, st); break;
-    case 8: launch_prefill_rep<8>(a, n_tiles, st); break;
+    case 1: launch_prefill_rep<1, NH>(a, n_tiles, st); break;
+    case 2: launch_prefill_rep<2, NH>(a, n_tiles, st); break;
+    case 4: launch_prefill_rep<4, NH>(a, n_tiles, st); break;
+    default: launch_prefill_rep<8, NH>(a, n_tiles, st); break;
+  }
+}
+}  // namespace
+
+int prefill_queries_per_tile(int rep, int head_dim) {
+  return head_dim == 256 ? prefill_qt<2>(rep) : prefill_qt<1>(rep);
+}
+
+int launch_prefill_mfma(const PrefillArgs& a, int rep, int head_dim, int n_tiles, hipStream_t st) {
+  switch (rep) {
+    case 1:
+    case 2:
+    case 4:
+    case 8:
+      if (head_dim == 256)
+        launch_prefill_nh<2>(a, rep, n_tiles, st);
+      else
+        launch_prefill_nh<1>(a, rep, n_tiles, st);
+      break;
     default: return fail(LNSKV_ERR_UNSUPPORTED, "n_heads/n_kv_heads = %d not supported (1, 2, 4, 8)", rep);
   }
   return hip_check("prefill kernel launch");

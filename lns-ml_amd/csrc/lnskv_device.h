@@ -416,14 +416,15 @@ template <bool FUSED>
 int launch_decode_mfma_wg(const DecodeArgs& a, int rep, int d, int n_seq, int n_wg, bool q8, hipStream_t st);
 int mfma_wg_count(int* n_wg);
 
-// Chunked prefill over f16 pages with head_dim 128 (lnskv_prefill_attention).
+// Chunked prefill over f16 or Q8A pages with head_dim 128 or 256
+// (lnskv_prefill_attention).
 struct PrefillArgs {
   const uint8_t* k_pages;
   const uint8_t* v_pages;
   const float* k_scales;   // Q8A pages: per (slot, kv head) scales; nullptr for f16
   const float* v_scales;
-  const float* q;          // [n_tok][n_heads][128]
-  float* out;              // [n_tok][n_heads][128]
+  const float* q;          // [n_tok][n_heads][head_dim]
+  float* out;              // [n_tok][n_heads][head_dim]
   const int4* chunks;      // [n_chunks]: {table row, first position, length, first token}
   const uint32_t* bt;      // [n_rows][bt_stride]
   const int32_t* p_start;  // [n_rows] window starts, or nullptr (0)
@@ -438,8 +439,8 @@ struct PrefillArgs {
   float scale_log2;
 };
 // Queries per tile of the prefill kernel (a workgroup per tile and kv head).
-int prefill_queries_per_tile(int rep);
-int launch_prefill_mfma(const PrefillArgs& a, int rep, int n_tiles, hipStream_t st);
+int prefill_queries_per_tile(int rep, int head_dim);
+int launch_prefill_mfma(const PrefillArgs& a, int rep, int head_dim, int n_tiles, hipStream_t st);
 
 int hip_check(const char* what);
 // A device buffer the library keeps per device: 0 the decode workspace, 1

@@ -1049,8 +1049,8 @@ int lnskv_prefill_attention(const lnskv_pages* c, const float* q, float* out, co
     return fail(LNSKV_ERR_INVALID, "n_heads %d is not a multiple of n_kv_heads %u", n_heads, c->n_kv_heads);
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(LNSKV_ERR_INVALID, "scale must be positive and finite");
   if (window < 0) return fail(LNSKV_ERR_INVALID, "window %d is negative", window);
-  if ((c->dtype != LNSKV_DTYPE_F16 && c->dtype != LNSKV_DTYPE_Q8A) || c->head_dim != 128)
-    return fail(LNSKV_ERR_UNSUPPORTED, "prefill attention is built for f16 and Q8A pages with head_dim 128");
+  if ((c->dtype != LNSKV_DTYPE_F16 && c->dtype != LNSKV_DTYPE_Q8A) || (c->head_dim != 128 && c->head_dim != 256))
+    return fail(LNSKV_ERR_UNSUPPORTED, "prefill attention is built for f16 and Q8A pages with head_dim 128 or 256");
   if (!aligned16(chunks) || !aligned16(q)) return fail(LNSKV_ERR_INVALID, "chunks and q must be 16-byte aligned");
   // the Q8A kernel addresses each scale array with 32-bit byte offsets
   if (c->dtype == LNSKV_DTYPE_Q8A && (uint64_t)c->num_pages * kPage * c->n_kv_heads * sizeof(float) > 0x7FFFFFF0u)
@@ -1078,10 +1078,10 @@ int lnskv_prefill_attention(const lnskv_pages* c, const float* q, float* out, co
   // at most one partly filled tile per chunk beyond n_tok / qt full ones;
   // blocks past the chunks' real tile count leave at once
   const int rep = n_heads / (int)c->n_kv_heads;
-  const int64_t qt = prefill_queries_per_tile(rep);
+  const int64_t qt = prefill_queries_per_tile(rep, (int)c->head_dim);
   const int64_t tiles = ((int64_t)n_tok + qt - 1) / qt + n_chunks;
   if (tiles * c->n_kv_heads > INT32_MAX) return fail(LNSKV_ERR_INVALID, "too many query tiles");
-  return launch_prefill_mfma(a, rep, (int)tiles, (hipStream_t)stream);
+  return launch_prefill_mfma(a, rep, (int)c->head_dim, (int)tiles, (hipStream_t)stream);
 }
 
 int lnskv_split_gated_query(const float* input, float* q_out, float* gate_out, int32_t n_rows, int32_t n_heads,

@@ -86,7 +86,7 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert rc == _lib.ERR_INVALID and "gate" in msg
     rc, _ = _status(lib.lnskv_split_gated_query, 1, 1, 1, 0, 4, 64, None)
     assert rc == _lib.ERR_INVALID
-    # chunked prefill: head_dim 128 only; Q8A scale arrays must stay under 2 GiB
+    # chunked prefill: head_dim 128 or 256 only; Q8A scale arrays must stay under 2 GiB
     # (num_pages * 16 * n_kv * 4 bytes: 2^22 pages x 8 kv heads is exactly 2 GiB)
     for pages, dt, d, want, text in ((64, _lib.DTYPE_F16, 64, _lib.ERR_UNSUPPORTED, "head_dim"),
                                      (1 << 22, _lib.DTYPE_Q8A, 128, _lib.ERR_UNSUPPORTED, "2 GiB"),

@@ -2,8 +2,10 @@
 float64 oracle run token by token: query t of a chunk must equal the decode
 of that token alone with kv_len = pos(t) + 1 (what the reference's
 token-at-a-time forward computes), within the page type's tolerance (1e-3
-relative per row for f16 pages, 1e-5 for Q8A pages).  f16 and Q8A pages.  Covers head ratios 1/2/4/8, a chunk with no earlier context, a
-single-token chunk, ragged tile ends, a sliding window, a missing page, a
+relative per row for f16 pages, 1e-5 for Q8A pages).  f16 and Q8A pages,
+head_dim 128 and 256.  Covers head ratios 1/2/4/8, a chunk with no earlier context, a
+single-token chunk, a chunk whose row start lies past all its queries (whole
+tiles with nothing to attend), ragged tile ends, a sliding window, a missing page, a
 chunk naming a table row outside the tables (skipped: its rows untouched),
 chunks out of sequence order, and two 128-token chunks over ~1500-token
 contexts (full pages)."""
@@ -20,10 +22,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(gpu, rep, chunks, ctx_pages, p_start=None, missing=(), n_kv=2, seed=0, extra_rows=0, window=0,
-         dtype=DTYPE_F16):
+         dtype=DTYPE_F16, d=128):
     """chunks: list of (table row, first position, length); tokens laid out in list order.
     window > 0: every token's reference start is max(p_start, kv_p_start(pos, window))."""
-    d = 128
     rng = np.random.default_rng(seed)
     n_rows = len(ctx_pages)
     num_pages = sum(ctx_pages) + 8
@@ -70,7 +71,7 @@ def _run(gpu, rep, chunks, ctx_pages, p_start=None, missing=(), n_kv=2, seed=0, 
                        scale)
     got = out.cpu().numpy()
     err = rel_err(got[idx], ref)
-    say("prefill", DTYPE_NAMES[dtype], "rep", rep, "tokens", len(idx), "max rel err", float(err.max()))
+    say("prefill", DTYPE_NAMES[dtype], "d", d, "rep", rep, "tokens", len(idx), "max rel err", float(err.max()))
     assert err.max() < TOL[dtype]
     untouched = np.setdiff1d(np.arange(n_tok), idx)
     assert np.all(got[untouched] == 7.0)
@@ -79,23 +80,34 @@ def _run(gpu, rep, chunks, ctx_pages, p_start=None, missing=(), n_kv=2, seed=0, 
 DTYPES = [DTYPE_F16, DTYPE_Q8A]
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rep", [1, 2, 4, 8])
-def test_prefill_small_cases(gpu, rep, dtype):
+def test_prefill_small_cases(gpu, rep, dtype, d):
     chunks = [(1, 1000, 16),   # a whole tile at a long context, with a missing page in its window
               (0, 0, 37),      # no earlier context; 3 tiles, the last ragged
               (2, 15, 1),      # a single token at the end of page 0
               (3, 300, 100),   # windowed: attends [200, pos]
+              (4, 100, 80),    # row start 400, past every query: nothing attended (zero rows)
               (9, 5, 4)]       # table row outside the tables: skipped
-    ctx_pages = [3, 64, 1, 26]
-    _run(gpu, rep, chunks, ctx_pages, p_start=[0, 0, 0, 200], missing=[(1, 20)], seed=rep, extra_rows=4,
-         dtype=dtype)
+    ctx_pages = [3, 64, 1, 26, 12]
+    _run(gpu, rep, chunks, ctx_pages, p_start=[0, 0, 0, 200, 400], missing=[(1, 20)], seed=rep, extra_rows=4,
+         dtype=dtype, d=d)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_prefill_long_chunks(gpu, dtype):
     chunks = [(0, 1400, 128), (1, 1600, 128)]
     _run(gpu, 4, chunks, [(1400 + 128 + 15) // 16, (1600 + 128 + 15) // 16], n_kv=8, seed=11, dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_prefill_long_chunks_d256(gpu, dtype):
+    """lns-ml's Qwen3.5 full-attention shape (16 query heads over 4 kv heads of
+    256): two 128-token chunks over ~1500-token contexts."""
+    chunks = [(0, 1400, 128), (1, 1600, 128)]
+    _run(gpu, 4, chunks, [(1400 + 128 + 15) // 16, (1600 + 128 + 15) // 16], n_kv=4, seed=12, dtype=dtype,
+         d=256)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -117,9 +129,10 @@ def test_prefill_many_chunks(gpu, dtype):
         _run(gpu, rep, chunks, ctx_pages, seed=20 + rep, dtype=dtype)
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rep", [2, 4, 8])
-def test_prefill_sliding_window(gpu, rep, dtype):
+def test_prefill_sliding_window(gpu, rep, dtype, d):
     """A sliding-window layer: each prompt token attends its own window
     [pos - w + 1, pos] (the reference's per-token kv_p_start), checked token by
     token against the oracle.  Chunks that cross the window (longer than it,
@@ -132,4 +145,4 @@ def test_prefill_sliding_window(gpu, rep, dtype):
     ctx_pages = [13, 53, 7, 35]
     for w in (100, 1, 16, 33):
         _run(gpu, rep, chunks, ctx_pages, p_start=[0, 0, 0, 520], missing=[(1, 44)], seed=30 + rep + w,
-             window=w, dtype=dtype)
+             window=w, dtype=dtype, d=d)
