@@ -72,6 +72,9 @@ def parse():
                    help="run only the plain copy (the calibration kernel for HBM byte counters)")
     p.add_argument("--reference-call-only", action="store_true",
                    help="run only the reference's one-sequence call (lnskv_attention_paged, Q8A, pos 4095)")
+    p.add_argument("--qwen35-only", action="store_true",
+                   help="run only lns-ml's Qwen3.5 attention shape (Hq16/Hkv4/d256, Q8A, RoPE 64, gated), with "
+                        "--prefill-reps chunked-prefill launches")
     return p.parse_args()
 
 
@@ -767,6 +770,10 @@ def main():
         return
     if args.reference_call_only:
         print(json.dumps({"reference_call_b1_q8a": reference_call_measure(dev)}), flush=True)
+        return
+    if args.qwen35_only:
+        print(json.dumps({"qwen35_shape": qwen35_measure(dev, min(args.steps, 100), pattern_reps=args.pattern_reps,
+                                                         prefill_reps=args.prefill_reps)}), flush=True)
         return
     if args.kv_dtype != "config":
         if args.config != "c2":

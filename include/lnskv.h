@@ -121,15 +121,16 @@ int lnskv_append(const lnskv_pages* c, const float* k_new_dev, const float* v_ne
  *   range: its output row is zero and the fused variants store nothing for
  *   it (as lnskv_append skips tokens outside the table).
  *   split_tokens: tokens per split-K partition (multiple of 16), or 0 to let
- *   the library schedule.  f16 and Q8A pages with head_dim 128 and at most
- *   4096 sequences then run one of two schedules, each giving every
+ *   the library schedule.  f16 and Q8A pages with head_dim 128 or 256 and at
+ *   most 4096 sequences then run one of two schedules, each giving every
  *   workgroup an equal share of all the batch's pages: a small batch (at most
  *   16 pages per compute unit, bounded from max_kv_len) one kernel whose
  *   workgroups merge the pieces they share; a larger one stream-K (one wave
  *   per resident slot, then a merge kernel).  The environment variable
  *   LNSKV_DECODE_SCHEDULE=stream-k or =workgroup forces one of the two (the
- *   workspace query must see the same setting).  Other shapes run split-K
- *   with a partition size chosen from the batch.
+ *   workspace query must see the same setting).  Q8A batches of more than
+ *   4096 sequences run stream-K in launches of 4096 sequences.  Other shapes
+ *   run split-K with a partition size chosen from the batch.
  *   workspace_dev/ws_bytes: 16-byte aligned device scratch of at least
  *   lnskv_decode_workspace_size(...) bytes (same n_seq, n_heads, max_kv_len
  *   and split_tokens, same current device), or NULL/0 to use a buffer the

@@ -382,8 +382,8 @@ bool mfma_path(int dtype, int d, int rep) {
 }
 
 // Q8A pages with head_dim 128 or 256 also run on the matrix cores, on the
-// stream-K and workgroup schedules only (split_tokens = 0, at most
-// kSkMaxSeqs sequences).
+// stream-K and workgroup schedules only (split_tokens = 0; stream-K in
+// launches of at most kSkMaxSeqs sequences).
 bool mfma_q8_path(int dtype, int d, int rep) {
   return dtype == LNSKV_DTYPE_Q8A && (d == 128 || d == 256) && (rep == 1 || rep == 2 || rep == 4 || rep == 8) &&
          !force_valu();
@@ -423,7 +423,8 @@ __global__ __launch_bounds__(kBlock) void split_gated_query_vec_kernel(const flo
 
 // How one decode call runs, when the caller leaves the split to the library,
 // the MFMA kernel serves the pages and there are at most kSkMaxSeqs
-// sequences: a small batch (at most kWgSmallPages units per workgroup) runs
+// sequences (Q8A pages: any number, stream-K in launches of kSkMaxSeqs): a
+// small batch (at most kWgSmallPages units per workgroup) runs
 // the workgroup schedule, one kernel whose workgroups merge what they share;
 // a larger one stream-K (one wave per resident slot, each taking an equal
 // share of all pages, then a merge kernel), which measured faster there.
@@ -456,13 +457,16 @@ int plan_decode(const lnskv_pages* c, int n_seq, int n_heads, int max_kv_len, in
   *p = DecodePlan{};
   const int64_t units = (int64_t)n_seq * n_kv * ((int64_t)max_kv_len / kPage + 1);
   const bool q8 = mfma_q8_path((int)c->dtype, d, rep);
-  if (split_tokens == 0 && (mfma_path((int)c->dtype, d, rep) || q8) && n_seq <= kSkMaxSeqs &&
+  // Q8A batches of more than kSkMaxSeqs sequences run stream-K in launches of
+  // at most kSkMaxSeqs sequences each (the Q8A pages have no split-K matrix
+  // kernel); f16 batches that large take the split-K matrix kernel
+  if (split_tokens == 0 && (mfma_path((int)c->dtype, d, rep) || q8) && (n_seq <= kSkMaxSeqs || q8) &&
       units < ((int64_t)1 << 30)) {
     int n_wg = 0;
     if (int rc = mfma_wg_count(&n_wg)) return rc;
     const int setting = schedule_setting();
-    if (setting == kScheduleWorkgroup ||
-        (setting == kScheduleAuto && units <= (int64_t)kWgSmallPages * n_wg)) {
+    if (n_seq <= kSkMaxSeqs &&
+        (setting == kScheduleWorkgroup || (setting == kScheduleAuto && units <= (int64_t)kWgSmallPages * n_wg))) {
       // a small batch: the workgroup schedule (one kernel); the header, then
       // 2 * rep partial rows of (acc[d], m, l) per workgroup
       p->wg = n_wg;
@@ -738,8 +742,25 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
     a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeaderBytes);
     a.ws_ml = a.ws_acc + (size_t)n_waves * 2 * rep * c->head_dim;
     a.sk_desc = reinterpret_cast<int4*>(a.ws_ml + (size_t)n_waves * 2 * rep * 2);
-    return launch_decode_mfma_sk<FUSED>(a, rep, d, n_seq, n_waves, c->dtype == LNSKV_DTYPE_Q8A,
-                                        (hipStream_t)stream);
+    // sequences [s0, s0 + ns) per launch; the launches share the workspace in
+    // stream order (each combine has read it before the next decode writes)
+    for (int s0 = 0; s0 < n_seq; s0 += kSkMaxSeqs) {
+      const int ns = std::min(n_seq - s0, kSkMaxSeqs);
+      DecodeArgs b = a;
+      const size_t qo = (size_t)s0 * n_heads * d, ko = (size_t)s0 * c->n_kv_heads * d;
+      b.q = a.q + qo;
+      b.out = a.out + qo;
+      b.gate = a.gate ? a.gate + qo : nullptr;
+      b.k_new = a.k_new ? a.k_new + ko : nullptr;
+      b.v_new = a.v_new ? a.v_new + ko : nullptr;
+      b.bt = a.bt + (size_t)s0 * bt_stride;
+      b.kv_len = a.kv_len ? a.kv_len + s0 : nullptr;
+      b.p_start = a.p_start ? a.p_start + s0 : nullptr;
+      if (int rc = launch_decode_mfma_sk<FUSED>(b, rep, d, ns, n_waves, c->dtype == LNSKV_DTYPE_Q8A,
+                                                (hipStream_t)stream))
+        return rc;
+    }
+    return LNSKV_OK;
   }
   if (need > 0) {
     a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeaderBytes);

@@ -357,13 +357,14 @@ def test_stream_k_caller_workspace_and_fallback(gpu, monkeypatch, schedule):
 
 @pytest.mark.parametrize("schedule", SCHEDULES)
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_Q8A])
-@pytest.mark.parametrize("n_seq", [130, 4096])
+@pytest.mark.parametrize("n_seq", [130, 4096, 9000])
 def test_stream_k_many_sequences(gpu, monkeypatch, n_seq, dtype, schedule):
     """More than 64 sequences on both schedules (groups of 64, one lane per
     sequence): a whole group of empty sequences, ragged lengths and windows,
     unfused and fused, against the f64 oracle; f16 and Q8A pages (the Q8A
     fused call quantizes each new token in the wave that holds it; pages and
-    scales bit-exact)."""
+    scales bit-exact).  9000 sequences: Q8A pages run stream-K in three
+    launches of at most 4096 sequences, f16 pages split-K."""
     monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", schedule)
     say(schedule, "n_seq", n_seq, DTYPE_NAMES[dtype])
     n_kv, d, rep = 8, 128, 4
