@@ -1861,6 +1861,15 @@ constexpr int kSkWavesPerCu = 4;
 // pages in flight, 51.0-51.4 with two waves and three, against 49.5 here.
 constexpr int kSkDepthQ8 = 2;
 constexpr int kSkWavesPerCuQ8 = 8;
+// 256-wide heads (one wave per SIMD on either page type): also two pages
+// in flight; at the Qwen3.5 shape three and four measured 57.8 and 61.6 us
+// per Q8A step (RoPE, gated) against 53.0, and 73.0 and 73.3 per f16 step
+// against 70.4-72.1.
+constexpr int kSkDepthWide = 2;
+template <bool Q8, int NH>
+constexpr int sk_depth() {
+  return NH == 2 ? kSkDepthWide : (Q8 ? kSkDepthQ8 : kSkDepth);
+}
 
 // Resident waves of one stream-K kernel (ROPE: the fused variant that turns
 // RoPE in registers, whose extra registers may fit fewer waves), capped at
@@ -1868,7 +1877,7 @@ constexpr int kSkWavesPerCuQ8 = 8;
 template <int REP, bool FUSED, bool Q8, int NH, bool ROPE>
 int sk_waves_of(int cus, int* waves) {
   int per_cu = 0;
-  constexpr int depth = Q8 ? kSkDepthQ8 : kSkDepth;
+  constexpr int depth = sk_depth<Q8, NH>();
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sk_kernel<REP, FUSED, depth, ROPE, Q8, NH>, kWave,
                                                    0) != hipSuccess)
     per_cu = 0;
@@ -1880,14 +1889,15 @@ int sk_waves_of(int cus, int* waves) {
 template <int REP, bool FUSED, int NH>
 void launch_sk_rep(const DecodeArgs& a, int n_seq, int n_waves, bool q8, hipStream_t st) {
   const bool rope = FUSED && a.rope_half > 0;
+  constexpr int dq = sk_depth<true, NH>(), df = sk_depth<false, NH>();
   if (q8 && rope)
-    decode_sk_kernel<REP, FUSED, kSkDepthQ8, FUSED, true, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+    decode_sk_kernel<REP, FUSED, dq, FUSED, true, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
   else if (q8)
-    decode_sk_kernel<REP, FUSED, kSkDepthQ8, false, true, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+    decode_sk_kernel<REP, FUSED, dq, false, true, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
   else if (rope)
-    decode_sk_kernel<REP, FUSED, kSkDepth, FUSED, false, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+    decode_sk_kernel<REP, FUSED, df, FUSED, false, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
   else
-    decode_sk_kernel<REP, FUSED, kSkDepth, false, false, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
+    decode_sk_kernel<REP, FUSED, df, false, false, NH><<<n_waves, kWave, 0, st>>>(a, n_seq, n_waves);
   combine_sk_kernel<REP, FUSED, NH><<<n_waves, kBlock, 0, st>>>(a, n_seq, n_waves);
 }
 }  // namespace
