@@ -1703,7 +1703,10 @@ void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg) {
   // the HP parts of head h through LDS, in part order.
   constexpr int HP = NW >= REP ? NW / REP : 1;  // parts per head
   constexpr int HW = NW >= REP ? 1 : REP / NW;  // heads per wave
-  constexpr int kChunk = 32 / NH;               // rows in flight (registers: kChunk x (2 + CL))
+  // rows in flight (registers: kChunk x (2 + CL), 128 at NH = 1 and 192 at
+  // NH = 2, whose one wave per SIMD has 512): one round for 32 workgroups at
+  // either head width
+  constexpr int kChunk = 32;
   lds_f32* prow = (lds_f32*)part_;  // free again: row v of wave v, acc then m, l
 #pragma unroll
   for (int side = 0; side < 2; ++side) {
