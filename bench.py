@@ -639,6 +639,83 @@ def reference_call_measure(dev, calls: int = 400, n_layers: int = 32) -> dict:
                     "same calls replayed from one captured graph, the GPU's own time per call"}
 
 
+def token_loop_measure(dev, tokens: int = 64, reps: int = 12) -> dict:
+    """The reference engine's per-token work for one full-attention layer
+    (engine.rs:1600-1604 then the attention at :3405): lnskv_step_pages, the
+    block table to the device, lnskv_attention_paged -- one sequence,
+    Hq32/Hkv8/d128 Q8A pages, positions 4064 .. 4064 + tokens - 1 (a new page
+    every 16).  Two ways to move the table: the whole row every token
+    (lnskv_block_tables_upload, upload_block_table's copy) and only the changed
+    entries (lnskv_block_tables_sync: nothing on 15 of 16 tokens, a by-value
+    patch when a page is mapped).  Per token: wall time of the host loop and
+    HIP-event time on the stream."""
+    import ctypes as C
+
+    import torch
+
+    from lnskv import DTYPE_Q8A
+    from lnskv._lib import lib
+    from lnskv.device import PagedKV
+    from lnskv.host import BlockTables, PagePool
+
+    pos0, hq, hkv, d, max_pages = 4064, 32, 8, 128, 512
+    n_pages = (pos0 + tokens) // 16 + 8
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    pk = PagedKV(n_pages, hkv, d, DTYPE_Q8A, dev)
+    for t in (pk.k, pk.v):
+        t.copy_(torch.randint(-127, 128, t.shape, generator=g, device=dev, dtype=torch.int8))
+    for t in (pk.ks, pk.vs):
+        t.copy_(torch.rand(t.shape, generator=g, device=dev) * 0.02 + 0.001)
+    q, k_in, v_in = (torch.randn(n, device=dev) for n in (hq * d, hkv * d, hkv * d))
+    out = torch.empty(hq * d, device=dev)
+    table_dev = torch.empty(max_pages, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    pool, bt = PagePool(n_pages), BlockTables(1, max_pages)
+    # the C ABI called directly with its arguments prepared once, as a native
+    # engine would (the Python wrappers' argument checks cost more host time
+    # than the GPU work being measured)
+    L = lib()
+    st = C.c_void_p(stream.cuda_stream)
+    args = [C.c_void_p(t.data_ptr()) for t in (q, k_in, v_in)]
+    tdev, odev, desc = C.c_void_p(table_dev.data_ptr()), C.c_void_p(out.data_ptr()), C.byref(pk.desc)
+    move = {"upload": L.lnskv_block_tables_upload, "sync": L.lnskv_block_tables_sync}
+    res = {}
+    for mode in ("upload", "sync"):
+        ev_sum, wall_sum, moved = 0.0, 0.0, 0
+        fn = move[mode]
+        for r in range(reps + 1):
+            bt.reset()
+            pool.reset()
+            for p in range(0, pos0, 16):
+                bt.ensure_kv_page(pool, 0, p)
+            bt.sync(table_dev.data_ptr(), stream.cuda_stream)
+            torch.cuda.synchronize()
+            moved += sum(1 for pos in range(pos0, pos0 + tokens) if pos % 16 == 0)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            a.record(stream)
+            for pos in range(pos0, pos0 + tokens):
+                if L.lnskv_step_pages(bt.handle, pool.handle, 0, 0, pos, 0) or fn(bt.handle, tdev, st) or \
+                        L.lnskv_attention_paged(*args, desc, tdev, odev, pos, d, hq, hkv, 0, st):
+                    raise RuntimeError(f"token loop failed at pos {pos}")
+            b.record(stream)
+            torch.cuda.synchronize()
+            if r > 0:  # the first round warms up
+                wall_sum += time.perf_counter() - t0
+                ev_sum += a.elapsed_time(b) / 1e3
+        res[mode] = {"us_per_token_wall": round(wall_sum / reps / tokens * 1e6, 2),
+                     "us_per_token_events": round(ev_sum / reps / tokens * 1e6, 2)}
+        if mode == "sync":
+            res[mode]["pages_mapped_per_token"] = round(moved / (reps + 1) / tokens, 3)
+    del pk
+    torch.cuda.empty_cache()
+    return {"shape": f"1 sequence, Hq32/Hkv8/d128, Q8A pages, positions {pos0}..{pos0 + tokens - 1}, one layer",
+            "table_upload_every_token": res["upload"], "table_sync_changed_entries": res["sync"],
+            "note": "per token: lnskv_step_pages (host) + the table to the device + lnskv_attention_paged, "
+                    "the C ABI called from a Python loop with prepared arguments"}
+
+
 def table_upload_measure(w, dev, reps: int = 200) -> dict:
     """upload_block_table's replacement timed on its own: lnskv_block_tables_upload
     of the configuration's [n_seq][stride] table from host memory (the
@@ -769,7 +846,8 @@ def main():
         print(json.dumps({"copy_ceiling": copy_ceiling(dev, args.copy_mb or 1024)}), flush=True)
         return
     if args.reference_call_only:
-        print(json.dumps({"reference_call_b1_q8a": reference_call_measure(dev)}), flush=True)
+        print(json.dumps({"reference_call_b1_q8a": reference_call_measure(dev),
+                          "reference_token_loop_b1_q8a": token_loop_measure(dev)}), flush=True)
         return
     if args.qwen35_only:
         print(json.dumps({"qwen35_shape": qwen35_measure(dev, min(args.steps, 100), pattern_reps=args.pattern_reps,
@@ -820,6 +898,7 @@ def main():
                   "c2_q8a_pages_rope": config_measure("c2", dev, args.steps, layers=args.layers, kv_dtype=2,
                                                       rope=True),
                   "reference_call_b1_q8a": reference_call_measure(dev),
+                  "reference_token_loop_b1_q8a": token_loop_measure(dev),
                   "qwen35_shape": qwen35_measure(dev, min(args.steps, 100), pattern_reps=args.pattern_reps,
                                                  prefill_reps=args.prefill_reps),
                   "block_table_upload": table_upload_measure(w, dev)}

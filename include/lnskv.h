@@ -489,6 +489,27 @@ int lnskv_fork_sequence(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t pa
  * so the host table may be changed as soon as the call returns. */
 int lnskv_block_tables_upload(const lnskv_block_tables* t, uint32_t* dst_dev,
                               lnskv_stream_t stream);
+/* upload_block_table for a device table that stays with its host table (the
+ * engine's kv_block_table_bufs[l], engine.rs:735-736, refreshed every token at
+ * engine.rs:1604 and 3233): writes only the entries that changed since the
+ * last lnskv_block_tables_sync of t.  The first call, and the first after
+ * lnskv_block_tables_reset, writes every entry.  A call with nothing changed
+ * (a decoding sequence gets a new page once every 16 tokens) enqueues
+ * nothing; up to LNSKV_TABLE_PATCH_MAX changed entries travel by value in the
+ * arguments of one small kernel; more, as one copy of the span holding them.
+ * dst_dev must be the device table the previous sync of t wrote, written by
+ * nothing else since.  Async on stream; the host table may change as soon as
+ * the call returns. */
+#define LNSKV_TABLE_PATCH_MAX 64
+int lnskv_block_tables_sync(lnskv_block_tables* t, uint32_t* dst_dev, lnskv_stream_t stream);
+/* Entries the next lnskv_block_tables_sync of t will write (host only). */
+int64_t lnskv_block_tables_changed(const lnskv_block_tables* t);
+/* The patch under lnskv_block_tables_sync, for callers that keep their own
+ * host tables: dst_dev[idx[j]] = val[j] for j < n, 1 <= n <=
+ * LNSKV_TABLE_PATCH_MAX, the pairs copied into the kernel's arguments before
+ * the call returns.  Async on stream. */
+int lnskv_block_table_patch(uint32_t* dst_dev, int32_t n, const uint32_t* idx, const uint32_t* val,
+                            lnskv_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Measurement (no counterpart in the reference)

@@ -204,11 +204,27 @@ struct lnskv_block_tables {
   int32_t max_pages;
   std::vector<uint32_t> table;  // [n_seq][max_pages]
   std::vector<int32_t> len;     // logical pages in use per row
+  // What lnskv_block_tables_sync still has to write: every entry (`all`), or
+  // the flat indices in `changed` (each once, flagged in `mark`).
+  bool all = true;
+  std::vector<uint32_t> changed;
+  std::vector<uint8_t> mark;
 };
 
 namespace {
 bool row_ok(const lnskv_block_tables* t, int32_t seq) {
   return t && seq >= 0 && seq < t->n_seq;
+}
+
+// Sets entry lp of row seq, noting it for the next sync when its value changes.
+void set_entry(lnskv_block_tables* t, int32_t seq, int32_t lp, uint32_t v) {
+  const size_t i = (size_t)seq * (size_t)t->max_pages + (size_t)lp;
+  if (t->table[i] == v) return;
+  t->table[i] = v;
+  if (!t->all && !t->mark[i]) {
+    t->mark[i] = 1;
+    t->changed.push_back((uint32_t)i);
+  }
 }
 }  // namespace
 
@@ -226,6 +242,7 @@ int lnskv_block_tables_create(int32_t n_seq, int32_t max_pages, lnskv_block_tabl
   try {
     t->table.assign((size_t)n_seq * (size_t)max_pages, LNSKV_NO_PAGE);
     t->len.assign((size_t)n_seq, 0);
+    t->mark.assign(t->table.size(), 0);
   } catch (...) {
     delete t;
     return fail(LNSKV_ERR_NOMEM, "block tables %d x %d: allocation failed", n_seq, max_pages);
@@ -248,6 +265,9 @@ void lnskv_block_tables_reset(lnskv_block_tables* t) {
   if (!t) return;
   std::fill(t->table.begin(), t->table.end(), LNSKV_NO_PAGE);
   std::fill(t->len.begin(), t->len.end(), 0);
+  for (uint32_t i : t->changed) t->mark[i] = 0;
+  t->changed.clear();
+  t->all = true;
 }
 
 int lnskv_ensure_kv_page(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t layer,
@@ -261,11 +281,11 @@ int lnskv_ensure_kv_page(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t l
   if (lp >= t->max_pages)
     return fail(LNSKV_ERR_INVALID, "position %d needs logical page %d; the table row holds %d",
                 pos, lp, t->max_pages);
-  while (len <= lp) row[len++] = LNSKV_NO_PAGE;
+  while (len <= lp) set_entry(t, seq, len++, LNSKV_NO_PAGE);
   uint32_t phys;
   if (lnskv_page_pool_alloc(pool, &phys) != LNSKV_OK)
     return fail(LNSKV_ERR_POOL_EXHAUSTED, "KV page pool exhausted at layer %d (pos=%d)", layer, pos);
-  row[lp] = phys;
+  set_entry(t, seq, lp, phys);
   return LNSKV_OK;
 }
 
@@ -284,7 +304,7 @@ int lnskv_evict_kv_pages(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t s
   for (int32_t lp = 0; lp < n; ++lp) {
     if (row[lp] != LNSKV_NO_PAGE) {
       if (int rc = lnskv_page_pool_free(pool, row[lp])) return rc;
-      row[lp] = LNSKV_NO_PAGE;
+      set_entry(t, seq, lp, LNSKV_NO_PAGE);
     }
   }
   return LNSKV_OK;
@@ -314,7 +334,7 @@ int lnskv_free_sequence(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t se
   for (int32_t lp = 0; lp < t->len[(size_t)seq]; ++lp) {
     if (row[lp] != LNSKV_NO_PAGE) {
       if (int rc = lnskv_page_pool_free(pool, row[lp])) return rc;
-      row[lp] = LNSKV_NO_PAGE;
+      set_entry(t, seq, lp, LNSKV_NO_PAGE);
     }
   }
   t->len[(size_t)seq] = 0;
@@ -348,10 +368,10 @@ int lnskv_fork_sequence(lnskv_block_tables* t, lnskv_page_pool* pool, int32_t pa
   }
   for (int32_t lp = 0; lp < n_shared; ++lp) {
     if (prow[lp] != LNSKV_NO_PAGE) lnskv_page_pool_retain(pool, prow[lp]);
-    crow[lp] = prow[lp];
+    set_entry(t, child, lp, prow[lp]);
   }
   if (partial_tail) {
-    crow[n_pages - 1] = fresh;
+    set_entry(t, child, n_pages - 1, fresh);
     *copy_src = prow[n_pages - 1];
     *copy_dst = fresh;
     *n_copy = 1;
@@ -367,6 +387,44 @@ int lnskv_block_tables_upload(const lnskv_block_tables* t, uint32_t* dst_dev, ln
                                 (hipStream_t)stream);
   if (e != hipSuccess) return fail(LNSKV_ERR_HIP, "block table upload: %s", hipGetErrorString(e));
   return LNSKV_OK;
+}
+
+int lnskv_block_tables_sync(lnskv_block_tables* t, uint32_t* dst_dev, lnskv_stream_t stream) {
+  if (!t || !dst_dev) return fail(LNSKV_ERR_INVALID, "table or destination is NULL");
+  const hipStream_t st = (hipStream_t)stream;
+  const size_t n = t->changed.size();
+  if (t->all) {
+    hipError_t e = hipMemcpyAsync(dst_dev, t->table.data(), t->table.size() * sizeof(uint32_t),
+                                  hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return fail(LNSKV_ERR_HIP, "block table upload: %s", hipGetErrorString(e));
+  } else if (n == 0) {
+    return LNSKV_OK;
+  } else if (n <= LNSKV_TABLE_PATCH_MAX) {
+    uint32_t val[LNSKV_TABLE_PATCH_MAX];
+    for (size_t j = 0; j < n; ++j) val[j] = t->table[t->changed[j]];
+    if (int rc = lnskv::table_patch(dst_dev, (int)n, t->changed.data(), val, stream)) return rc;
+  } else {
+    const auto mm = std::minmax_element(t->changed.begin(), t->changed.end());
+    const size_t lo = *mm.first, hi = *mm.second;
+    hipError_t e = hipMemcpyAsync(dst_dev + lo, t->table.data() + lo, (hi - lo + 1) * sizeof(uint32_t),
+                                  hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return fail(LNSKV_ERR_HIP, "block table upload: %s", hipGetErrorString(e));
+  }
+  for (uint32_t i : t->changed) t->mark[i] = 0;
+  t->changed.clear();
+  t->all = false;
+  return LNSKV_OK;
+}
+
+int lnskv_block_table_patch(uint32_t* dst_dev, int32_t n, const uint32_t* idx, const uint32_t* val,
+                            lnskv_stream_t stream) {
+  if (!dst_dev || !idx || !val) return fail(LNSKV_ERR_INVALID, "destination, indices and values must be non-null");
+  return lnskv::table_patch(dst_dev, n, idx, val, stream);
+}
+
+int64_t lnskv_block_tables_changed(const lnskv_block_tables* t) {
+  if (!t) return 0;
+  return t->all ? (int64_t)t->table.size() : (int64_t)t->changed.size();
 }
 
 // RoPE tables (engine.rs:826-833 and 139-195), host only.

@@ -32,5 +32,8 @@ uint32_t* ws_error_word(void* stream, bool allocate);
 // Reads and clears the word (after a stream synchronization): 1 if set.
 int take_ws_error();
 float f16_bits_to_f32(uint16_t h);
+// Writes val[j] to dst_dev[idx[j]] for j < n (n <= LNSKV_TABLE_PATCH_MAX) with
+// one small kernel whose arguments carry the pairs; async on stream.
+int table_patch(uint32_t* dst_dev, int n, const uint32_t* idx, const uint32_t* val, void* stream);
 
 }  // namespace lnskv

@@ -309,6 +309,20 @@ __global__ __launch_bounds__(kBlock) void zero_kernel(uint4* p, size_t n16) {
     p[i] = make_uint4(0, 0, 0, 0);
 }
 
+// The changed entries of a block table, by value: no staging copy of host
+// memory, only the kernel's arguments (4 + 8 * LNSKV_TABLE_PATCH_MAX bytes).
+struct TablePatch {
+  int32_t n;
+  uint32_t idx[LNSKV_TABLE_PATCH_MAX];
+  uint32_t val[LNSKV_TABLE_PATCH_MAX];
+};
+static_assert(LNSKV_TABLE_PATCH_MAX <= kWave, "one lane per changed entry");
+
+__global__ __launch_bounds__(kWave) void table_patch_kernel(uint32_t* dst, TablePatch p) {
+  const int i = (int)threadIdx.x;
+  if (i < p.n) dst[p.idx[i]] = p.val[i];
+}
+
 // ---------------------------------------------------------------------------
 // Host-side dispatch.
 template <int DT>
@@ -770,6 +784,19 @@ int decode_entry(const lnskv_pages* c, const float* q, const float* k_new, const
 }
 
 }  // namespace
+
+int table_patch(uint32_t* dst_dev, int n, const uint32_t* idx, const uint32_t* val, void* stream) {
+  if (n < 1 || n > LNSKV_TABLE_PATCH_MAX) return fail(LNSKV_ERR_INVALID, "table patch of %d entries", n);
+  TablePatch p{};
+  p.n = n;
+  for (int j = 0; j < n; ++j) {
+    p.idx[j] = idx[j];
+    p.val[j] = val[j];
+  }
+  table_patch_kernel<<<1, kWave, 0, (hipStream_t)stream>>>(dst_dev, p);
+  return hip_check("block table patch launch");
+}
+
 }  // namespace lnskv
 
 using namespace lnskv;

@@ -325,6 +325,9 @@ pub struct KvPaging {
     pub pool: PagePool,
     pub table: BlockTable,
     table_dev: DeviceBuffer<u32>,
+    // the entries the device table holds (what the last upload wrote); None
+    // until the first upload
+    on_device: Option<Vec<u32>>,
 }
 
 impl KvPaging {
@@ -336,6 +339,7 @@ impl KvPaging {
             pool: PagePool::new(capacity),
             table: BlockTable::new(max_pages),
             table_dev: DeviceBuffer::new(max_pages)?,
+            on_device: None,
         })
     }
 
@@ -351,9 +355,36 @@ impl KvPaging {
     /// the device table, ordered on `stream` after the work already queued
     /// there (a previous step's attention still reading the table finishes
     /// first); the host rows are staged before the call returns.
+    /// Only the entries that differ from what the device table holds are
+    /// written: none on most tokens (a new page comes every 16), up to
+    /// `LNSKV_TABLE_PATCH_MAX` by value through `lnskv_block_table_patch`
+    /// (no staging copy), the whole row otherwise.
     pub fn upload(&mut self, stream: HipStream) -> Result<(), String> {
-        let n = self.table.as_slice().len();
-        self.table_dev.copy_from_async(&self.table.as_slice()[..n], stream)
+        let now = self.table.as_slice();
+        if let Some(dev) = &self.on_device {
+            let mut idx: Vec<u32> = Vec::new();
+            let mut val: Vec<u32> = Vec::new();
+            for (i, &v) in now.iter().enumerate() {
+                if dev.get(i) != Some(&v) {
+                    idx.push(i as u32);
+                    val.push(v);
+                }
+            }
+            if idx.is_empty() {
+                return Ok(());
+            }
+            if idx.len() <= sys::LNSKV_TABLE_PATCH_MAX {
+                let dst = self.table_dev.as_mut_ptr();
+                check(unsafe {
+                    sys::lnskv_block_table_patch(dst, idx.len() as i32, idx.as_ptr(), val.as_ptr(), stream)
+                })?;
+                self.on_device = Some(now.to_vec());
+                return Ok(());
+            }
+        }
+        self.table_dev.copy_from_async(now, stream)?;
+        self.on_device = Some(now.to_vec());
+        Ok(())
     }
 
     /// The device table `attention_paged` reads.
@@ -365,6 +396,7 @@ impl KvPaging {
     pub fn reset(&mut self) {
         self.pool.reset();
         self.table = BlockTable::new(self.table.max_pages());
+        self.on_device = None;
     }
 }
 

@@ -21,6 +21,8 @@ pub const LNSKV_NOALLOC_SCRATCH_BYTES: usize = 24 << 20;
 /// `LNSKV_Q4L_DISK_BYTES` / `LNSKV_Q4L_DEVICE_BYTES`: one Q4_L super-block on disk / on the device.
 pub const LNSKV_Q4L_DISK_BYTES: usize = 134;
 pub const LNSKV_Q4L_DEVICE_BYTES: usize = 144;
+/// `LNSKV_TABLE_PATCH_MAX`: changed block-table entries one patch writes by value.
+pub const LNSKV_TABLE_PATCH_MAX: usize = 64;
 
 /// `lnskv_dtype`.
 pub const LNSKV_DTYPE_F32: i32 = 0;
@@ -387,6 +389,15 @@ extern "C" {
     pub fn lnskv_block_tables_upload(
         t: *const LnskvBlockTables,
         dst_dev: *mut u32,
+        stream: HipStream,
+    ) -> c_int;
+    pub fn lnskv_block_tables_sync(t: *mut LnskvBlockTables, dst_dev: *mut u32, stream: HipStream) -> c_int;
+    pub fn lnskv_block_tables_changed(t: *const LnskvBlockTables) -> i64;
+    pub fn lnskv_block_table_patch(
+        dst_dev: *mut u32,
+        n: i32,
+        idx: *const u32,
+        val: *const u32,
         stream: HipStream,
     ) -> c_int;
     pub fn lnskv_read_units(

@@ -26,6 +26,9 @@ ERR_HIP = -4
 ERR_UNSUPPORTED = -5
 ERR_WORKSPACE = -6
 
+# changed block-table entries that one lnskv_block_tables_sync writes by value
+TABLE_PATCH_MAX = 64
+
 # leading bytes of a decode workspace that must be zero before its first use
 # (the workgroup schedule's counters; every call leaves them zero)
 WORKSPACE_HEADER_BYTES = 4096
@@ -113,6 +116,9 @@ SIGNATURES = {
     "lnskv_fork_sequence": (
         C.c_int, [_vp, _vp, _i32, _i32, _i32, C.POINTER(_u32), C.POINTER(_u32), C.POINTER(_i32)]),
     "lnskv_block_tables_upload": (C.c_int, [_vp, _vp, _vp]),
+    "lnskv_block_tables_sync": (C.c_int, [_vp, _vp, _vp]),
+    "lnskv_block_tables_changed": (C.c_int64, [_vp]),
+    "lnskv_block_table_patch": (C.c_int, [_vp, _i32, _vp, _vp, _vp]),
     "lnskv_rope_dim": (_i32, [_i32, _f32]),
     "lnskv_rope_inv_freqs": (C.c_int, [_i32, _f32, _i32, _vp, _vp]),
     "lnskv_rope_append_workspace_size": (C.c_int, [_P, _R, _i32, C.POINTER(_sz)]),

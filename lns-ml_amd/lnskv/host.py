@@ -128,6 +128,14 @@ class BlockTables:
     def upload(self, dst_dev_ptr: int, stream: int = 0) -> None:
         check(lib().lnskv_block_tables_upload(self._h, C.c_void_p(dst_dev_ptr), C.c_void_p(stream)))
 
+    def sync(self, dst_dev_ptr: int, stream: int = 0) -> None:
+        """Write only the entries changed since the last sync to the same device table."""
+        check(lib().lnskv_block_tables_sync(self._h, C.c_void_p(dst_dev_ptr), C.c_void_p(stream)))
+
+    def changed(self) -> int:
+        """Entries the next sync writes (every entry before the first sync and after reset)."""
+        return int(lib().lnskv_block_tables_changed(self._h))
+
 
 def kv_p_start(pos: int, window: int) -> int:
     return lib().lnskv_kv_p_start(pos, window)

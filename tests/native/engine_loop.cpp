@@ -4,8 +4,10 @@
 // reference's paged type), a 40-token sliding window on a pool of
 // lnskv_window_pages(40) pages, so that pages are evicted and reused:
 //   per position pos: lnskv_step_pages (evict, then ensure: engine.rs:
-//   2960-2990 with the exhaustion fixed), lnskv_block_tables_upload
-//   (upload_block_table, engine.rs:2992-3005), lnskv_dispatch_attention_paged
+//   2960-2990 with the exhaustion fixed), lnskv_block_tables_sync
+//   (upload_block_table, engine.rs:2992-3005, writing only the entries that
+//   changed: a patch when a page is mapped or evicted, nothing on the other
+//   positions), lnskv_dispatch_attention_paged
 //   (dispatch_attention_paged_q8a, lns-metal/src/lib.rs:1046-1094) with
 //   p_start = lnskv_kv_p_start(pos, 40) (engine.rs:3007-3013), then the
 //   o_proj: lnskv_q4l_gemv_accumulate adds W_o attn_out to the residual x
@@ -181,7 +183,7 @@ int run() {
         !hip_ok(hipMemcpy(v_dev, v.data(), v.size() * 4, hipMemcpyHostToDevice), "v upload"))
       return 1;
     if (!ok(lnskv_step_pages(bt, pool, 0, 0, pos, kWindow), "lnskv_step_pages")) return 1;
-    if (!ok(lnskv_block_tables_upload(bt, table_dev, nullptr), "lnskv_block_tables_upload")) return 1;
+    if (!ok(lnskv_block_tables_sync(bt, table_dev, nullptr), "lnskv_block_tables_sync")) return 1;
     const int p_start = lnskv_kv_p_start(pos, kWindow);
     if (!ok(lnskv_dispatch_attention_paged(q_dev, k_dev, v_dev, &c, table_dev, out_dev, (uint32_t)pos, kD, kHq,
                                            kHkv, (uint32_t)p_start, nullptr),

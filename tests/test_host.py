@@ -207,3 +207,22 @@ def test_reset_clears_rows():
     bt.reset()
     pool.reset()
     assert (bt.array() == NO_PAGE).all() and bt.row_len(1) == 0 and pool.num_free == 8
+
+
+def test_sync_counts_every_entry_until_the_first_sync():
+    """lnskv_block_tables_changed before any sync (and after reset): the whole
+    table, whatever changed since; the sync itself needs a device and is
+    checked in test_gpu_ops.py."""
+    pool, bt = PagePool(16), BlockTables(3, 5)
+    assert bt.changed() == 15
+    bt.ensure_kv_page(pool, 1, 40)
+    assert bt.changed() == 15
+    bt.reset()
+    assert bt.changed() == 15
+    assert _lib.lib().lnskv_block_tables_changed(None) == 0
+    # the patch primitive refuses NULL pointers and counts outside [1, 64]
+    # before touching any device
+    idx = (C.c_uint32 * 65)()
+    val = (C.c_uint32 * 65)()
+    assert _lib.lib().lnskv_block_table_patch(None, 1, idx, val, None) == _lib.ERR_INVALID
+    assert _lib.lib().lnskv_block_tables_sync(None, None, None) == _lib.ERR_INVALID

@@ -16,8 +16,8 @@ CRATE = os.path.join(ROOT, "lns-ml_amd", "lns-kv-hip")
 
 STRUCTS = {"lnskv_pages": "LnskvPages", "lnskv_rope": "LnskvRope", "lnskv_page_pool": "LnskvPagePool",
            "lnskv_block_tables": "LnskvBlockTables"}
-SCALARS = {"int": "c_int", "int32_t": "i32", "uint32_t": "u32", "size_t": "usize", "float": "f32",
-           "void": "c_void", "char": "c_char"}
+SCALARS = {"int": "c_int", "int32_t": "i32", "int64_t": "i64", "uint32_t": "u32", "size_t": "usize",
+           "float": "f32", "void": "c_void", "char": "c_char"}
 
 
 def rust_type(c: str) -> str:
