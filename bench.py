@@ -741,8 +741,48 @@ def table_upload_measure(w, dev, reps: int = 200) -> dict:
     b.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / reps
-    return {"bytes": int(dst.numel() * 4), "us_per_upload_events": round(a.elapsed_time(b) * 1e3 / reps, 2),
+    nbytes = int(dst.numel() * 4)
+    # decode steps: every sequence appends one token (a page mapped when it
+    # crosses a page boundary), then the device table is brought up to date,
+    # by the whole upload or by the changed-entries sync; HIP events around
+    # that one call per step (the host's page bookkeeping is outside them)
+    lens = [int((w.tables[s] != 0xFFFFFFFF).sum()) * 16 for s in range(w.n_seq)]
+    stride = w.tables.shape[1] + (2 * reps + 16) // 16 + 2  # room for the appended tokens
+    bt = BlockTables(w.n_seq, stride)
+    pool = PagePool(w.num_pages)
+    for s in range(w.n_seq):
+        for p in range(0, lens[s], 16):
+            bt.ensure_kv_page(pool, s, p)
+    dst = torch.empty(w.n_seq * stride, dtype=torch.int32, device=dev)
+    per_step = {}
+    for mode in ("upload", "sync"):
+        fn = bt.upload if mode == "upload" else bt.sync
+        fn(dst.data_ptr(), stream.cuda_stream)
+        torch.cuda.synchronize()
+        total, moved, warm = 0.0, 0, 8  # the first steps (kernel loading) are not timed
+        for step in range(reps + warm):
+            for s in range(w.n_seq):
+                bt.ensure_kv_page(pool, s, lens[s] + (step if mode == "upload" else reps + warm + step))
+            if step >= warm:
+                moved += bt.changed() if mode == "sync" else 0
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn(dst.data_ptr(), stream.cuda_stream)
+            e1.record(stream)
+            e1.synchronize()
+            if step >= warm:
+                total += e0.elapsed_time(e1) * 1e3
+        per_step[mode] = round(total / reps, 2)
+        if mode == "sync":
+            per_step["entries_per_step"] = round(moved / reps, 2)
+    return {"bytes": nbytes, "us_per_upload_events": round(a.elapsed_time(b) * 1e3 / reps, 2),
             "us_per_upload_wall": round(wall * 1e6, 2),
+            "decode_steps": {"us_per_step_upload_events": per_step["upload"],
+                             "us_per_step_sync_events": per_step["sync"],
+                             "changed_entries_per_step": per_step["entries_per_step"],
+                             "note": f"{reps} steps of one token per sequence: the whole table "
+                                     "(lnskv_block_tables_upload) against the changed entries "
+                                     "(lnskv_block_tables_sync), HIP events around the one call"},
             "note": "hipMemcpyAsync from pageable host memory; the step's kernels are not in the timed region"}
 
 
