@@ -324,6 +324,7 @@ def test_stream_k_caller_workspace_and_fallback(gpu, monkeypatch, schedule):
     sequence leaves most waves idle.  The workspace is zeroed once and
     reused: every call leaves its counter header zero."""
     monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", schedule)
+    monkeypatch.delenv("LNSKV_FORCE_VALU", raising=False)  # the matrix-core schedules themselves
     say(schedule, "workspace / fallback")
     n_kv, d, rep = 8, 128, 4
     pk0 = PagedKV(16, n_kv, d, DTYPE_F16, gpu)
@@ -405,6 +406,7 @@ def test_schedule_chosen_by_batch_size(gpu, monkeypatch):
     for a batch of at most 16 pages per compute unit (the reference's
     one-sequence call: 4096 tokens, 8 kv heads) and stream-K for a larger one
     (64 such sequences): the workspace sizes match the forced settings'."""
+    monkeypatch.delenv("LNSKV_FORCE_VALU", raising=False)  # the matrix-core schedules themselves
     n_kv, d, rep = 8, 128, 4
     pk = PagedKV(16, n_kv, d, DTYPE_Q8A, gpu)
 

@@ -36,6 +36,7 @@ def _drain_report():
 
 def test_decode_poisoned_header_is_reported(gpu, monkeypatch):
     monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", "workgroup")
+    monkeypatch.delenv("LNSKV_FORCE_VALU", raising=False)  # the matrix-core schedule itself
     say("decode workgroup schedule, poisoned workspace header")
     n_kv, d, rep, L = 8, 128, 4, 4096
     rng = np.random.default_rng(5)
