@@ -623,6 +623,15 @@ def reference_call_measure(dev, calls: int = 400, n_layers: int = 32) -> dict:
     replays = max(calls // n_layers, 10)
     ev_graph, _ = timed_steps(lambda i: graph.replay(), stream, replays, 3)
     per_call_graph = ev_graph / n_layers
+    # the same call at contexts whose page count per kv head (254, 257, 258)
+    # is not a multiple of the workgroups' share of pages
+    table_all = torch.from_numpy(np.random.default_rng(1).permutation(npg + 8).astype(np.int32)).to(dev)
+    by_pos = {}
+    for p in (4063, 4096, 4127):
+        ev_p, _ = timed_steps(lambda i, p=p: layers[i % n_layers].attention_paged(q, k_in, v_in, table_all, p, hq,
+                                                                                  out=out),
+                              stream, calls, 2 * n_layers)
+        by_pos[str(p)] = round(ev_p * 1e6, 2)
     nbytes = (pos + 1) * 2 * hkv * (d + 4) + 2 * hkv * d * 4 + 2 * hq * d * 4 + npg * 4
     del graph, layers
     torch.cuda.empty_cache()
@@ -630,6 +639,7 @@ def reference_call_measure(dev, calls: int = 400, n_layers: int = 32) -> dict:
             "us_per_call_events": round(ev * 1e6, 2), "us_per_call_median": dist["median"],
             "us_per_call_wall": round(wall * 1e6, 2),
             "us_per_call_graph_replay": round(per_call_graph * 1e6, 2),
+            "us_per_call_events_at_pos": by_pos,
             "host_launch_share": round(max(0.0, 1.0 - per_call_graph / wall), 3),
             "bytes_per_call": int(nbytes),
             "gb_per_s": round(nbytes / ev / 1e9, 1),

@@ -1303,6 +1303,22 @@ __device__ __forceinline__ SkSeq sk_fields(const DecodeArgs& a, int s, int n_seq
   return q;
 }
 
+// Three inclusive scans over the wave's lanes, their steps interleaved.
+__device__ __forceinline__ void wave_incl_scan3(int& x, int& y, int& z) {
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int xs = __shfl_up(x, d, kWave);
+    const int ys = __shfl_up(y, d, kWave);
+    const int zs = __shfl_up(z, d, kWave);
+    if (lane >= d) {
+      x += xs;
+      y += ys;
+      z += zs;
+    }
+  }
+}
+
 __device__ __forceinline__ int wave_incl_scan(int x) {
   const int lane = (int)(threadIdx.x & (kWave - 1));
 #pragma unroll
@@ -1465,9 +1481,13 @@ __global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_
 // ---------------------------------------------------------------------------
 // Workgroup schedule (small batches): G workgroups of NW waves (two per CU
 // at most; only as many as the batch can fill).  The units (sequence,
-// kv head, page) are ordered as for stream-K; workgroup g of G takes units
-// [A, B) = [g C, g C + C) with C = max(NW kWgMinPages, ceil(T / G)), and its
-// waves split that range equally (wave i: [A + i Cw, A + (i + 1) Cw)).  Each
+// kv head, page) are ordered as for stream-K.  When the batch is at most 64
+// sequences and the grid holds it, each (sequence, kv head) segment gets
+// workgroups of its own that split its pages evenly (segment-aligned
+// ranges; the reference's one-sequence call always runs so); otherwise
+// workgroup g of G takes units [A, B) = [g C, g C + C) with C = max(NW
+// kWgMinPages, ceil(T / G)).  The waves split [A, B) equally (wave i:
+// [A + i Cw, A + (i + 1) Cw)).  Each
 // wave runs its pieces exactly as stream-K does, except that a piece that is
 // not a whole segment leaves its partial rows in LDS (slot 0 for the wave's
 // first piece, slot 1 for its last).  After a barrier the workgroup merges,
@@ -1525,7 +1545,7 @@ template <int REP, bool FUSED, int DEPTH, bool ROPE, bool Q8, int NW, int NH = 1
 // registers, so it keeps its registers and the occupancy they allow.)
 __global__ __launch_bounds__(kWave* NW)
 __attribute__((amdgpu_waves_per_eu(Q8 && NH == 1 && !(ROPE && REP == 8) ? 2 : 1)))
-void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg) {
+void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg, int n_cu) {
   static_assert(2 * REP <= 16, "hi and lo columns must fit one 16-wide MFMA tile");
   constexpr int kSlots = Q8 ? 1 : DEPTH;
   constexpr int D = NH * kD;                    // head dim
@@ -1545,19 +1565,66 @@ void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg) {
 
   // the layout (every wave computes it)
   const int n_groups = (n_seq + kWave - 1) / kWave;
+  // Segment-aligned ranges when the batch is one group and the grid holds
+  // them: segment (s, h) gets kseg[s] workgroups of its own, which split its
+  // pages evenly, so no workgroup or wave holds the end of one segment and
+  // the start of the next (two pieces in a row on one wave, two merges on one
+  // workgroup).  kseg = ceil(np / S) (S = NW kWgMinPages, the fewest units
+  // of a workgroup) while those workgroups have a CU each, else
+  // max(1, floor(np / S)): a wave with one more page costs less than two
+  // workgroups on one CU.  Otherwise workgroup g takes [g C, g C + C).
+  constexpr int kMinShare = NW * kWgMinPages;
   int total = 0, gb = 0, g = 0;
+  int kseg = 0, kincl = 0;
+  bool aligned = false;
   SkSeq q;
   if (n_groups == 1) {
-    q = sk_group<FUSED>(a, n_seq, 0, 0);
+    q = sk_fields<FUSED>(a, lane, n_seq);
+    const int kc = (q.np + kMinShare - 1) / kMinShare, kf = q.np > 0 ? max(1, q.np / kMinShare) : 0;
+    int ic = kc * a.n_kv, iflo = kf * a.n_kv;
+    q.incl = q.cnt;
+    wave_incl_scan3(q.incl, ic, iflo);  // units and both workgroup counts in one pass
     total = __builtin_amdgcn_readlane(q.incl, kWave - 1);
+    const bool ceil_fits = __builtin_amdgcn_readlane(ic, kWave - 1) <= n_cu;
+    kseg = ceil_fits ? kc : kf;
+    kincl = ceil_fits ? ic : iflo;
+    aligned = __builtin_amdgcn_readlane(kincl, kWave - 1) <= n_wg;
   } else {
     gb = sk_group_bases<FUSED>(a, n_seq, &total);
     q = sk_group<FUSED>(a, n_seq, 0, 0);
   }
   rope_inv_store<ROPE>((lds_u8*)rope_table_[wi], rinv);
   const int C = wg_chunk(total, n_wg, NW);
-  const int A = min(total, wg * C), B = min(total, A + C);
-  const int Cw = (B - A + NW - 1) / NW;
+  int A, B;
+  if (aligned) {
+    const int si = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(kincl <= wg));
+    A = B = total;
+    if (si < kWave) {
+      const int k = __builtin_amdgcn_readlane(kseg, si);
+      const int kb = __builtin_amdgcn_readlane(kincl, si) - k * a.n_kv;
+      const int np = __builtin_amdgcn_readlane(q.np, si);
+      const int h = (wg - kb) / k, j = (wg - kb) - h * k;
+      const int x0 = __builtin_amdgcn_readlane(q.incl, si) - __builtin_amdgcn_readlane(q.cnt, si) + h * np;
+      A = x0 + j * np / k;
+      B = x0 + (j + 1) * np / k;
+    }
+  } else {
+    A = min(total, wg * C);
+    B = min(total, A + C);
+  }
+  const int Cw = (B - A + NW - 1) / NW;  // wave i: [A + i Cw, A + (i + 1) Cw) within [A, B)
+  // the first and last workgroup of segment (s, kvh) = units [x0, x1)
+  auto seg_wgs = [&](int s, int kvh, int x0, int x1, int& ga, int& gz) {
+    if (aligned) {
+      const int sl = __builtin_amdgcn_readfirstlane(s);
+      const int k = __builtin_amdgcn_readlane(kseg, sl);
+      ga = __builtin_amdgcn_readlane(kincl, sl) - k * a.n_kv + kvh * k;
+      gz = ga + k - 1;
+    } else {
+      ga = x0 / C;
+      gz = (x1 - 1) / C;
+    }
+  };
   int cur = min(B, A + wi * Cw);
   const int end = min(B, cur + Cw);
   if (n_groups > 1 && cur < end) {
@@ -1674,7 +1741,8 @@ void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg) {
       // device-scope stores and the merge reads them with device-scope loads,
       // so no cache-wide write-back or invalidate is needed: the wait for the
       // stores to complete orders them before the count.
-      const int ga = x0 / C, gz = (x1 - 1) / C;
+      int ga, gz;
+      seg_wgs(s, kvh, x0, x1, ga, gz);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       uint32_t old = 0;
       if (lane == 0) old = __hip_atomic_fetch_add(a.wg_cnt + ga, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1713,7 +1781,9 @@ void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg) {
     const int e = last_[side];
     if (e < 0) continue;  // block-uniform
     const int s = split_[e][0], kvh = split_[e][1], x0 = split_[e][2], x1 = split_[e][3];
-    const int ga = x0 / C, nwg = (x1 - 1) / C - ga + 1;
+    int ga, gz;
+    seg_wgs(s, kvh, x0, x1, ga, gz);
+    const int nwg = gz - ga + 1;
     for (int hh = 0; hh < HW; ++hh) {
       const int h = NW >= REP ? wi % REP : wi + hh * NW;
       const int part = NW >= REP ? wi / REP : 0;
@@ -1961,20 +2031,20 @@ constexpr int kWgWavesQ8 = 4;
 constexpr int kWgPerCu = 2;
 
 template <int REP, bool FUSED, int NH>
-void launch_wg_rep(const DecodeArgs& a, int n_seq, int n_wg, bool q8, hipStream_t st) {
+void launch_wg_rep(const DecodeArgs& a, int n_seq, int n_wg, int n_cu, bool q8, hipStream_t st) {
   const bool rope = FUSED && a.rope_half > 0;
   if (q8 && rope)
     decode_wg_kernel<REP, FUSED, kSkDepthQ8, FUSED, true, kWgWavesQ8, NH>
-        <<<n_wg, kWave * kWgWavesQ8, 0, st>>>(a, n_seq, n_wg);
+        <<<n_wg, kWave * kWgWavesQ8, 0, st>>>(a, n_seq, n_wg, n_cu);
   else if (q8)
     decode_wg_kernel<REP, FUSED, kSkDepthQ8, false, true, kWgWavesQ8, NH>
-        <<<n_wg, kWave * kWgWavesQ8, 0, st>>>(a, n_seq, n_wg);
+        <<<n_wg, kWave * kWgWavesQ8, 0, st>>>(a, n_seq, n_wg, n_cu);
   else if (rope)
     decode_wg_kernel<REP, FUSED, kSkDepth, FUSED, false, kWgWaves, NH>
-        <<<n_wg, kWave * kWgWaves, 0, st>>>(a, n_seq, n_wg);
+        <<<n_wg, kWave * kWgWaves, 0, st>>>(a, n_seq, n_wg, n_cu);
   else
     decode_wg_kernel<REP, FUSED, kSkDepth, false, false, kWgWaves, NH>
-        <<<n_wg, kWave * kWgWaves, 0, st>>>(a, n_seq, n_wg);
+        <<<n_wg, kWave * kWgWaves, 0, st>>>(a, n_seq, n_wg, n_cu);
 }
 }  // namespace
 
@@ -2006,13 +2076,29 @@ int launch_decode_mfma_wg(const DecodeArgs& a, int rep, int d, int n_seq, int n_
   // Launch only the workgroups the batch can fill: with at most `bound`
   // units (from max_kv_len), groups of NW * kWgMinPages units each cover
   // them, so the kernel's chunk C = max(NW * kWgMinPages, ceil(T / G)) stays
-  // at its minimum and [0, G * C) still holds every unit.
+  // at its minimum and [0, G * C) still holds every unit; one more per
+  // segment lets the segment-aligned ranges (ceil(np / C) or fewer
+  // workgroups per segment, at most T / C + n_seq n_kv in all) fit the grid.
   const int nw = q8 ? kWgWavesQ8 : kWgWaves;
   const int64_t bound = (int64_t)n_seq * a.n_kv * ((int64_t)a.max_kv_len / kPage + 1);
   const int64_t per = (int64_t)nw * kWgMinPages;
-  const int groups = (int)std::max<int64_t>(1, std::min<int64_t>(n_wg, (bound + per - 1) / per));
+  const int n_cu = n_wg / kWgPerCu;
+  int64_t want = (bound + per - 1) / per + (int64_t)n_seq * a.n_kv;
+  if (!a.kv_len && !a.p_start) {
+    // every sequence has the scalar window (the reference's one-sequence
+    // call): exactly the kernel's segment-aligned count, np as in sk_fields
+    int L = a.kv_len_scalar;
+    L = L > std::min(a.max_kv_len, a.bt_stride * kPage) ? 0 : std::max(L, 0);
+    const int p0 = std::min(std::max(a.p_start_scalar, 0), L);
+    const int lo = FUSED && L > 0 ? std::min(p0, L - 1) : p0;
+    const int64_t np = L > lo ? (L - 1) / kPage - lo / kPage + 1 : 0;
+    const int64_t segs = (int64_t)n_seq * a.n_kv;
+    want = segs * ((np + per - 1) / per);
+    if (want > n_cu) want = segs * (np > 0 ? std::max<int64_t>(1, np / per) : 0);
+  }
+  const int groups = (int)std::max<int64_t>(1, std::min<int64_t>(n_wg, want));
   if (int rc = with_rep_nh(rep, d, [&](auto rep_c, auto nh_c) {
-        launch_wg_rep<decltype(rep_c)::value, FUSED, decltype(nh_c)::value>(a, n_seq, groups, q8, st);
+        launch_wg_rep<decltype(rep_c)::value, FUSED, decltype(nh_c)::value>(a, n_seq, groups, n_cu, q8, st);
       }))
     return rc;
   return hip_check("workgroup decode kernel launch");

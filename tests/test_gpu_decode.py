@@ -252,6 +252,74 @@ def test_reference_single_sequence_call_q8a_d128(gpu):
         assert rel_err(out, ref).max() < TOL[DTYPE_Q8A]
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_Q8A, DTYPE_F16])
+def test_reference_call_page_counts(gpu, dtype):
+    """lnskv_attention_paged at contexts around 4096 tokens (the workgroup
+    schedule): page counts per kv head that are and are not a multiple of
+    the workgroups' share (253 to 258 pages, and a short context), so that
+    segments start inside a workgroup's nominal range; windows 0 and 1000.
+    Pages bit-exact, output against the f64 oracle."""
+    n_kv, d, hq = 8, 128, 32
+    pk = PagedKV(272, n_kv, d, dtype, gpu)
+    fill_pages(pk, seed=4)
+    rng = np.random.default_rng(11)
+    bt = np.full(512, NO_PAGE, np.uint32)
+    bt[:272] = rng.permutation(272).astype(np.uint32)
+    for pos, p_start in ((4031, 0), (4063, 0), (4064, 0), (4095, 0), (4096, 0), (4111, 1000), (4127, 0),
+                         (130, 0)):
+        say("attention_paged page counts", DTYPE_NAMES[dtype], "pos", pos, "p_start", p_start)
+        q = rng.standard_normal((hq, d)).astype(np.float32)
+        k_in = rng.standard_normal(n_kv * d).astype(np.float32)
+        v_in = rng.standard_normal(n_kv * d).astype(np.float32)
+        hp, _ = host_pages(pk)
+        O.append(hp, k_in[None], v_in[None], np.zeros(1, np.int32), np.array([pos], np.int32), bt[None])
+        ref = O.decode_f64(hp, q[None], bt[None], np.array([pos + 1], np.int32), np.array([p_start], np.int32),
+                           1.0 / np.sqrt(d))[0]
+        out = pk.attention_paged(dev_f32(q, gpu), dev_f32(k_in, gpu), dev_f32(v_in, gpu), dev_i32(bt, gpu),
+                                 pos=pos, n_heads=hq, p_start=p_start, dispatch=True)
+        got, _ = host_pages(pk)
+        assert np.array_equal(got.k.view(np.uint8), hp.k.view(np.uint8))
+        assert np.array_equal(got.v.view(np.uint8), hp.v.view(np.uint8))
+        if dtype == DTYPE_Q8A:
+            assert np.array_equal(got.ks, hp.ks) and np.array_equal(got.vs, hp.vs)
+        assert rel_err(out, ref).max() < TOL[dtype], (pos, p_start)
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_Q8A, DTYPE_F16])
+def test_workgroup_schedule_small_batches(gpu, monkeypatch, dtype):
+    """The workgroup schedule on batches of 2 to 9 sequences whose segments
+    get workgroups of their own (ragged lengths, an empty sequence, one of a
+    single token, windows), unfused and fused, against the f64 oracle."""
+    monkeypatch.setenv("LNSKV_DECODE_SCHEDULE", "workgroup")
+    monkeypatch.delenv("LNSKV_FORCE_VALU", raising=False)
+    n_kv, d, rep = 8, 128, 4
+    for lens in ((4097, 17), (0, 1, 2049, 333, 4000), (1500,) * 3 + (1501, 1499, 16, 32, 48, 4111)):
+        say("workgroup schedule small batch", DTYPE_NAMES[dtype], lens)
+        pk, tables, kv_len, q = _case(gpu, dtype, d, rep, n_kv, lens, seed=len(lens))
+        p_start = np.zeros(len(lens), np.int32)
+        p_start[-1] = min(int(kv_len[-1]), 700)
+        hp, _ = host_pages(pk)
+        scale = 1.0 / np.sqrt(d)
+        ref = O.decode_f64(hp, q, tables, kv_len, p_start, scale)
+        out = pk.decode(dev_f32(q, gpu), dev_i32(tables, gpu), dev_i32(kv_len, gpu), n_heads=n_kv * rep,
+                        max_kv_len=int(kv_len.max()), scale=float(scale), p_start=dev_i32(p_start, gpu), split=0)
+        sync()
+        assert rel_err(out, ref).max() < TOL[dtype]
+        kv1 = np.minimum(kv_len + 1, tables.shape[1] * 16).astype(np.int32)
+        rng = np.random.default_rng(len(lens))
+        k_new = rng.standard_normal((len(lens), n_kv, d)).astype(np.float32)
+        v_new = rng.standard_normal((len(lens), n_kv, d)).astype(np.float32)
+        O.append(hp, k_new, v_new, np.arange(len(lens), dtype=np.int32), kv1 - 1, tables)
+        ref1 = O.decode_f64(hp, q, tables, kv1, p_start, scale)
+        out1 = pk.append_decode(dev_f32(q, gpu), dev_f32(k_new, gpu), dev_f32(v_new, gpu), dev_i32(tables, gpu),
+                                dev_i32(kv1, gpu), n_heads=n_kv * rep, max_kv_len=int(kv1.max()),
+                                scale=float(scale), p_start=dev_i32(p_start, gpu), split=0)
+        sync()
+        got, _ = host_pages(pk)
+        assert np.array_equal(got.k, hp.k) and np.array_equal(got.v, hp.v)
+        assert rel_err(out1, ref1).max() < TOL[dtype]
+
+
 def _sk_lens(n, seed):
     """Lengths for a stream-K batch: empty, sub-page, page-edge and long
     sequences, so that waves hold several pieces and segments span waves."""
