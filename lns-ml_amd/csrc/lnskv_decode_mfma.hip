@@ -1507,6 +1507,17 @@ __global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_
 // result does not depend on which one that is: the merge order is fixed.
 // ---------------------------------------------------------------------------
 constexpr int kWgMinPages = 2;  // fewest pages per wave
+// the last merge's rows in flight per wave: one round of loads for up to 32
+// workgroups per segment (registers: 32 x (2 + D / 64), 128 at D = 128 and
+// 192 at D = 256, whose one wave per SIMD has 512)
+constexpr int kWgMergeRows = 32;
+
+// Workgroups of a segment of np pages in the segment-aligned ranges (S the
+// fewest pages of a workgroup): ceil(np / S), or floor(np / S) when that
+// keeps the last merge to one round.
+__host__ __device__ constexpr int wg_seg_ceil(int np, int S) {
+  return (np + S - 1) / S > kWgMergeRows && np / S <= kWgMergeRows ? np / S : (np + S - 1) / S;
+}
 
 __device__ __forceinline__ int wg_chunk(int total, int n_wg, int nw) {
   return max(nw * kWgMinPages, (total + n_wg - 1) / n_wg);
@@ -1570,9 +1581,10 @@ void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg, int n_cu) {
   // pages evenly, so no workgroup or wave holds the end of one segment and
   // the start of the next (two pieces in a row on one wave, two merges on one
   // workgroup).  kseg = ceil(np / S) (S = NW kWgMinPages, the fewest units
-  // of a workgroup) while those workgroups have a CU each, else
-  // max(1, floor(np / S)): a wave with one more page costs less than two
-  // workgroups on one CU.  Otherwise workgroup g takes [g C, g C + C).
+  // of a workgroup; floor(np / S) where that keeps the last merge to one
+  // round) while those workgroups have a CU each, else max(1, floor(np / S)):
+  // a wave with one more page costs less than two workgroups on one CU or a
+  // second round of row loads.  Otherwise workgroup g takes [g C, g C + C).
   constexpr int kMinShare = NW * kWgMinPages;
   int total = 0, gb = 0, g = 0;
   int kseg = 0, kincl = 0;
@@ -1580,7 +1592,7 @@ void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg, int n_cu) {
   SkSeq q;
   if (n_groups == 1) {
     q = sk_fields<FUSED>(a, lane, n_seq);
-    const int kc = (q.np + kMinShare - 1) / kMinShare, kf = q.np > 0 ? max(1, q.np / kMinShare) : 0;
+    const int kc = wg_seg_ceil(q.np, kMinShare), kf = q.np > 0 ? max(1, q.np / kMinShare) : 0;
     int ic = kc * a.n_kv, iflo = kf * a.n_kv;
     q.incl = q.cnt;
     wave_incl_scan3(q.incl, ic, iflo);  // units and both workgroup counts in one pass
@@ -1771,10 +1783,7 @@ void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg, int n_cu) {
   // the HP parts of head h through LDS, in part order.
   constexpr int HP = NW >= REP ? NW / REP : 1;  // parts per head
   constexpr int HW = NW >= REP ? 1 : REP / NW;  // heads per wave
-  // rows in flight (registers: kChunk x (2 + CL), 128 at NH = 1 and 192 at
-  // NH = 2, whose one wave per SIMD has 512): one round for 32 workgroups at
-  // either head width
-  constexpr int kChunk = 32;
+  constexpr int kChunk = kWgMergeRows;
   lds_f32* prow = (lds_f32*)part_;  // free again: row v of wave v, acc then m, l
 #pragma unroll
   for (int side = 0; side < 2; ++side) {
@@ -2093,7 +2102,7 @@ int launch_decode_mfma_wg(const DecodeArgs& a, int rep, int d, int n_seq, int n_
     const int lo = FUSED && L > 0 ? std::min(p0, L - 1) : p0;
     const int64_t np = L > lo ? (L - 1) / kPage - lo / kPage + 1 : 0;
     const int64_t segs = (int64_t)n_seq * a.n_kv;
-    want = segs * ((np + per - 1) / per);
+    want = segs * wg_seg_ceil((int)np, (int)per);
     if (want > n_cu) want = segs * (np > 0 ? std::max<int64_t>(1, np / per) : 0);
   }
   const int groups = (int)std::max<int64_t>(1, std::min<int64_t>(n_wg, want));

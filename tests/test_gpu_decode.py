@@ -252,14 +252,17 @@ def test_reference_single_sequence_call_q8a_d128(gpu):
         assert rel_err(out, ref).max() < TOL[DTYPE_Q8A]
 
 
+@pytest.mark.parametrize("shape", [(32, 8, 128), (16, 4, 256)])
 @pytest.mark.parametrize("dtype", [DTYPE_Q8A, DTYPE_F16])
-def test_reference_call_page_counts(gpu, dtype):
+def test_reference_call_page_counts(gpu, dtype, shape):
     """lnskv_attention_paged at contexts around 4096 tokens (the workgroup
     schedule): page counts per kv head that are and are not a multiple of
     the workgroups' share (253 to 258 pages, and a short context), so that
-    segments start inside a workgroup's nominal range; windows 0 and 1000.
-    Pages bit-exact, output against the f64 oracle."""
-    n_kv, d, hq = 8, 128, 32
+    segments start inside a workgroup's nominal range and some take fewer
+    workgroups than ceil(pages / share); windows 0 and 1000; Llama-3-8B's
+    and Qwen3.5's head shapes.  Pages bit-exact, output against the f64
+    oracle."""
+    hq, n_kv, d = shape
     pk = PagedKV(272, n_kv, d, dtype, gpu)
     fill_pages(pk, seed=4)
     rng = np.random.default_rng(11)
