@@ -1466,14 +1466,19 @@ __global__ __launch_bounds__(kBlock) void combine_sk_kernel(DecodeArgs a, int n_
   if (d.w == 0) return;
   const int s = d.x, kvh = d.y, wa = d.z, nw = d.w >> 1, first_slot = d.w & 1;
   for (int h = wv; h < REP; h += kWavesPerBlock) {
+    const size_t row = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * D;
+    float gv[C];  // the gate, loaded before the partial rows
+#pragma unroll
+    for (int c = 0; c < C; ++c) gv[c] = a.gate ? a.gate[row + c * kWave + lane] : 1.0f;
     float M, Ls, A[C];
     merge_wave<D, 1, 8>(reinterpret_cast<const float2*>(a.ws_ml), a.ws_acc, 0, nw,
                         [=](int j) { return ((size_t)(wa + j) * 2 + (j == 0 ? first_slot : 0)) * REP + h; },
                         M, Ls, A);
-    const size_t row = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * D;
 #pragma unroll
-    for (int c = 0; c < C; ++c)
-      a.out[row + c * kWave + lane] = gated(a, row + c * kWave + lane, Ls > 0.0f ? A[c] / Ls : 0.0f);
+    for (int c = 0; c < C; ++c) {
+      const float v = Ls > 0.0f ? A[c] / Ls : 0.0f;
+      a.out[row + c * kWave + lane] = a.gate ? v * gv[c] : v;
+    }
   }
 }
 
@@ -1796,6 +1801,12 @@ void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg, int n_cu) {
     for (int hh = 0; hh < HW; ++hh) {
       const int h = NW >= REP ? wi % REP : wi + hh * NW;
       const int part = NW >= REP ? wi / REP : 0;
+      const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * D;
+      // the gate of the row this wave writes, loaded before the rows (its
+      // round trip overlaps theirs instead of following the merge)
+      float gv[CL];
+#pragma unroll
+      for (int c = 0; c < CL; ++c) gv[c] = HP == 1 && a.gate ? a.gate[orow + c * kWave + lane] : 1.0f;
       float M = kMInit, Ls = 0.0f, Av[CL];
 #pragma unroll
       for (int c = 0; c < CL; ++c) Av[c] = 0.0f;
@@ -1834,11 +1845,13 @@ void decode_wg_kernel(DecodeArgs a, int n_seq, int n_wg, int n_cu) {
         }
         M = Mc;
       }
-      const size_t orow = ((size_t)s * a.n_heads + (size_t)kvh * REP + h) * D;
       if constexpr (HP == 1) {
         const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
 #pragma unroll
-        for (int c = 0; c < CL; ++c) a.out[orow + c * kWave + lane] = gated(a, orow + c * kWave + lane, Av[c] * inv);
+        for (int c = 0; c < CL; ++c) {
+          const float v = Av[c] * inv;
+          a.out[orow + c * kWave + lane] = a.gate ? v * gv[c] : v;
+        }
       } else {
 #pragma unroll
         for (int c = 0; c < CL; ++c) prow[wi * kRow + c * kWave + lane] = Av[c];
